@@ -1,0 +1,198 @@
+/*
+ * w4a16.h -- C ABI of the MI355X (gfx950) W4A16 library: int4 weight-only GEMM for the
+ * GPTQ and AWQ packings, its act-order (g_idx) and fused-MoE variants, and a HIP runtime
+ * that stands in for the reference's DeviceRuntime trait.
+ *
+ * Replaces, for this path, what the reference compiles through Triton and launches with
+ * cudarc (sizzlecar/triton-rs):
+ *   crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:103-129  (GPTQ GEMM parameter list)
+ *   crates/triton-dsl/examples/awq_gemm_int4_typed.rs:94-115     (AWQ GEMM parameter list)
+ *   crates/triton-dsl/examples/ferrum_dequant_int4.rs:27-37      (GPTQ asym dequant)
+ *   crates/triton-dsl/examples/ferrum_dequant_int4_sym.rs:24-31  (GPTQ sym dequant)
+ *   crates/triton-runtime/src/lib.rs:18-85                       (RuntimeError, KernelArg,
+ *                                                                 DeviceRuntime)
+ *
+ * Conventions (all functions):
+ *  - Return int status: 0 (W4A16_OK) or a w4a16_status error. Nothing throws or aborts.
+ *    w4a16_last_error() returns the calling thread's message for its last failure.
+ *  - Arguments are validated on the host before any HIP call, so every argument error is
+ *    reported without touching the GPU.
+ *  - Pointers are device pointers (hipMalloc'd or HIP-visible); fp16 data is IEEE binary16.
+ *  - `stream` is a hipStream_t (NULL = the null stream). Work is enqueued asynchronously.
+ *  - Matrices are row-major. Sizes and strides are int32, as in the reference (its offsets
+ *    are i32, w4a16_gptq_gemm_typed.rs:119-128); offsets are computed in 64 bits here.
+ */
+#ifndef W4A16_H
+#define W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4A16_API __attribute__((visibility("default")))
+
+/* Status codes. ModuleLoad / InvalidLaunchConfig / Device / BackendDisabled mirror the
+ * reference's RuntimeError variants (crates/triton-runtime/src/lib.rs:18-35). */
+typedef enum {
+    W4A16_OK = 0,
+    W4A16_ERR_INVALID_ARG = 1,       /* null pointer, bad size, bad divisibility, bad handle */
+    W4A16_ERR_UNSUPPORTED = 2,       /* valid request outside what this build implements */
+    W4A16_ERR_DEVICE = 3,            /* RuntimeError::Device: a HIP call failed */
+    W4A16_ERR_MODULE_LOAD = 4,       /* RuntimeError::ModuleLoad */
+    W4A16_ERR_LAUNCH_CONFIG = 5,     /* RuntimeError::InvalidLaunchConfig */
+    W4A16_ERR_BACKEND_DISABLED = 6,  /* RuntimeError::BackendDisabled: no usable HIP device */
+    W4A16_ERR_NOT_FOUND = 7          /* kernel name not present in a loaded module */
+} w4a16_status;
+
+/* Weight packings.
+ *  GPTQ     qweight int32 [K/8, N], row k in nibble slot k%8 (w4a16_gptq_gemm_typed.rs:15-32);
+ *           qzeros int32 [K/G, N/8], column n in slot n%8, zero = nibble + zero_offset
+ *           (the reference GEMM uses +1, :224-236; its asym dequant uses 0).
+ *  GPTQ_SYM as GPTQ with zero = 8 and no qzeros (ferrum_dequant_int4_sym.rs:60).
+ *  AWQ      qweight int32 [K, N/8] and qzeros int32 [K/G, N/8]; column n in slot
+ *           (n%8)/2 + (n%8)%2*4, i.e. [0,4,1,5,2,6,3,7]; zero = nibble
+ *           (awq_gemm_int4_typed.rs:10-31, 139-151, 203-205).
+ * scales are fp16 [K/G, N] for all three. */
+typedef enum { W4A16_FMT_GPTQ = 0, W4A16_FMT_GPTQ_SYM = 1, W4A16_FMT_AWQ = 2 } w4a16_format;
+
+/* Kernel regimes reported by w4a16_gemm_plan(). */
+typedef enum {
+    W4A16_KERNEL_GEMV = 1,       /* decode: split-K GEMV, VALU dot2, no MFMA */
+    W4A16_KERNEL_SKINNY = 2,     /* small batch: MFMA, weights streamed once */
+    W4A16_KERNEL_PREFILL = 3,    /* large M: dequant-to-LDS + MFMA tiles */
+    W4A16_KERNEL_STRIDED = 4     /* generic strided kernel (any layout, any shape) */
+} w4a16_kernel;
+
+W4A16_API const char* w4a16_last_error(void);
+W4A16_API const char* w4a16_version(void);
+
+/* ------------------------------------------------------------------ op level */
+
+/* out[M, N] = x[M, K] @ W16[K, N], W16 = RNE_f16((q - z) * scale[g, n]) with
+ * g = g_idx ? g_idx[k] : k / group_size; fp32 accumulation; fp16 output.
+ * Contiguous row-major tensors. qzeros is ignored (may be NULL) for GPTQ_SYM. g_idx
+ * (int32 [K], values in [0, K/group_size)) is optional and, in the reference, absent:
+ * it adds GPTQ act-order. Requirements: M, N, K, group_size >= 1; K % group_size == 0;
+ * N % 8 == 0; K % 8 == 0 for GPTQ formats. The kernel is chosen by shape (see
+ * w4a16_gemm_plan). The decode kernels use a per-(device, stream) split-K workspace
+ * that the library allocates on first use of a size and keeps; concurrent calls on
+ * different streams are safe. */
+W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
+                         const void* scales, const void* qzeros, const int32_t* g_idx,
+                         void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                         int32_t gptq_zero_offset);
+
+/* Which kernel w4a16_gemm would run for this problem (no GPU access). */
+W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                              int has_g_idx, int* kernel);
+
+/* ------------------------------------------------------------------ kernel level
+ * The reference kernels' exact parameter lists (a_ptr, qweight_ptr, scales_ptr, qzeros_ptr,
+ * c_ptr, m, n, k, group_size, 10 strides), prefixed by the stream. Any strides (in
+ * elements of the tensor's own type), any M/N/K; masked tails read as zero. */
+
+/* replaces w4a16_gptq_gemm_typed (w4a16_gptq_gemm_typed.rs:103-129), zero = nibble + 1 */
+W4A16_API int w4a16_gptq_gemm_typed(void* stream, const void* a_ptr, const void* qweight_ptr,
+                                    const void* scales_ptr, const void* qzeros_ptr,
+                                    void* c_ptr, int32_t m_size, int32_t n_size,
+                                    int32_t k_size, int32_t group_size, int32_t stride_am,
+                                    int32_t stride_ak, int32_t stride_qwk, int32_t stride_qwn,
+                                    int32_t stride_sk, int32_t stride_sn, int32_t stride_qzk,
+                                    int32_t stride_qzn, int32_t stride_cm, int32_t stride_cn);
+
+/* replaces awq_gemm_int4_typed (awq_gemm_int4_typed.rs:94-115) */
+W4A16_API int awq_gemm_int4_typed(void* stream, const void* a_ptr, const void* qweight_ptr,
+                                  const void* scales_ptr, const void* qzeros_ptr, void* c_ptr,
+                                  int32_t m_size, int32_t n_size, int32_t k_size,
+                                  int32_t group_size, int32_t stride_am, int32_t stride_ak,
+                                  int32_t stride_qwk, int32_t stride_qwn, int32_t stride_sk,
+                                  int32_t stride_sn, int32_t stride_qzk, int32_t stride_qzn,
+                                  int32_t stride_cm, int32_t stride_cn);
+
+/* replaces dequant_int4_to_fp16 (ferrum_dequant_int4.rs:27-37): GPTQ qweight [K/8, N],
+ * qzeros [K/G, N/8] with zero = nibble (no +1), output fp16 TRANSPOSED [N, K]
+ * (out[n*K + k]). n_div_8 must equal n_dim / 8. */
+W4A16_API int dequant_int4_to_fp16(void* stream, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, void* output, int32_t k_dim,
+                                   int32_t n_dim, int32_t group_size, int32_t n_div_8);
+
+/* replaces dequant_int4_sym_to_fp16 (ferrum_dequant_int4_sym.rs:24-31): zero = 8. */
+W4A16_API int dequant_int4_sym_to_fp16(void* stream, const int32_t* qweight, const void* scales,
+                                       void* output, int32_t k_dim, int32_t n_dim,
+                                       int32_t group_size);
+
+/* Dequantise any format to fp16, row-major [K, N] (transposed = 0) or [N, K] (= 1).
+ * g_idx optional. No reference counterpart beyond the two functions above. */
+W4A16_API int w4a16_dequant(void* stream, int fmt, const void* qweight, const void* scales,
+                            const void* qzeros, const int32_t* g_idx, void* out, int32_t K,
+                            int32_t N, int32_t group_size, int32_t gptq_zero_offset,
+                            int transposed);
+
+/* ------------------------------------------------------------------ runtime
+ * A HIP backend for the reference's DeviceRuntime trait (crates/triton-runtime/src/
+ * lib.rs:64-85): load a code object, launch a kernel by name with KernelArg-style
+ * arguments. Plus the allocation / copy / stream / event calls the reference's examples
+ * take from cudarc (crates/triton-runtime/examples/run_vec_add.rs:70-123). */
+
+typedef struct hiprt_ctx hiprt_ctx;
+typedef struct hiprt_module hiprt_module;
+
+/* KernelArg (crates/triton-runtime/src/lib.rs:46-60) as a tagged union. */
+typedef enum {
+    HIPRT_ARG_I32 = 0,
+    HIPRT_ARG_U32 = 1,
+    HIPRT_ARG_I64 = 2,
+    HIPRT_ARG_F32 = 3,
+    HIPRT_ARG_DEVICE_PTR = 4,
+    HIPRT_ARG_BYTES = 5
+} hiprt_arg_kind;
+
+typedef struct {
+    int32_t kind;           /* hiprt_arg_kind */
+    uint32_t size;          /* HIPRT_ARG_BYTES only: byte count */
+    union {
+        int32_t i32;
+        uint32_t u32;
+        int64_t i64;
+        float f32;
+        uint64_t device_ptr;
+        const void* bytes;  /* copied into the kernel parameter buffer, 8-byte aligned */
+    } v;
+} hiprt_arg;
+
+/* Bind a context to a device (fails with BACKEND_DISABLED when there is none). */
+W4A16_API int hiprt_create(int32_t device, hiprt_ctx** out);
+W4A16_API int hiprt_destroy(hiprt_ctx* ctx);
+
+/* DeviceRuntime::load_module: `binary` is a gfx950 code object (.hsaco); it is borrowed. */
+W4A16_API int hiprt_module_load(hiprt_ctx* ctx, const void* binary, size_t size,
+                                hiprt_module** out);
+W4A16_API int hiprt_module_unload(hiprt_module* module);
+
+/* DeviceRuntime::launch. Arguments are packed at their natural alignment. */
+W4A16_API int hiprt_launch(hiprt_ctx* ctx, const hiprt_module* module, const char* kernel_name,
+                           const uint32_t grid[3], const uint32_t block[3],
+                           uint32_t shared_mem_bytes, void* stream, const hiprt_arg* args,
+                           size_t nargs);
+
+W4A16_API int hiprt_stream_create(hiprt_ctx* ctx, void** stream);
+W4A16_API int hiprt_stream_destroy(void* stream);
+W4A16_API int hiprt_stream_synchronize(void* stream);
+W4A16_API int hiprt_malloc(hiprt_ctx* ctx, size_t bytes, uint64_t* device_ptr);
+W4A16_API int hiprt_free(hiprt_ctx* ctx, uint64_t device_ptr);
+W4A16_API int hiprt_memcpy_htod_async(uint64_t dst, const void* src, size_t bytes, void* stream);
+W4A16_API int hiprt_memcpy_dtoh_async(void* dst, uint64_t src, size_t bytes, void* stream);
+W4A16_API int hiprt_memset_async(uint64_t dst, int value, size_t bytes, void* stream);
+W4A16_API int hiprt_event_create(void** event);
+W4A16_API int hiprt_event_destroy(void* event);
+W4A16_API int hiprt_event_record(void* event, void* stream);
+W4A16_API int hiprt_event_synchronize(void* event);
+W4A16_API int hiprt_event_elapsed_ms(void* start, void* stop, float* ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* W4A16_H */

@@ -1,0 +1,162 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol include/w4a16.h
+declares, and rejects bad arguments before touching the GPU (no compute calls here)."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+
+import pytest
+
+from helpers import ROOT, pkg
+
+HEADER = os.path.join(ROOT, "include", "w4a16.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return re.findall(r"W4A16_API\s+[\w\s\*]+?\b(\w+)\s*\(", text)
+
+
+def test_library_exports_every_declared_symbol():
+    P = pkg()
+    L = P.lib()
+    names = declared_functions()
+    assert len(names) >= 25
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in include/w4a16.h but not exported"
+    assert set(names) == set(P.EXPORTED)
+    out = subprocess.run(["nm", "-D", "--defined-only", P.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert set(names) <= exported
+
+
+def test_version_and_empty_error():
+    P = pkg()
+    assert "gfx950" in P.version()
+
+
+def _gemm(P, **over):
+    a = dict(stream=None, fmt=P.FMT_AWQ, x=1, qw=1, sc=1, qz=1, g=None, out=1, M=1, N=4096,
+             K=4096, G=128, zo=1)
+    a.update(over)
+    p = lambda v: None if v is None else ctypes.c_void_p(v)
+    return P.lib().w4a16_gemm(a["stream"], a["fmt"], p(a["x"]), p(a["qw"]), p(a["sc"]), p(a["qz"]),
+                              p(a["g"]), p(a["out"]), a["M"], a["N"], a["K"], a["G"], a["zo"])
+
+
+@pytest.mark.parametrize("over,needle", [
+    (dict(x=None), "null pointer"),
+    (dict(qz=None), "qzeros is required"),
+    (dict(K=4000), "multiple of group_size"),
+    (dict(N=4100), "multiple of 8"),
+    (dict(M=0), "sizes must be positive"),
+    (dict(G=0), "sizes must be positive"),
+    (dict(fmt=7), "unknown weight format"),
+    (dict(fmt=0, K=4100, G=4100), "multiple of 8 for GPTQ"),
+])
+def test_gemm_argument_errors_before_any_hip_call(over, needle):
+    P = pkg()
+    rc = _gemm(P, **over)
+    assert rc == P.ERR_INVALID_ARG
+    assert needle in P.lib().w4a16_last_error().decode()
+
+
+def test_gptq_sym_does_not_need_qzeros():
+    P = pkg()
+    k = ctypes.c_int()
+    assert P.lib().w4a16_gemm_plan(P.FMT_GPTQ_SYM, 1, 4096, 4096, 128, 0, ctypes.byref(k)) == 0
+
+
+def test_plan_regimes():
+    P = pkg()
+    assert P.plan("awq", 1, 14336, 4096, 128) == "gemv"
+    assert P.plan("awq", 1, 4096, 14336, 128) == "gemv"
+    assert P.plan("gptq_sym", 1, 4096, 4096, 128) == "gemv"
+    assert P.plan("gptq", 1, 4096, 4096, 128, has_g_idx=True) != "gemv"
+
+
+def test_dequant_reference_arg_check():
+    P = pkg()
+    rc = P.lib().dequant_int4_to_fp16(None, ctypes.c_void_p(1), ctypes.c_void_p(1),
+                                      ctypes.c_void_p(1), ctypes.c_void_p(16), 4096, 4096, 128, 511)
+    assert rc == P.ERR_INVALID_ARG and "n_div_8" in P.lib().w4a16_last_error().decode()
+
+
+def test_runtime_null_and_launch_config_errors():
+    P = pkg()
+    L = P.lib()
+    assert L.hiprt_create(0, None) == P.ERR_INVALID_ARG
+    assert L.hiprt_module_load(None, None, 0, None) == P.ERR_INVALID_ARG
+    g = (ctypes.c_uint32 * 3)(1, 1, 1)
+    b = (ctypes.c_uint32 * 3)(2048, 1, 1)
+    # a fake non-null ctx/module is never dereferenced: the launch config is checked first
+    rc = L.hiprt_launch(ctypes.c_void_p(8), ctypes.c_void_p(8), b"k", g, b, 0, None, None, 0)
+    assert rc == P.ERR_LAUNCH_CONFIG
+    z = (ctypes.c_uint32 * 3)(0, 1, 1)
+    assert L.hiprt_launch(ctypes.c_void_p(8), ctypes.c_void_p(8), b"k", z, g, 0, None, None, 0) \
+        == P.ERR_LAUNCH_CONFIG
+    big = (ctypes.c_uint32 * 3)(64, 1, 1)
+    assert L.hiprt_launch(ctypes.c_void_p(8), ctypes.c_void_p(8), b"k", g, big, 200 * 1024, None,
+                          None, 0) == P.ERR_LAUNCH_CONFIG
+
+
+def test_runtime_backend_disabled_without_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    P = pkg()
+    with pytest.raises(P.BackendDisabled):
+        P.HipRuntime(0)
+
+
+def test_typed_code_object_names_and_metadata():
+    P = pkg()
+    data = P.typed_module_bytes()
+    assert data[:4] == b"\x7fELF"
+    out = subprocess.run(["readelf", "-sW", P.HSACO_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    for name in ("w4a16_gptq_gemm_typed", "awq_gemm_int4_typed"):
+        assert re.search(rf"\b{name}\b", out), name
+    meta = P.typed_module_meta()
+    names = {k["name"] for k in meta["kernels"]}
+    assert names == {"w4a16_gptq_gemm_typed", "awq_gemm_int4_typed"}
+    for k in meta["kernels"]:
+        assert k["num_warps"] * 32 == k["threads_per_block"] == 256
+        assert k["params"] == 21
+
+
+def _disassemble_tu(obj, tmp_path):
+    """gfx950 disassembly of one of our own build's translation units."""
+    fb, dev = tmp_path / "fb.bin", tmp_path / "dev.o"
+    subprocess.run(["objcopy", "-O", "binary", "--only-section=.hip_fatbin", obj, str(fb)],
+                   check=True)
+    subprocess.run(["/opt/rocm/llvm/bin/clang-offload-bundler", "--unbundle", "--type=o",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={fb}",
+                    f"--output={dev}"], check=True)
+    dis = subprocess.run(["/opt/rocm/llvm/bin/llvm-objdump", "-d", str(dev)],
+                         capture_output=True, text=True, check=True).stdout
+    funcs = {}
+    for chunk in re.split(r"\n(?=[0-9a-f]+ <)", dis):
+        m = re.match(r"[0-9a-f]+ <([^>]+)>", chunk)
+        if m:
+            funcs[m.group(1)] = chunk
+    return funcs
+
+
+def test_kernel_choice_evidence_in_isa(tmp_path):
+    """The decode GEMV uses v_dot2 and no MFMA; the strided GEMM uses fp16 MFMA."""
+    bdir = os.path.join(ROOT, "triton-rs_amd", "_build")
+    gemv_o, strided_o = os.path.join(bdir, "kernels_gemv.o"), os.path.join(bdir, "kernels_strided.o")
+    if not (os.path.exists(gemv_o) and os.path.exists(strided_o)):
+        pytest.skip("build objects not present (run build first)")
+    gemv = {k: v for k, v in _disassemble_tu(gemv_o, tmp_path).items() if "gemv_" in k}
+    strided = {k: v for k, v in _disassemble_tu(strided_o, tmp_path).items()
+               if "strided_gemm_kernel" in k}
+    assert len(gemv) >= 12 and len(strided) == 3
+    for name, body in gemv.items():
+        assert "v_mfma" not in body, name
+        assert "v_dot2" in body, name
+    for name, body in strided.items():
+        assert "v_mfma_f32_16x16x32_f16" in body, name

@@ -1,0 +1,203 @@
+"""GPU parity: the HIP W4A16 kernels, called through the C ABI, against the CPU oracle.
+
+Bar: dequantised weights bit-exact; GEMM outputs within max
+relative error 1e-2 (helpers.rel_err: |y - ref| / max(|ref|, rms(ref))) of the oracle's
+float64-accumulated dequant-then-matmul on identical seeded inputs.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import synth
+from helpers import assert_parity, pkg, to_dev
+from synth import Problem
+
+pytestmark = pytest.mark.gpu
+
+GPTQ, SYM, AWQ = 0, 1, 2
+FMT_NAME = {GPTQ: "gptq", SYM: "gptq_sym", AWQ: "awq"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def _run_gemm(torch, p: Problem, g_idx=None):
+    P = pkg()
+    y = P.gemm(to_dev(p.x), to_dev(p.qweight), to_dev(p.scales),
+               None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[p.fmt],
+               group_size=p.G, g_idx=None if g_idx is None else to_dev(g_idx),
+               zero_offset=p.zero_offset)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _oracle(orc, p: Problem, g_idx=None):
+    return orc.w4a16_gemm(p.fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
+                          g_idx=g_idx, zero_offset=p.zero_offset, want_f32=True)[1]
+
+
+# ------------------------------------------------------------------ decode GEMV
+
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+def test_gemv_small(torch_cuda, orc, fmt, M):
+    p = Problem(fmt, M=M, K=1024, N=512, G=128, seed=1000 + 10 * fmt + M)
+    assert pkg().plan(FMT_NAME[fmt], M, p.N, p.K, p.G) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"gemv fmt={fmt} M={M}")
+
+
+@pytest.mark.parametrize("fmt,G", [(AWQ, 32), (AWQ, 64), (GPTQ, 32), (GPTQ, 64), (GPTQ, 256)])
+def test_gemv_group_sizes(torch_cuda, orc, fmt, G):
+    p = Problem(fmt, M=1, K=2048, N=256, G=G, seed=1100 + G)
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"gemv fmt={fmt} G={G}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [
+    (SYM, 1, 4096, 4096),          # config 0: GPTQ symmetric GEMV
+    (AWQ, 1, 4096, 14336),         # config 1: gate/up
+    (AWQ, 1, 14336, 4096),         # config 1: down
+    (AWQ, 4, 4096, 14336),
+])
+def test_gemv_full_size(torch_cuda, orc, fmt, M, K, N):
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0x5EED0000 + (0 if fmt == SYM else 1))
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"full fmt={fmt} M={M} K={K} N={N}")
+
+
+def test_gemv_deterministic_and_reusable(torch_cuda, orc):
+    """Split-K fix-up sums in a fixed order and leaves the workspace ready for the next call."""
+    P = pkg()
+    p = Problem(AWQ, M=1, K=4096, N=2048, G=128, seed=7)
+    args = [to_dev(a) for a in (p.x, p.qweight, p.scales, p.qzeros)]
+    ys = [P.gemm(*args, fmt="awq").cpu().numpy() for _ in range(3)]
+    assert all(np.array_equal(ys[0].view(np.uint16), y.view(np.uint16)) for y in ys[1:])
+    # a different shape in between, then the first again
+    q = Problem(AWQ, M=2, K=1024, N=512, G=128, seed=8)
+    assert_parity(_run_gemm(torch_cuda, q), _oracle(orc, q))
+    y2 = P.gemm(*args, fmt="awq").cpu().numpy()
+    assert np.array_equal(ys[0].view(np.uint16), y2.view(np.uint16))
+    assert_parity(ys[0], _oracle(orc, p))
+
+
+# ------------------------------------------------------------------ strided / generic
+
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N", [(16, 512, 256), (64, 1024, 384), (37, 384, 200)])
+def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N):
+    if N % 8:
+        N = N // 8 * 8
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=1200 + M + fmt)
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"strided fmt={fmt} M={M}")
+
+
+def test_act_order_gidx(torch_cuda, orc):
+    p = Problem(GPTQ, M=16, K=1024, N=384, G=128, seed=1300, act_order=True)
+    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) in ("strided", "skinny")
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what="act-order")
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, AWQ])
+def test_reference_typed_entry_points_with_strides(torch_cuda, orc, fmt):
+    """w4a16_gptq_gemm_typed / awq_gemm_int4_typed with non-contiguous strides and tails."""
+    torch = torch_cuda
+    P = pkg()
+    M, K, N, G = 45, 320, 136, 64
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1400 + fmt)
+    dev = "cuda:0"
+    # A stored transposed ([K, M] buffer, read through stride_am=1, stride_ak=M)
+    a_t = torch.from_numpy(np.ascontiguousarray(p.x.T)).to(dev)
+    # qweight / scales / qzeros with padded leading dimensions
+    def padded(a, pad):
+        buf = np.zeros((a.shape[0], a.shape[1] + pad), dtype=a.dtype)
+        buf[:, : a.shape[1]] = a
+        return torch.from_numpy(buf).to(dev), buf.shape[1]
+    qw, ldq = padded(p.qweight.view(np.int32), 3)
+    sc, lds = padded(p.scales, 5)
+    qz, ldz = padded(p.qzeros.view(np.int32), 2)
+    c = torch.zeros((M, N + 7), dtype=torch.float16, device=dev)
+    fn = P.w4a16_gptq_gemm_typed if fmt == GPTQ else P.awq_gemm_int4_typed
+    fn(a_t, qw, sc, qz, c, M, N, K, G, 1, M, ldq, 1, lds, 1, ldz, 1, N + 7, 1)
+    torch.cuda.synchronize()
+    y = c[:, :N].cpu().numpy()
+    ref = _oracle(orc, p)
+    assert_parity(y, ref, what="typed strided")
+    assert np.all(c[:, N:].cpu().numpy() == 0)   # nothing written outside [M, N]
+
+
+def test_hip_runtime_module_launch(torch_cuda, orc):
+    """DeviceRuntime path: load w4a16_typed.hsaco, launch awq_gemm_int4_typed by name with
+    KernelArg values (the reference's 19 parameters + 2 scratch pointers)."""
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(AWQ, M=70, K=256, N=200 // 8 * 8, G=128, seed=1500)
+    M, K, N = p.M, p.K, p.N
+    rt = P.HipRuntime(0)
+    mod = rt.load_module(P.typed_module_bytes())
+    meta = {k["name"]: k for k in P.typed_module_meta()["kernels"]}["awq_gemm_int4_typed"]
+    a, qw, sc, qz = (to_dev(v) for v in (p.x, p.qweight, p.scales, p.qzeros))
+    c = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
+    scratch = torch.empty(1, dtype=torch.uint8, device="cuda:0")
+    A = P.KernelArg
+    args = [A.ptr(a), A.ptr(qw), A.ptr(sc), A.ptr(qz), A.ptr(c), A.i32(M), A.i32(N), A.i32(K),
+            A.i32(p.G), A.i32(K), A.i32(1), A.i32(N // 8), A.i32(1), A.i32(N), A.i32(1),
+            A.i32(N // 8), A.i32(1), A.i32(N), A.i32(1), A.ptr(scratch), A.ptr(scratch)]
+    grid = (-(-M // meta["block_m"]), -(-N // meta["block_n"]), 1)
+    rt.launch(mod, "awq_gemm_int4_typed", grid, (meta["threads_per_block"], 1, 1),
+              meta["shared_mem"], None, args)
+    torch.cuda.synchronize()
+    assert_parity(c.cpu().numpy(), _oracle(orc, p), what="hiprt launch")
+    with pytest.raises(P.NotFound):
+        rt.launch(mod, "no_such_kernel", grid, (256, 1, 1), 0, None, args)
+    with pytest.raises(P.ModuleLoad):
+        rt.load_module(b"not a code object at all")
+    rt.unload_module(mod)
+    rt.close()
+
+
+# ------------------------------------------------------------------ dequant (bit-exact)
+
+@pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dequant_bit_exact(torch_cuda, orc, fmt, transposed):
+    P = pkg()
+    p = Problem(fmt, M=1, K=512, N=320, G=64, seed=1600 + fmt)
+    out = P.dequant(to_dev(p.qweight), to_dev(p.scales),
+                    None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[fmt],
+                    group_size=p.G, transposed=transposed)
+    torch_cuda.cuda.synchronize()
+    ref = orc.dequant(fmt, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G, transposed=transposed)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_dequant_act_order_bit_exact(torch_cuda, orc):
+    P = pkg()
+    p = Problem(GPTQ, M=1, K=1024, N=128, G=128, seed=1700, act_order=True)
+    out = P.dequant(to_dev(p.qweight), to_dev(p.scales), to_dev(p.qzeros), fmt="gptq",
+                    group_size=p.G, g_idx=to_dev(p.g_idx))
+    ref = orc.dequant(GPTQ, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G, g_idx=p.g_idx)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_reference_dequant_entry_points(torch_cuda, orc):
+    """dequant_int4_to_fp16 (zero = nibble, no +1) and dequant_int4_sym_to_fp16, [N, K] output."""
+    torch = torch_cuda
+    P = pkg()
+    K, N, G = 256, 192, 128
+    p = Problem(GPTQ, M=1, K=K, N=N, G=G, seed=1800)
+    out = torch.empty((N, K), dtype=torch.float16, device="cuda:0")
+    P.dequant_int4_to_fp16(to_dev(p.qweight), to_dev(p.scales), to_dev(p.qzeros), out, K, N, G, N // 8)
+    ref = orc.dequant(GPTQ, p.qweight, p.scales, p.qzeros, K, N, G, zero_offset=0, transposed=True)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+    P.dequant_int4_sym_to_fp16(to_dev(p.qweight), to_dev(p.scales), out, K, N, G)
+    ref = orc.dequant(SYM, p.qweight, p.scales, None, K, N, G, transposed=True)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))

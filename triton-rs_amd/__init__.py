@@ -1,0 +1,353 @@
+"""Python host side of the MI355X W4A16 library (ctypes over libw4a16.so, include/w4a16.h).
+
+Mirrors the reference's launch interface for this path: the kernel-level functions keep
+the parameter lists of `w4a16_gptq_gemm_typed` and `awq_gemm_int4_typed`
+(crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:103-129,
+awq_gemm_int4_typed.rs:94-115) and of the two dequant kernels
+(ferrum_dequant_int4.rs:27-37, ferrum_dequant_int4_sym.rs:24-31); `HipRuntime` mirrors the
+DeviceRuntime trait (crates/triton-runtime/src/lib.rs:64-85) with RuntimeError-style
+exceptions. Tensors are torch tensors on the GPU (torch provides memory and streams);
+every computation runs in the HIP library, and loading fails loudly when it is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # loaded first so the process has one HIP runtime (same SONAME)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libw4a16.so")
+HSACO_PATH = os.path.join(HERE, "w4a16_typed.hsaco")
+META_PATH = os.path.join(HERE, "w4a16_typed.json")
+
+FMT_GPTQ, FMT_GPTQ_SYM, FMT_AWQ = 0, 1, 2
+FORMATS = {"gptq": FMT_GPTQ, "gptq_sym": FMT_GPTQ_SYM, "awq": FMT_AWQ}
+KERNELS = {1: "gemv", 2: "skinny", 3: "prefill", 4: "strided"}
+
+OK, ERR_INVALID_ARG, ERR_UNSUPPORTED, ERR_DEVICE, ERR_MODULE_LOAD, ERR_LAUNCH_CONFIG, \
+    ERR_BACKEND_DISABLED, ERR_NOT_FOUND = range(8)
+
+
+class RuntimeError_(RuntimeError):
+    """Base of the runtime errors (crates/triton-runtime/src/lib.rs:18-35)."""
+
+    code = -1
+
+
+class InvalidArgument(RuntimeError_, ValueError):
+    code = ERR_INVALID_ARG
+
+
+class Unsupported(RuntimeError_):
+    code = ERR_UNSUPPORTED
+
+
+class DeviceError(RuntimeError_):
+    code = ERR_DEVICE
+
+
+class ModuleLoad(RuntimeError_):
+    code = ERR_MODULE_LOAD
+
+
+class InvalidLaunchConfig(RuntimeError_):
+    code = ERR_LAUNCH_CONFIG
+
+
+class BackendDisabled(RuntimeError_):
+    code = ERR_BACKEND_DISABLED
+
+
+class NotFound(RuntimeError_):
+    code = ERR_NOT_FOUND
+
+
+_ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, ModuleLoad,
+                               InvalidLaunchConfig, BackendDisabled, NotFound)}
+
+EXPORTED = (
+    "w4a16_last_error", "w4a16_version", "w4a16_gemm", "w4a16_gemm_plan",
+    "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
+    "dequant_int4_sym_to_fp16", "w4a16_dequant",
+    "hiprt_create", "hiprt_destroy", "hiprt_module_load", "hiprt_module_unload", "hiprt_launch",
+    "hiprt_stream_create", "hiprt_stream_destroy", "hiprt_stream_synchronize", "hiprt_malloc",
+    "hiprt_free", "hiprt_memcpy_htod_async", "hiprt_memcpy_dtoh_async", "hiprt_memset_async",
+    "hiprt_event_create", "hiprt_event_destroy", "hiprt_event_record", "hiprt_event_synchronize",
+    "hiprt_event_elapsed_ms",
+)
+
+_lib = None
+_P, _I, _Z = ctypes.c_void_p, ctypes.c_int32, ctypes.c_size_t
+
+
+def lib() -> ctypes.CDLL:
+    """Load libw4a16.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run `python triton-rs_amd/build.py` "
+                              "(or __graft_entry__.build()) first")
+        L = ctypes.CDLL(LIB_PATH)
+        L.w4a16_last_error.restype = ctypes.c_char_p
+        L.w4a16_version.restype = ctypes.c_char_p
+        L.w4a16_gemm.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.w4a16_gemm_plan.argtypes = [_I, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]
+        L.w4a16_gptq_gemm_typed.argtypes = [_P] * 6 + [_I] * 14
+        L.awq_gemm_int4_typed.argtypes = [_P] * 6 + [_I] * 14
+        L.dequant_int4_to_fp16.argtypes = [_P] * 5 + [_I] * 4
+        L.dequant_int4_sym_to_fp16.argtypes = [_P] * 4 + [_I] * 3
+        L.w4a16_dequant.argtypes = [_P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.hiprt_create.argtypes = [_I, ctypes.POINTER(_P)]
+        L.hiprt_destroy.argtypes = [_P]
+        L.hiprt_module_load.argtypes = [_P, _P, _Z, ctypes.POINTER(_P)]
+        L.hiprt_module_unload.argtypes = [_P]
+        L.hiprt_launch.argtypes = [_P, _P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_uint32),
+                                   ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint32, _P, _P, _Z]
+        L.hiprt_stream_create.argtypes = [_P, ctypes.POINTER(_P)]
+        L.hiprt_stream_destroy.argtypes = [_P]
+        L.hiprt_stream_synchronize.argtypes = [_P]
+        L.hiprt_malloc.argtypes = [_P, _Z, ctypes.POINTER(ctypes.c_uint64)]
+        L.hiprt_free.argtypes = [_P, ctypes.c_uint64]
+        L.hiprt_memcpy_htod_async.argtypes = [ctypes.c_uint64, _P, _Z, _P]
+        L.hiprt_memcpy_dtoh_async.argtypes = [_P, ctypes.c_uint64, _Z, _P]
+        L.hiprt_memset_async.argtypes = [ctypes.c_uint64, ctypes.c_int, _Z, _P]
+        L.hiprt_event_create.argtypes = [ctypes.POINTER(_P)]
+        L.hiprt_event_destroy.argtypes = [_P]
+        L.hiprt_event_record.argtypes = [_P, _P]
+        L.hiprt_event_synchronize.argtypes = [_P]
+        L.hiprt_event_elapsed_ms.argtypes = [_P, _P, ctypes.POINTER(ctypes.c_float)]
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        msg = lib().w4a16_last_error().decode(errors="replace")
+        raise _ERRORS.get(rc, RuntimeError_)(msg)
+
+
+def version() -> str:
+    return lib().w4a16_version().decode()
+
+
+# ------------------------------------------------------------------ tensor plumbing
+
+def _stream(t: torch.Tensor | None = None):
+    dev = t.device if t is not None else torch.device("cuda")
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _fmt(fmt) -> int:
+    if isinstance(fmt, str):
+        return FORMATS[fmt]
+    return int(fmt)
+
+
+def _require(t: torch.Tensor, name: str, dtypes, device: torch.device | None = None):
+    if not isinstance(t, torch.Tensor):
+        raise InvalidArgument(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise InvalidArgument(f"{name} must be on the GPU")
+    if t.dtype not in dtypes:
+        raise InvalidArgument(f"{name} has dtype {t.dtype}, expected one of {dtypes}")
+    if device is not None and t.device != device:
+        raise InvalidArgument(f"{name} is on {t.device}, expected {device}")
+
+
+_INT32 = (torch.int32,)
+_HALF = (torch.float16,)
+
+
+# ------------------------------------------------------------------ op level
+
+def plan(fmt, M: int, N: int, K: int, group_size: int, has_g_idx: bool = False) -> str:
+    """Name of the kernel regime w4a16_gemm would choose (no GPU access)."""
+    k = ctypes.c_int(0)
+    check(lib().w4a16_gemm_plan(_fmt(fmt), M, N, K, group_size, int(has_g_idx), ctypes.byref(k)))
+    return KERNELS[k.value]
+
+
+def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
+         qzeros: torch.Tensor | None, fmt="awq", group_size: int = 128,
+         g_idx: torch.Tensor | None = None, out: torch.Tensor | None = None,
+         zero_offset: int = 1) -> torch.Tensor:
+    """out[M, N] = x[M, K] @ dequant(qweight) in fp16 with fp32 accumulation.
+
+    fmt: "gptq" (qweight int32 [K/8, N], qzeros [K/G, N/8], zero = nibble + zero_offset),
+    "gptq_sym" (zero = 8, qzeros unused) or "awq" (qweight [K, N/8], AWQ nibble order).
+    """
+    f = _fmt(fmt)
+    _require(x, "x", _HALF)
+    dev = x.device
+    _require(qweight, "qweight", _INT32, dev)
+    _require(scales, "scales", _HALF, dev)
+    if qzeros is not None:
+        _require(qzeros, "qzeros", _INT32, dev)
+    if g_idx is not None:
+        _require(g_idx, "g_idx", _INT32, dev)
+    if x.dim() != 2:
+        raise InvalidArgument("x must be 2-D [M, K]")
+    M, K = x.shape
+    N = qweight.shape[1] * 8 if f == FMT_AWQ else qweight.shape[1]
+    for t, n in ((x, "x"), (qweight, "qweight"), (scales, "scales"), (qzeros, "qzeros"),
+                 (g_idx, "g_idx")):
+        if t is not None and not t.is_contiguous():
+            raise InvalidArgument(f"{n} must be contiguous")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    else:
+        _require(out, "out", _HALF, dev)
+        if tuple(out.shape) != (M, N) or not out.is_contiguous():
+            raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
+    check(lib().w4a16_gemm(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
+                           _ptr(g_idx), _ptr(out), M, N, K, group_size, zero_offset))
+    return out
+
+
+def dequant(qweight, scales, qzeros, fmt="gptq", K: int | None = None, group_size: int = 128,
+            g_idx=None, zero_offset: int = 1, transposed: bool = False) -> torch.Tensor:
+    """W16 as fp16, [K, N] (or [N, K] when transposed)."""
+    f = _fmt(fmt)
+    _require(qweight, "qweight", _INT32)
+    if f == FMT_AWQ:
+        K, N = qweight.shape[0], qweight.shape[1] * 8
+    else:
+        K, N = qweight.shape[0] * 8, qweight.shape[1]
+    out = torch.empty((N, K) if transposed else (K, N), dtype=torch.float16, device=qweight.device)
+    check(lib().w4a16_dequant(_stream(qweight), f, _ptr(qweight), _ptr(scales), _ptr(qzeros),
+                              _ptr(g_idx), _ptr(out), K, N, group_size, zero_offset,
+                              int(transposed)))
+    return out
+
+
+# ------------------------------------------------------------------ kernel level (reference names)
+
+def w4a16_gptq_gemm_typed(a_ptr, qweight_ptr, scales_ptr, qzeros_ptr, c_ptr, m_size, n_size,
+                          k_size, group_size, stride_am, stride_ak, stride_qwk, stride_qwn,
+                          stride_sk, stride_sn, stride_qzk, stride_qzn, stride_cm, stride_cn,
+                          stream=None):
+    """Reference parameter list (w4a16_gptq_gemm_typed.rs:110-128); tensors or raw pointers."""
+    st = stream if stream is not None else _stream(a_ptr if isinstance(a_ptr, torch.Tensor) else None)
+    args = [_p(a_ptr), _p(qweight_ptr), _p(scales_ptr), _p(qzeros_ptr), _p(c_ptr)]
+    check(lib().w4a16_gptq_gemm_typed(st, *args, m_size, n_size, k_size, group_size, stride_am,
+                                      stride_ak, stride_qwk, stride_qwn, stride_sk, stride_sn,
+                                      stride_qzk, stride_qzn, stride_cm, stride_cn))
+
+
+def awq_gemm_int4_typed(a_ptr, qweight_ptr, scales_ptr, qzeros_ptr, c_ptr, m_size, n_size,
+                        k_size, group_size, stride_am, stride_ak, stride_qwk, stride_qwn,
+                        stride_sk, stride_sn, stride_qzk, stride_qzn, stride_cm, stride_cn,
+                        stream=None):
+    """Reference parameter list (awq_gemm_int4_typed.rs:96-114); tensors or raw pointers."""
+    st = stream if stream is not None else _stream(a_ptr if isinstance(a_ptr, torch.Tensor) else None)
+    args = [_p(a_ptr), _p(qweight_ptr), _p(scales_ptr), _p(qzeros_ptr), _p(c_ptr)]
+    check(lib().awq_gemm_int4_typed(st, *args, m_size, n_size, k_size, group_size, stride_am,
+                                    stride_ak, stride_qwk, stride_qwn, stride_sk, stride_sn,
+                                    stride_qzk, stride_qzn, stride_cm, stride_cn))
+
+
+def dequant_int4_to_fp16(qweight, scales, qzeros, output, k_dim, n_dim, group_size, n_div_8,
+                         stream=None):
+    """ferrum_dequant_int4.rs:27-37: output[n*K + k], zero = nibble (no +1)."""
+    st = stream if stream is not None else _stream(qweight if isinstance(qweight, torch.Tensor) else None)
+    check(lib().dequant_int4_to_fp16(st, _p(qweight), _p(scales), _p(qzeros), _p(output), k_dim,
+                                     n_dim, group_size, n_div_8))
+
+
+def dequant_int4_sym_to_fp16(qweight, scales, output, k_dim, n_dim, group_size, stream=None):
+    """ferrum_dequant_int4_sym.rs:24-31: output[n*K + k], zero = 8."""
+    st = stream if stream is not None else _stream(qweight if isinstance(qweight, torch.Tensor) else None)
+    check(lib().dequant_int4_sym_to_fp16(st, _p(qweight), _p(scales), _p(output), k_dim, n_dim,
+                                         group_size))
+
+
+def _p(t):
+    if t is None:
+        return None
+    if isinstance(t, torch.Tensor):
+        return ctypes.c_void_p(t.data_ptr())
+    return ctypes.c_void_p(int(t))
+
+
+# ------------------------------------------------------------------ DeviceRuntime mirror
+
+class KernelArg(ctypes.Structure):
+    """hiprt_arg: the tagged union for KernelArg{I32,U32,I64,F32,DevicePtr,Bytes}."""
+
+    class _V(ctypes.Union):
+        _fields_ = [("i32", ctypes.c_int32), ("u32", ctypes.c_uint32), ("i64", ctypes.c_int64),
+                    ("f32", ctypes.c_float), ("device_ptr", ctypes.c_uint64),
+                    ("bytes", ctypes.c_void_p)]
+
+    _fields_ = [("kind", ctypes.c_int32), ("size", ctypes.c_uint32), ("v", _V)]
+
+    I32, U32, I64, F32, DEVICE_PTR, BYTES = range(6)
+
+    @classmethod
+    def i32(cls, v):
+        a = cls(); a.kind = cls.I32; a.v.i32 = v; return a
+
+    @classmethod
+    def u32(cls, v):
+        a = cls(); a.kind = cls.U32; a.v.u32 = v; return a
+
+    @classmethod
+    def i64(cls, v):
+        a = cls(); a.kind = cls.I64; a.v.i64 = v; return a
+
+    @classmethod
+    def f32(cls, v):
+        a = cls(); a.kind = cls.F32; a.v.f32 = v; return a
+
+    @classmethod
+    def ptr(cls, v):
+        a = cls(); a.kind = cls.DEVICE_PTR
+        a.v.device_ptr = v.data_ptr() if isinstance(v, torch.Tensor) else int(v)
+        return a
+
+
+class HipRuntime:
+    """DeviceRuntime (crates/triton-runtime/src/lib.rs:64-85) over hiprt_*."""
+
+    def __init__(self, device: int = 0):
+        self._ctx = ctypes.c_void_p()
+        check(lib().hiprt_create(device, ctypes.byref(self._ctx)))
+
+    def close(self):
+        if self._ctx:
+            check(lib().hiprt_destroy(self._ctx))
+            self._ctx = ctypes.c_void_p()
+
+    def load_module(self, binary: bytes) -> ctypes.c_void_p:
+        buf = ctypes.create_string_buffer(binary, len(binary))
+        mod = ctypes.c_void_p()
+        check(lib().hiprt_module_load(self._ctx, buf, len(binary), ctypes.byref(mod)))
+        return mod
+
+    def unload_module(self, module) -> None:
+        check(lib().hiprt_module_unload(module))
+
+    def launch(self, module, kernel_name: str, grid, block, shared_mem_bytes: int, stream,
+               args) -> None:
+        g = (ctypes.c_uint32 * 3)(*grid)
+        b = (ctypes.c_uint32 * 3)(*block)
+        arr = (KernelArg * max(1, len(args)))(*args)
+        st = stream if stream is not None else _stream()
+        check(lib().hiprt_launch(self._ctx, module, kernel_name.encode(), g, b, shared_mem_bytes,
+                                 st, arr, len(args)))
+
+
+def typed_module_bytes() -> bytes:
+    with open(HSACO_PATH, "rb") as f:
+        return f.read()
+
+
+def typed_module_meta() -> dict:
+    import json
+    with open(META_PATH) as f:
+        return json.load(f)

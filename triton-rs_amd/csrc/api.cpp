@@ -1,0 +1,271 @@
+// C-ABI op layer: argument validation (before any HIP call), kernel selection, split-K
+// workspace management and error reporting for include/w4a16.h.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "../../include/w4a16.h"
+#include "launch.h"
+
+namespace w4a16 {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(W4A16_ERR_DEVICE, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+static inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// ------------------------------------------------------------------ workspace
+
+// One split-K workspace per (device, stream): counters (zeroed at allocation, reset to
+// zero by the kernels themselves) followed by fp32 partials.
+struct Workspace {
+    void* base = nullptr;
+    size_t bytes = 0;
+};
+static std::mutex g_ws_mu;
+static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+constexpr size_t COUNTER_BYTES = 64 * 1024;  // room for 16384 column tiles
+
+static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = g_ws[{dev, st}];
+    const size_t total = COUNTER_BYTES + need;
+    if (w.bytes < total) {
+        if (w.base) {
+            // the old buffer may still be read by queued work on this stream
+            e = hipStreamSynchronize(st);
+            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+            (void)hipFree(w.base);
+            w.base = nullptr;
+            w.bytes = 0;
+        }
+        size_t grow = total < (size_t)(8 << 20) ? (size_t)(8 << 20) : total;
+        e = hipMalloc(&w.base, grow);
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
+        e = hipMemset(w.base, 0, COUNTER_BYTES);
+        if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace counters)");
+        w.bytes = grow;
+    }
+    *counters = static_cast<uint32_t*>(w.base);
+    *partials = reinterpret_cast<float*>(static_cast<char*>(w.base) + COUNTER_BYTES);
+    return W4A16_OK;
+}
+
+// ------------------------------------------------------------------ validation
+
+static int check_gemm_args(int fmt, const void* x, const void* qweight, const void* scales,
+                           const void* qzeros, const void* out, int32_t M, int32_t N,
+                           int32_t K, int32_t G) {
+    if (fmt != W4A16_FMT_GPTQ && fmt != W4A16_FMT_GPTQ_SYM && fmt != W4A16_FMT_AWQ)
+        return fail(W4A16_ERR_INVALID_ARG, "unknown weight format %d", fmt);
+    if (!x || !qweight || !scales || !out)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument (x, qweight, scales or out)");
+    if (fmt != W4A16_FMT_GPTQ_SYM && !qzeros)
+        return fail(W4A16_ERR_INVALID_ARG, "qzeros is required for GPTQ and AWQ formats");
+    if (M < 1 || N < 1 || K < 1 || G < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "sizes must be positive (M=%d N=%d K=%d group_size=%d)",
+                    M, N, K, G);
+    if (K % G)
+        return fail(W4A16_ERR_INVALID_ARG, "K (%d) must be a multiple of group_size (%d)", K, G);
+    if (N % 8)
+        return fail(W4A16_ERR_INVALID_ARG, "N (%d) must be a multiple of 8 (packed qzeros / AWQ)", N);
+    if (fmt != W4A16_FMT_AWQ && K % 8)
+        return fail(W4A16_ERR_INVALID_ARG, "K (%d) must be a multiple of 8 for GPTQ packing", K);
+    return W4A16_OK;
+}
+
+static int plan(int fmt, int M, int N, int K, int G, bool has_gidx) {
+    if (!has_gidx && gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
+    return W4A16_KERNEL_STRIDED;
+}
+
+}  // namespace w4a16
+
+using namespace w4a16;
+
+extern "C" {
+
+W4A16_API const char* w4a16_last_error(void) { return g_last_error.c_str(); }
+
+W4A16_API const char* w4a16_version(void) { return "w4a16-mi355x 0.1 (gfx950)"; }
+
+W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t G, int has_g_idx,
+                              int* kernel) {
+    int rc = check_gemm_args(fmt, (void*)1, (void*)1, (void*)1, (void*)1, (void*)1, M, N, K, G);
+    if (rc) return rc;
+    if (!kernel) return fail(W4A16_ERR_INVALID_ARG, "kernel out-pointer is null");
+    *kernel = plan(fmt, M, N, K, G, has_g_idx != 0);
+    return W4A16_OK;
+}
+
+W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
+                         const void* scales, const void* qzeros, const int32_t* g_idx, void* out,
+                         int32_t M, int32_t N, int32_t K, int32_t G, int32_t zero_offset) {
+    int rc = check_gemm_args(fmt, x, qweight, scales, qzeros, out, M, N, K, G);
+    if (rc) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool vec_ok = aligned(x, 16) && aligned(qweight, 16) && aligned(scales, 16) &&
+                        aligned(out, 4) && (!qzeros || aligned(qzeros, 16));
+    int kernel = plan(fmt, M, N, K, G, g_idx != nullptr);
+    if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
+
+    if (kernel == W4A16_KERNEL_GEMV) {
+        const GemvShape s = gemv_shape(fmt, M, N, K, G);
+        GemvParams p{};
+        p.x = static_cast<const half_t*>(x);
+        p.qweight = static_cast<const uint32_t*>(qweight);
+        p.scales = static_cast<const half_t*>(scales);
+        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset; p.splits = s.splits;
+        if (s.splits > 1) {
+            if ((size_t)s.col_tiles * sizeof(uint32_t) > COUNTER_BYTES)
+                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K counter area");
+            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
+            if (rc) return rc;
+        }
+        hipError_t e = launch_gemv(fmt, p, s, st);
+        if (e != hipSuccess) return hip_fail(e, "gemv launch");
+        return W4A16_OK;
+    }
+
+    StridedParams p{};
+    p.a = static_cast<const half_t*>(x);
+    p.qweight = static_cast<const uint32_t*>(qweight);
+    p.scales = static_cast<const half_t*>(scales);
+    p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+    p.g_idx = g_idx;
+    p.c = static_cast<half_t*>(out);
+    p.m = M; p.n = N; p.k = K; p.group_size = G; p.zero_offset = zero_offset;
+    p.stride_am = K; p.stride_ak = 1;
+    if (fmt == W4A16_FMT_AWQ) { p.stride_qwk = N / 8; p.stride_qwn = 1; }
+    else { p.stride_qwk = N; p.stride_qwn = 1; }
+    p.stride_sk = N; p.stride_sn = 1;
+    p.stride_qzk = N / 8; p.stride_qzn = 1;
+    p.stride_cm = N; p.stride_cn = 1;
+    hipError_t e = launch_strided_gemm(fmt, p, st);
+    if (e != hipSuccess) return hip_fail(e, "strided gemm launch");
+    return W4A16_OK;
+}
+
+static int typed_common(int fmt, void* stream, const void* a, const void* qw, const void* sc,
+                        const void* qz, void* c, int32_t m, int32_t n, int32_t k, int32_t G,
+                        const int32_t* strides) {
+    if (!a || !qw || !sc || !qz || !c)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (m < 0 || n < 0 || k < 0 || G < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "negative size or group_size < 1");
+    if (m == 0 || n == 0) return W4A16_OK;
+    StridedParams p{};
+    p.a = static_cast<const half_t*>(a);
+    p.qweight = static_cast<const uint32_t*>(qw);
+    p.scales = static_cast<const half_t*>(sc);
+    p.qzeros = static_cast<const uint32_t*>(qz);
+    p.g_idx = nullptr;
+    p.c = static_cast<half_t*>(c);
+    p.m = m; p.n = n; p.k = k; p.group_size = G;
+    p.stride_am = strides[0]; p.stride_ak = strides[1];
+    p.stride_qwk = strides[2]; p.stride_qwn = strides[3];
+    p.stride_sk = strides[4]; p.stride_sn = strides[5];
+    p.stride_qzk = strides[6]; p.stride_qzn = strides[7];
+    p.stride_cm = strides[8]; p.stride_cn = strides[9];
+    p.zero_offset = (fmt == W4A16_FMT_GPTQ) ? 1 : 0;
+    hipError_t e = launch_strided_gemm(fmt, p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "typed gemm launch");
+    return W4A16_OK;
+}
+
+W4A16_API int w4a16_gptq_gemm_typed(void* stream, const void* a_ptr, const void* qweight_ptr,
+                                    const void* scales_ptr, const void* qzeros_ptr, void* c_ptr,
+                                    int32_t m_size, int32_t n_size, int32_t k_size,
+                                    int32_t group_size, int32_t stride_am, int32_t stride_ak,
+                                    int32_t stride_qwk, int32_t stride_qwn, int32_t stride_sk,
+                                    int32_t stride_sn, int32_t stride_qzk, int32_t stride_qzn,
+                                    int32_t stride_cm, int32_t stride_cn) {
+    const int32_t s[10] = {stride_am, stride_ak, stride_qwk, stride_qwn, stride_sk,
+                           stride_sn, stride_qzk, stride_qzn, stride_cm, stride_cn};
+    return typed_common(W4A16_FMT_GPTQ, stream, a_ptr, qweight_ptr, scales_ptr, qzeros_ptr, c_ptr,
+                        m_size, n_size, k_size, group_size, s);
+}
+
+W4A16_API int awq_gemm_int4_typed(void* stream, const void* a_ptr, const void* qweight_ptr,
+                                  const void* scales_ptr, const void* qzeros_ptr, void* c_ptr,
+                                  int32_t m_size, int32_t n_size, int32_t k_size,
+                                  int32_t group_size, int32_t stride_am, int32_t stride_ak,
+                                  int32_t stride_qwk, int32_t stride_qwn, int32_t stride_sk,
+                                  int32_t stride_sn, int32_t stride_qzk, int32_t stride_qzn,
+                                  int32_t stride_cm, int32_t stride_cn) {
+    const int32_t s[10] = {stride_am, stride_ak, stride_qwk, stride_qwn, stride_sk,
+                           stride_sn, stride_qzk, stride_qzn, stride_cm, stride_cn};
+    return typed_common(W4A16_FMT_AWQ, stream, a_ptr, qweight_ptr, scales_ptr, qzeros_ptr, c_ptr,
+                        m_size, n_size, k_size, group_size, s);
+}
+
+static int dequant_common(void* stream, int fmt, const void* qweight, const void* scales,
+                          const void* qzeros, const int32_t* g_idx, void* out, int32_t K,
+                          int32_t N, int32_t G, int32_t zero_offset, int transposed) {
+    int rc = check_gemm_args(fmt, (void*)1, qweight, scales, qzeros, out, 1, N, K, G);
+    if (rc) return rc;
+    if (fmt == W4A16_FMT_AWQ && !aligned(out, 16) && !transposed)
+        return fail(W4A16_ERR_INVALID_ARG, "out must be 16-byte aligned");
+    if (fmt != W4A16_FMT_AWQ && transposed && (!aligned(out, 16) || K % 8))
+        return fail(W4A16_ERR_INVALID_ARG, "out must be 16-byte aligned");
+    DequantParams p{};
+    p.qweight = static_cast<const uint32_t*>(qweight);
+    p.scales = static_cast<const half_t*>(scales);
+    p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+    p.g_idx = g_idx;
+    p.out = static_cast<half_t*>(out);
+    p.K = K; p.N = N; p.G = G; p.zero_offset = zero_offset; p.transposed = transposed;
+    hipError_t e = launch_dequant(fmt, p, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return W4A16_OK;
+}
+
+W4A16_API int dequant_int4_to_fp16(void* stream, const int32_t* qweight, const void* scales,
+                                   const int32_t* qzeros, void* output, int32_t k_dim,
+                                   int32_t n_dim, int32_t group_size, int32_t n_div_8) {
+    if (n_div_8 * 8 != n_dim)
+        return fail(W4A16_ERR_INVALID_ARG, "n_div_8 (%d) must equal n_dim / 8 (n_dim=%d)", n_div_8,
+                    n_dim);
+    return dequant_common(stream, W4A16_FMT_GPTQ, qweight, scales, qzeros, nullptr, output, k_dim,
+                          n_dim, group_size, 0, 1);
+}
+
+W4A16_API int dequant_int4_sym_to_fp16(void* stream, const int32_t* qweight, const void* scales,
+                                       void* output, int32_t k_dim, int32_t n_dim,
+                                       int32_t group_size) {
+    return dequant_common(stream, W4A16_FMT_GPTQ_SYM, qweight, scales, nullptr, nullptr, output,
+                          k_dim, n_dim, group_size, 0, 1);
+}
+
+W4A16_API int w4a16_dequant(void* stream, int fmt, const void* qweight, const void* scales,
+                            const void* qzeros, const int32_t* g_idx, void* out, int32_t K,
+                            int32_t N, int32_t G, int32_t zero_offset, int transposed) {
+    return dequant_common(stream, fmt, qweight, scales, qzeros, g_idx, out, K, N, G, zero_offset,
+                          transposed ? 1 : 0);
+}
+
+}  // extern "C"

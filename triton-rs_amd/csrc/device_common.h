@@ -1,0 +1,80 @@
+// Device-side helpers shared by the W4A16 kernels (gfx950, wave64).
+//
+// Numeric contract (crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:246-260,
+// awq_gemm_int4_typed.rs:213-228): a weight is W16 = RNE_f16(f32(q - z) * f32(s)).
+// Because |q - z| <= 16 and s has an 11-bit significand, (q - z) * s is exact in f32, so
+// one correctly rounded fp16 multiply of fp16(q - z) by s yields the same bits. The
+// kernels build fp16(q) with the exponent trick: the bit pattern 0x6400 | q is the fp16
+// number 1024 + q (ulp 1 in [1024, 2048)), and 0x6400 | (q << 4) is 1024 + 16 q.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+constexpr int FMT_GPTQ = 0;
+constexpr int FMT_GPTQ_SYM = 1;
+constexpr int FMT_AWQ = 2;
+
+constexpr uint32_t MAGIC2 = 0x64006400u;  // (1024, 1024) as two fp16
+
+__device__ __forceinline__ half2_t as_h2(uint32_t u) { return __builtin_bit_cast(half2_t, u); }
+__device__ __forceinline__ uint32_t as_u32(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+
+// v_perm_b32: result byte i = byte sel_i of the 8-byte value {hi:lo}; selectors 0..3 pick
+// `lo`, 4..7 pick `hi`.
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// fp32 += a.x*b.x + a.y*b.y  (v_dot2c_f32_f16: f16 x f16 products, f32 accumulate)
+__device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// Nibble slot that column n occupies in an AWQ word: (n%8)/2 + (n%8)%2*4
+// (awq_gemm_int4_typed.rs:139-151). Slot s is read from bits [4s, 4s+4).
+__host__ __device__ constexpr int awq_slot(int n) { return ((n & 7) >> 1) + ((n & 1) << 2); }
+
+// Column (within its 8-group) stored in AWQ slot s: the inverse of awq_slot.
+__host__ __device__ constexpr int awq_col_of_slot(int s) { return ((s & 3) << 1) + (s >> 2); }
+
+// Logical-shift nibble extract (arith.shrui + andi 0xF).
+__device__ __forceinline__ int nib(uint32_t w, int slot) { return (int)((w >> (4 * slot)) & 0xFu); }
+
+// Zero point for (group row `qz_row`, column n) under each format.
+//   GPTQ: straight slot n%8, + zero_offset (+1 in the reference GEMM, :231-236)
+//   GPTQ_SYM: 8 (ferrum_dequant_int4_sym.rs:60)
+//   AWQ: slot awq_slot(n), no offset (awq_gemm_int4_typed.rs:203-205)
+template <int FMT>
+__device__ __forceinline__ int zero_of(uint32_t qz_word, int n, int zero_offset) {
+    if constexpr (FMT == FMT_GPTQ_SYM) return 8;
+    else if constexpr (FMT == FMT_AWQ) return nib(qz_word, awq_slot(n));
+    else return nib(qz_word, n & 7) + zero_offset;
+}
+
+// Bit-exact dequant of one weight: RNE_f16((q - z) * s).
+__device__ __forceinline__ half_t dequant1(int q, int z, half_t s) {
+    return (half_t)(q - z) * s;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Streaming (non-temporal) loads for packed weights, which are read exactly once.
+__device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ u32x2 ld_stream2(const uint32_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+__device__ __forceinline__ u32x4 ld_stream4(const uint32_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+}  // namespace w4a16

@@ -1,0 +1,375 @@
+// Decode-regime W4A16 GEMV (M <= 4): HBM-bound, no MFMA.
+//
+// Computes out[m, n] = sum_k x[m, k] * W16[k, n] for the reference's two packings
+// (crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:15-32 GPTQ [K/8, N] packed along K;
+// awq_gemm_int4_typed.rs:10-31 AWQ [K, N/8] packed along N, slot order [0,4,1,5,2,6,3,7]),
+// split over K so that a launch has ~900 workgroups, with a deterministic in-kernel
+// split-K fix-up (the last workgroup of a column tile sums the fp32 partials in split order).
+//
+// Per lane the inner loop is: 128-bit (or 32-bit) coalesced loads of packed words, a
+// nibble unpack into fp16 with the 0x6400 exponent trick (1024 + q, or 1024 + 16 q for the
+// odd nibble of each byte, so no shift is needed for it), and v_dot2c_f32_f16 against
+// pairs of x. All rows a lane touches lie in one quantisation group, so the zero point and
+// the scale are applied once per lane and column to the fp32 sum:
+//     sum_k x_k (q_k - z) s = s * (A - 1024 X - z X),   A = sum_k x_k (1024 + q_k)
+// which equals the reference's dequant-then-dot up to fp32 rounding (the reference rounds
+// each dequantised weight to fp16 first; the difference is < 2^-11 relative per term).
+#include "device_common.h"
+#include "launch.h"
+
+namespace w4a16 {
+
+// ------------------------------------------------------------------ split-K fix-up
+
+// Called by every thread of the block after it has written its partials for this tile.
+// Returns true in the (single) block that must produce the final output for the tile.
+__device__ __forceinline__ bool splitk_arrive(uint32_t* counter, int splits, int* lds_flag) {
+    __threadfence();  // release this thread's partial stores at agent scope
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t prev = atomicAdd(counter, 1u);
+        *lds_flag = (prev == (uint32_t)(splits - 1));
+    }
+    __syncthreads();
+    const bool last = *lds_flag != 0;
+    if (last) __threadfence();  // acquire: the other blocks' partials are visible
+    return last;
+}
+
+__device__ __forceinline__ float ld_coherent(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Sum the partials of one column tile in split order and store fp16; reset the counter.
+template <int M>
+__device__ __forceinline__ void splitk_finish(const float* __restrict__ ws, half_t* __restrict__ out,
+                                              uint32_t* counter, int splits, int N, int n0,
+                                              int C) {
+    for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
+        const int m = i / C, c = i - m * C;
+        const size_t off = (size_t)m * N + n0 + c;
+        float s = 0.f;
+        for (int sp = 0; sp < splits; ++sp) s += ld_coherent(ws + (size_t)sp * M * N + off);
+        out[off] = (half_t)s;
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------ AWQ GEMV
+
+// Tile: 256 columns (32 words per row) x R rows. Lane mapping: LPR = 32 / CW lanes per row,
+// each owning CW words (8*CW columns); RPW = 64 / LPR row-lanes per wave; a lane walks RL
+// consecutive rows (all in one group: G % RL == 0).
+template <int M, int CW, int RL, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+gemv_awq_kernel(GemvParams p) {
+    constexpr int LPR = 32 / CW;
+    constexpr int RPW = 64 / LPR;
+    constexpr int RB = RPW * WAVES;
+    constexpr int R = RB * RL;
+    constexpr int C = 256;
+    static_assert(RL % 2 == 0 && RL % 8 == 0, "rows per lane must be a multiple of 8");
+
+    __shared__ float red[RB][M][C];
+    __shared__ int flag;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cl = lane % LPR;
+    const int rb = wave * RPW + lane / LPR;
+    const int ct = blockIdx.x;
+    const int split = blockIdx.y;
+    const int NW = p.N >> 3;                       // words per qweight row
+    const int wc0 = ct * 32 + cl * CW;             // first word column of this lane
+    const int k0 = split * R + rb * RL;            // first row of this lane
+    const int g = k0 / p.G;
+
+    // ---- issue all weight loads (RL rows x CW words) up front
+    uint32_t w[RL][CW];
+    const uint32_t* qp = p.qweight + (size_t)k0 * NW + wc0;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        if constexpr (CW == 4) {
+            const u32x4 v = ld_stream4(qp + (size_t)j * NW);
+            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
+        } else if constexpr (CW == 2) {
+            const u32x2 v = ld_stream2(qp + (size_t)j * NW);
+            w[j][0] = v.x; w[j][1] = v.y;
+        } else {
+            w[j][0] = ld_stream(qp + (size_t)j * NW);
+        }
+    }
+
+    // ---- x pairs (rows 2i, 2i+1 of this lane) for every m, and X = sum of x
+    half2_t xs[M][RL / 2];
+    float X[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        const uint4* xp = reinterpret_cast<const uint4*>(p.x + (size_t)m * p.K + k0);
+#pragma unroll
+        for (int i = 0; i < RL / 8; ++i) {
+            const uint4 v = xp[i];
+            xs[m][4 * i + 0] = as_h2(v.x); xs[m][4 * i + 1] = as_h2(v.y);
+            xs[m][4 * i + 2] = as_h2(v.z); xs[m][4 * i + 3] = as_h2(v.w);
+        }
+        float s = 0.f;
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int i = 0; i < RL / 2; ++i) s = dot2(xs[m][i], one2, s);
+        X[m] = s;
+    }
+
+    // ---- main loop: acc[m][cw][slot]
+    float acc[M][CW][8];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int c = 0; c < CW; ++c)
+#pragma unroll
+            for (int s = 0; s < 8; ++s) acc[m][c][s] = 0.f;
+
+#pragma unroll
+    for (int i = 0; i < RL / 2; ++i) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            const uint32_t a = w[2 * i][c], b = w[2 * i + 1][c];
+            // bytes {a0,a1,b0,b1}: slots 0-3 of row 2i in the low half, of row 2i+1 in the high
+            const uint32_t lo = perm(b, a, 0x05040100u);
+            const uint32_t hi = perm(b, a, 0x07060302u);
+            const uint32_t lo8 = lo >> 8, hi8 = hi >> 8;
+            half2_t h[8];
+            h[0] = as_h2((lo & 0x000F000Fu) | MAGIC2);   // slot 0: 1024 + q
+            h[1] = as_h2((lo & 0x00F000F0u) | MAGIC2);   // slot 1: 1024 + 16 q
+            h[2] = as_h2((lo8 & 0x000F000Fu) | MAGIC2);  // slot 2
+            h[3] = as_h2((lo8 & 0x00F000F0u) | MAGIC2);  // slot 3 (x16)
+            h[4] = as_h2((hi & 0x000F000Fu) | MAGIC2);   // slot 4
+            h[5] = as_h2((hi & 0x00F000F0u) | MAGIC2);   // slot 5 (x16)
+            h[6] = as_h2((hi8 & 0x000F000Fu) | MAGIC2);  // slot 6
+            h[7] = as_h2((hi8 & 0x00F000F0u) | MAGIC2);  // slot 7 (x16)
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+                for (int s = 0; s < 8; ++s) acc[m][c][s] = dot2(h[s], xs[m][i], acc[m][c][s]);
+        }
+    }
+
+    // ---- zero point and scale, once per lane and column; columns written in natural order
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+        const int wcol = wc0 + c;
+        uint32_t qz = 0;
+        if (p.qzeros) qz = p.qzeros[(size_t)g * NW + wcol];
+        const uint4 sv = *reinterpret_cast<const uint4*>(p.scales + (size_t)g * p.N + 8 * wcol);
+        const half_t* sh = reinterpret_cast<const half_t*>(&sv);
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            float col[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const int n = awq_col_of_slot(s);
+                const float z = (float)nib(qz, s);
+                const float inv_f = (s & 1) ? (1.0f / 16.0f) : 1.0f;
+                const float u = (acc[m][c][s] - 1024.0f * X[m]) * inv_f - z * X[m];
+                col[n] = (float)sh[n] * u;
+            }
+            float4* dst = reinterpret_cast<float4*>(&red[rb][m][(cl * CW + c) * 8]);
+            dst[0] = make_float4(col[0], col[1], col[2], col[3]);
+            dst[1] = make_float4(col[4], col[5], col[6], col[7]);
+        }
+    }
+    __syncthreads();
+
+    // ---- reduce over row blocks; write partial (or the output when there is one split)
+    const int n0 = ct * C;
+    for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
+        const int m = i / C, cidx = i - m * C;
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
+        const size_t off = (size_t)m * p.N + n0 + cidx;
+        if (p.splits == 1) p.out[off] = (half_t)s;
+        else p.ws[(size_t)split * M * p.N + off] = s;
+    }
+    if (p.splits == 1) return;
+    if (splitk_arrive(p.counters + ct, p.splits, &flag))
+        splitk_finish<M>(p.ws, p.out, p.counters + ct, p.splits, p.N, n0, C);
+}
+
+// ------------------------------------------------------------------ GPTQ GEMV
+
+// Tile: C = LPR * CW columns x R k-rows. A lane owns CW consecutive columns (one 128-bit
+// load per packed row for CW = 4) and RL consecutive packed rows (8*RL k, one group).
+template <int FMT, int M, int CW, int RL, int WAVES, int LPR>
+__global__ void __launch_bounds__(64 * WAVES)
+gemv_gptq_kernel(GemvParams p) {
+    constexpr int RPW = 64 / LPR;
+    constexpr int RB = RPW * WAVES;
+    constexpr int C = LPR * CW;
+    constexpr int RK = RB * RL * 8;  // k rows per block
+
+    __shared__ float red[RB][M][C];
+    __shared__ int flag;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int cl = lane % LPR;
+    const int rb = wave * RPW + lane / LPR;
+    const int ct = blockIdx.x;
+    const int split = blockIdx.y;
+    const int n0 = ct * C;
+    const int c0 = n0 + cl * CW;                       // first column of this lane
+    const int kp0 = (split * RK) / 8 + rb * RL;        // first packed row
+    const int k0 = kp0 * 8;
+    const int g = k0 / p.G;
+
+    uint32_t w[RL][CW];
+    const uint32_t* qp = p.qweight + (size_t)kp0 * p.N + c0;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        if constexpr (CW == 4) {
+            const u32x4 v = ld_stream4(qp + (size_t)j * p.N);
+            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
+        } else if constexpr (CW == 2) {
+            const u32x2 v = ld_stream2(qp + (size_t)j * p.N);
+            w[j][0] = v.x; w[j][1] = v.y;
+        } else {
+            w[j][0] = ld_stream(qp + (size_t)j * p.N);
+        }
+    }
+
+    // x for packed row j, rearranged to the unpack order: (x0,x4) (x1,x5) (x2,x6) (x3,x7)
+    half2_t xs[M][RL][4];
+    float X[M], B[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float x1 = 0.f, x16 = 0.f;
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int j = 0; j < RL; ++j) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p.x + (size_t)m * p.K + k0 + 8 * j);
+            xs[m][j][0] = as_h2(perm(v.z, v.x, 0x05040100u));
+            xs[m][j][1] = as_h2(perm(v.z, v.x, 0x07060302u));
+            xs[m][j][2] = as_h2(perm(v.w, v.y, 0x05040100u));
+            xs[m][j][3] = as_h2(perm(v.w, v.y, 0x07060302u));
+            x1 = dot2(xs[m][j][0], one2, x1);
+            x1 = dot2(xs[m][j][2], one2, x1);
+            x16 = dot2(xs[m][j][1], one2, x16);
+            x16 = dot2(xs[m][j][3], one2, x16);
+        }
+        X[m] = x1 + x16;
+        B[m] = 1024.0f * (x1 + x16 * (1.0f / 16.0f));
+    }
+
+    float a1[M][CW], a16[M][CW];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int c = 0; c < CW; ++c) { a1[m][c] = 0.f; a16[m][c] = 0.f; }
+
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            const uint32_t q = w[j][c];
+            const uint32_t q8 = q >> 8;
+            const half2_t h0 = as_h2((q & 0x000F000Fu) | MAGIC2);   // k0, k4
+            const half2_t h1 = as_h2((q & 0x00F000F0u) | MAGIC2);   // k1, k5 (x16)
+            const half2_t h2 = as_h2((q8 & 0x000F000Fu) | MAGIC2);  // k2, k6
+            const half2_t h3 = as_h2((q8 & 0x00F000F0u) | MAGIC2);  // k3, k7 (x16)
+#pragma unroll
+            for (int m = 0; m < M; ++m) {
+                a1[m][c] = dot2(h0, xs[m][j][0], a1[m][c]);
+                a1[m][c] = dot2(h2, xs[m][j][2], a1[m][c]);
+                a16[m][c] = dot2(h1, xs[m][j][1], a16[m][c]);
+                a16[m][c] = dot2(h3, xs[m][j][3], a16[m][c]);
+            }
+        }
+    }
+
+    // zero point and scale for the lane's CW columns (same qzeros word: CW divides 8)
+    uint32_t qz = 0;
+    if constexpr (FMT == FMT_GPTQ) qz = p.qzeros[(size_t)g * (p.N >> 3) + (c0 >> 3)];
+    half_t sc[CW];
+    if constexpr (CW == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(p.scales + (size_t)g * p.N + c0);
+        const half_t* hv = reinterpret_cast<const half_t*>(&v);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sc[c] = hv[c];
+    } else {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) sc[c] = p.scales[(size_t)g * p.N + c0 + c];
+    }
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+#pragma unroll
+        for (int c = 0; c < CW; ++c) {
+            const float z = (float)zero_of<FMT>(qz, c0 + c, p.zero_offset);
+            const float u = a1[m][c] + a16[m][c] * (1.0f / 16.0f) - B[m] - z * X[m];
+            red[rb][m][cl * CW + c] = (float)sc[c] * u;
+        }
+    }
+    __syncthreads();
+
+    for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
+        const int m = i / C, cidx = i - m * C;
+        float s = 0.f;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
+        const size_t off = (size_t)m * p.N + n0 + cidx;
+        if (p.splits == 1) p.out[off] = (half_t)s;
+        else p.ws[(size_t)split * M * p.N + off] = s;
+    }
+    if (p.splits == 1) return;
+    if (splitk_arrive(p.counters + ct, p.splits, &flag))
+        splitk_finish<M>(p.ws, p.out, p.counters + ct, p.splits, p.N, n0, C);
+}
+
+// ------------------------------------------------------------------ host launchers
+
+namespace {
+// AWQ: CW = 1 word per lane per row, 32 rows per lane, 4 waves -> 256 columns x 256 rows.
+constexpr int AWQ_CW = 1, AWQ_RL = 32, AWQ_WAVES = 4;
+constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
+// GPTQ: CW = 4 columns per lane, 4 packed rows per lane, LPR = 32 -> 128 columns x 256 k.
+constexpr int GQ_CW = 4, GQ_RL = 4, GQ_WAVES = 4, GQ_LPR = 32;
+constexpr int GQ_COLS = GQ_LPR * GQ_CW;
+constexpr int GQ_ROWS = (64 / GQ_LPR) * GQ_WAVES * GQ_RL * 8;
+}  // namespace
+
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G) {
+    GemvShape s{};
+    if (M < 1 || M > GEMV_MAX_M) return s;
+    if (fmt == FMT_AWQ) {
+        if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
+        s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
+    } else {
+        if (N % GQ_COLS || K % GQ_ROWS || G % (GQ_RL * 8) || K % G) return s;
+        s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / GQ_ROWS; s.threads = 64 * GQ_WAVES;
+    }
+    return s;
+}
+
+template <int M>
+static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
+    const dim3 grid(s.col_tiles, s.splits), block(s.threads);
+    if (fmt == FMT_AWQ)
+        hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES>), grid, block, 0, st, p);
+    else if (fmt == FMT_GPTQ)
+        hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR>), grid, block, 0, st, p);
+    else
+        hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR>), grid, block, 0, st, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
+    switch (p.M) {
+        case 1: return launch_gemv_m<1>(fmt, p, s, st);
+        case 2: return launch_gemv_m<2>(fmt, p, s, st);
+        case 3: return launch_gemv_m<3>(fmt, p, s, st);
+        case 4: return launch_gemv_m<4>(fmt, p, s, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace w4a16

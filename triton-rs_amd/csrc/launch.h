@@ -1,0 +1,62 @@
+// Internal host-side interface between the C-ABI layer (api.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4a16 {
+
+typedef _Float16 half_t;
+
+constexpr int GEMV_MAX_M = 4;
+
+struct GemvParams {
+    const half_t* x;          // [M, K] contiguous
+    const uint32_t* qweight;  // GPTQ [K/8, N] | AWQ [K, N/8]
+    const half_t* scales;     // [K/G, N]
+    const uint32_t* qzeros;   // [K/G, N/8] (null for GPTQ_SYM)
+    half_t* out;              // [M, N]
+    float* ws;                // split-K partials [splits, M, N]
+    uint32_t* counters;       // [col_tiles], zero between calls
+    int M, N, K, G, zero_offset, splits;
+};
+
+struct GemvShape {
+    bool ok;
+    int col_tiles, splits, threads;
+};
+
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G);
+hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st);
+
+// Generic strided GEMM with the reference kernels' parameter list
+// (w4a16_gptq_gemm_typed.rs:110-128, awq_gemm_int4_typed.rs:96-114) plus optional g_idx.
+struct StridedParams {
+    const half_t* a;
+    const uint32_t* qweight;
+    const half_t* scales;
+    const uint32_t* qzeros;   // null for GPTQ_SYM
+    const int32_t* g_idx;     // null: group = k / G
+    half_t* c;
+    int m, n, k, group_size;
+    int stride_am, stride_ak, stride_qwk, stride_qwn, stride_sk, stride_sn;
+    int stride_qzk, stride_qzn, stride_cm, stride_cn;
+    int zero_offset;
+};
+hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st);
+
+// Standalone dequant to a transposed fp16 [N, K] matrix
+// (ferrum_dequant_int4.rs:27-139, ferrum_dequant_int4_sym.rs:24-131), and a row-major
+// [K, N] variant used by the dense fallback.
+struct DequantParams {
+    const uint32_t* qweight;
+    const half_t* scales;
+    const uint32_t* qzeros;
+    const int32_t* g_idx;
+    half_t* out;
+    int K, N, G, zero_offset;
+    int transposed;
+};
+hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st);
+
+}  // namespace w4a16
