@@ -87,14 +87,70 @@ def test_gemv_deterministic_and_reusable(torch_cuda, orc):
     assert_parity(ys[0], _oracle(orc, p))
 
 
+# ------------------------------------------------------------------ MFMA (small batch / prefill)
+
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N", [(5, 1024, 512), (8, 4096, 1024), (16, 512, 256),
+                                   (33, 1024, 512), (64, 2048, 768), (128, 1024, 512),
+                                   (200, 512, 1024)])
+def test_mfma_shapes(torch_cuda, orc, fmt, M, K, N):
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2000 + M + 7 * fmt)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, p.G) in ("skinny", "prefill")
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"mfma fmt={fmt} M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("fmt,G", [(AWQ, 32), (AWQ, 64), (GPTQ, 32), (GPTQ, 256), (SYM, 64)])
+def test_mfma_group_sizes(torch_cuda, orc, fmt, G):
+    p = Problem(fmt, M=24, K=1024, N=512, G=G, seed=2100 + G + fmt)
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"mfma fmt={fmt} G={G}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [
+    (AWQ, 8, 4096, 14336),         # config 1, M=8, gate/up
+    (AWQ, 8, 14336, 4096),         # config 1, M=8, down
+    (GPTQ, 16, 4096, 6144),        # config 2 shape (plain group order)
+    (GPTQ, 64, 4096, 6144),
+])
+def test_mfma_full_size(torch_cuda, orc, fmt, M, K, N):
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0x5EED0000 + (1 if fmt == AWQ else 2))
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"full fmt={fmt} M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+def test_prefill_full_size_sampled_rows(torch_cuda, orc, K, N):
+    """Config 3 (AWQ, M=2048) at full size; the oracle checks 24 sampled rows in full."""
+    P = pkg()
+    M = 2048
+    p = Problem(AWQ, M=M, K=K, N=N, G=128, seed=0x5EED0003)
+    assert P.plan("awq", M, N, K, 128) == "prefill"
+    y = _run_gemm(torch_cuda, p)
+    rows = np.random.default_rng(3).choice(M, 24, replace=False).astype(np.int32)
+    rows[:2] = [0, M - 1]
+    ref = orc.w4a16_gemm_rows(AWQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"prefill K={K} N={N}")
+    assert np.all(np.isfinite(y))
+
+
+def test_mfma_split_k_deterministic(torch_cuda, orc):
+    P = pkg()
+    p = Problem(AWQ, M=8, K=4096, N=1024, G=128, seed=2200)
+    args = [to_dev(a) for a in (p.x, p.qweight, p.scales, p.qzeros)]
+    ys = [P.gemm(*args, fmt="awq").cpu().numpy() for _ in range(3)]
+    assert all(np.array_equal(ys[0].view(np.uint16), y.view(np.uint16)) for y in ys[1:])
+    assert_parity(ys[0], _oracle(orc, p))
+
+
 # ------------------------------------------------------------------ strided / generic
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
-@pytest.mark.parametrize("M,K,N", [(16, 512, 256), (64, 1024, 384), (37, 384, 200)])
+@pytest.mark.parametrize("M,K,N", [(16, 384, 264), (64, 1024, 384), (37, 384, 200)])
 def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N):
-    if N % 8:
-        N = N // 8 * 8
+    """Shapes the tiled kernels do not take (N not a multiple of 256, K not of 128)."""
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=1200 + M + fmt)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, p.G) == "strided"
     y = _run_gemm(torch_cuda, p)
     assert_parity(y, _oracle(orc, p), what=f"strided fmt={fmt} M={M}")
 

@@ -96,8 +96,32 @@ static int check_gemm_args(int fmt, const void* x, const void* qweight, const vo
     return W4A16_OK;
 }
 
-static int plan(int fmt, int M, int N, int K, int G, bool has_gidx) {
-    if (!has_gidx && gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
+constexpr int DEFAULT_CUS = 256;  // MI355X
+
+// Compute units of the current device (cached per device; 256 when it cannot be queried).
+static int device_cus() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { (void)hipGetLastError(); return DEFAULT_CUS; }
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0) {
+        (void)hipGetLastError();
+        cus = DEFAULT_CUS;
+    }
+    cache[dev] = cus;
+    return cus;
+}
+
+static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
+    if (has_gidx) return W4A16_KERNEL_STRIDED;
+    if (gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
+    if (mfma_shape(fmt, M, N, K, G, cus).ok)
+        return M <= 64 ? W4A16_KERNEL_SKINNY : W4A16_KERNEL_PREFILL;
     return W4A16_KERNEL_STRIDED;
 }
 
@@ -127,9 +151,31 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool vec_ok = aligned(x, 16) && aligned(qweight, 16) && aligned(scales, 16) &&
-                        aligned(out, 4) && (!qzeros || aligned(qzeros, 16));
-    int kernel = plan(fmt, M, N, K, G, g_idx != nullptr);
+                        aligned(out, 16) && (!qzeros || aligned(qzeros, 16));
+    const int cus = device_cus();
+    int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
+
+    if (kernel == W4A16_KERNEL_SKINNY || kernel == W4A16_KERNEL_PREFILL) {
+        const MfmaShape s = mfma_shape(fmt, M, N, K, G, cus);
+        MfmaParams p{};
+        p.x = static_cast<const half_t*>(x);
+        p.qweight = static_cast<const uint32_t*>(qweight);
+        p.scales = static_cast<const half_t*>(scales);
+        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
+        p.splits = s.splits; p.k_per_split = s.k_per_split;
+        if (s.splits > 1) {
+            if ((size_t)s.col_tiles * s.row_tiles * sizeof(uint32_t) > COUNTER_BYTES)
+                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
+            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
+            if (rc) return rc;
+        }
+        hipError_t e = launch_mfma(fmt, p, s, st);
+        if (e != hipSuccess) return hip_fail(e, "mfma launch");
+        return W4A16_OK;
+    }
 
     if (kernel == W4A16_KERNEL_GEMV) {
         const GemvShape s = gemv_shape(fmt, M, N, K, G);

@@ -73,8 +73,10 @@ W4A16_API int hiprt_module_load(hiprt_ctx* ctx, const void* binary, size_t size,
     if (int rc = set_device(ctx)) return rc;
     hipModule_t m = nullptr;
     hipError_t e = hipModuleLoadData(&m, binary);
-    if (e != hipSuccess)
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // do not leave the failure for a later launch to report
         return fail(W4A16_ERR_MODULE_LOAD, "module load failed: %s", hipGetErrorString(e));
+    }
     hiprt_module* mod = new hiprt_module();
     mod->ctx = ctx;
     mod->module = m;
@@ -140,9 +142,11 @@ W4A16_API int hiprt_launch(hiprt_ctx* ctx, const hiprt_module* module, const cha
             fn = it->second;
         } else {
             hipError_t e = hipModuleGetFunction(&fn, module->module, kernel_name);
-            if (e != hipSuccess || !fn)
+            if (e != hipSuccess || !fn) {
+                (void)hipGetLastError();
                 return fail(W4A16_ERR_NOT_FOUND, "kernel `%s` not found in module: %s", kernel_name,
                             hipGetErrorString(e));
+            }
             module->fns.emplace(kernel_name, fn);
         }
     }

@@ -16,45 +16,9 @@
 // each dequantised weight to fp16 first; the difference is < 2^-11 relative per term).
 #include "device_common.h"
 #include "launch.h"
+#include "splitk.h"
 
 namespace w4a16 {
-
-// ------------------------------------------------------------------ split-K fix-up
-
-// Called by every thread of the block after it has written its partials for this tile.
-// Returns true in the (single) block that must produce the final output for the tile.
-__device__ __forceinline__ bool splitk_arrive(uint32_t* counter, int splits, int* lds_flag) {
-    __threadfence();  // release this thread's partial stores at agent scope
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t prev = atomicAdd(counter, 1u);
-        *lds_flag = (prev == (uint32_t)(splits - 1));
-    }
-    __syncthreads();
-    const bool last = *lds_flag != 0;
-    if (last) __threadfence();  // acquire: the other blocks' partials are visible
-    return last;
-}
-
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Sum the partials of one column tile in split order and store fp16; reset the counter.
-template <int M>
-__device__ __forceinline__ void splitk_finish(const float* __restrict__ ws, half_t* __restrict__ out,
-                                              uint32_t* counter, int splits, int N, int n0,
-                                              int C) {
-    for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
-        const int m = i / C, c = i - m * C;
-        const size_t off = (size_t)m * N + n0 + c;
-        float s = 0.f;
-        for (int sp = 0; sp < splits; ++sp) s += ld_coherent(ws + (size_t)sp * M * N + off);
-        out[off] = (half_t)s;
-    }
-    if (threadIdx.x == 0)
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // ------------------------------------------------------------------ AWQ GEMV
 
@@ -189,7 +153,7 @@ gemv_awq_kernel(GemvParams p) {
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
         if (p.splits == 1) p.out[off] = (half_t)s;
-        else p.ws[(size_t)split * M * p.N + off] = s;
+        else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(p.counters + ct, p.splits, &flag))
@@ -318,7 +282,7 @@ gemv_gptq_kernel(GemvParams p) {
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
         if (p.splits == 1) p.out[off] = (half_t)s;
-        else p.ws[(size_t)split * M * p.N + off] = s;
+        else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(p.counters + ct, p.splits, &flag))
@@ -353,6 +317,7 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G) {
 template <int M>
 static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     const dim3 grid(s.col_tiles, s.splits), block(s.threads);
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (fmt == FMT_AWQ)
         hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES>), grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ)

@@ -10,6 +10,7 @@ __global__ void __launch_bounds__(256) strided_gemm_kernel(StridedParams p) {
 
 hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st) {
     const dim3 grid((p.m + STR_BM - 1) / STR_BM, (p.n + STR_BN - 1) / STR_BN), block(256);
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (fmt == FMT_AWQ) hipLaunchKernelGGL(strided_gemm_kernel<FMT_AWQ>, grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ) hipLaunchKernelGGL(strided_gemm_kernel<FMT_GPTQ>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(strided_gemm_kernel<FMT_GPTQ_SYM>, grid, block, 0, st, p);
@@ -70,6 +71,7 @@ __global__ void __launch_bounds__(256) dequant_kernel(DequantParams p) {
 hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st) {
     const int64_t words = (int64_t)p.K * p.N / 8;
     const dim3 grid((unsigned)((words + 255) / 256)), block(256);
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (fmt == FMT_AWQ) hipLaunchKernelGGL(dequant_kernel<FMT_AWQ>, grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ) hipLaunchKernelGGL(dequant_kernel<FMT_GPTQ>, grid, block, 0, st, p);
     else hipLaunchKernelGGL(dequant_kernel<FMT_GPTQ_SYM>, grid, block, 0, st, p);

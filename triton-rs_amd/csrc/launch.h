@@ -29,6 +29,26 @@ struct GemvShape {
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G);
 hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st);
 
+// MFMA GEMM (M >= 5): 4 waves along N, register-direct dequant, optional split-K.
+struct MfmaParams {
+    const half_t* x;
+    const uint32_t* qweight;
+    const half_t* scales;
+    const uint32_t* qzeros;
+    half_t* out;
+    float* ws;
+    uint32_t* counters;
+    int M, N, K, G, zero_offset, splits, k_per_split;
+};
+
+struct MfmaShape {
+    bool ok;
+    int bm, cpl, col_tiles, row_tiles, splits, k_per_split;
+};
+
+MfmaShape mfma_shape(int fmt, int M, int N, int K, int G, int num_cus);
+hipError_t launch_mfma(int fmt, const MfmaParams& p, const MfmaShape& s, hipStream_t st);
+
 // Generic strided GEMM with the reference kernels' parameter list
 // (w4a16_gptq_gemm_typed.rs:110-128, awq_gemm_int4_typed.rs:96-114) plus optional g_idx.
 struct StridedParams {
