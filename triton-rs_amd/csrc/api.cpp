@@ -34,8 +34,8 @@ static inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) 
 
 // ------------------------------------------------------------------ workspace
 
-// One split-K workspace per (device, stream): counters (zeroed at allocation, reset to
-// zero by the kernels themselves) followed by fp32 partials.
+// One split-K workspace per (device, stream): per-(tile, split) flags (zeroed at
+// allocation, cleared again by the kernels themselves) followed by fp32 partials.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
@@ -43,7 +43,7 @@ struct Workspace {
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-constexpr size_t COUNTER_BYTES = 64 * 1024;  // room for 16384 column tiles
+constexpr size_t COUNTER_BYTES = 256 * 1024;  // room for 65536 (tile, split) flags
 
 static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
     int dev = 0;
@@ -167,8 +167,8 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.splits = s.splits; p.k_per_split = s.k_per_split;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.row_tiles * sizeof(uint32_t) > COUNTER_BYTES)
-                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
+            if ((size_t)s.col_tiles * s.row_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
+                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K flag area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;
         }
@@ -187,8 +187,8 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset; p.splits = s.splits;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * sizeof(uint32_t) > COUNTER_BYTES)
-                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K counter area");
+            if ((size_t)s.col_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
+                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K flag area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;
         }

@@ -34,6 +34,20 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// (a & mask) | bits in one v_and_or_b32. Written as inline asm with all operands in VGPRs:
+// left to itself the compiler emits v_and_b32 + v_or_b32, because a VOP3 instruction on
+// this target cannot encode the two literal constants.
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    return r;
+}
+
+// fp16 pair (1024 + nibble at bit 0, 1024 + nibble at bit 16) from v
+__device__ __forceinline__ half2_t nib_pair(uint32_t v) { return as_h2(and_or(v, 0x000F000Fu, MAGIC2)); }
+// same for the nibbles at bits 4 and 20, left in place: (1024 + 16 q_lo, 1024 + 16 q_hi)
+__device__ __forceinline__ half2_t nib_pair16(uint32_t v) { return as_h2(and_or(v, 0x00F000F0u, MAGIC2)); }
+
 // fp32 += a.x*b.x + a.y*b.y  (v_dot2c_f32_f16: f16 x f16 products, f32 accumulate)
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
@@ -67,6 +81,13 @@ __device__ __forceinline__ half_t dequant1(int q, int z, half_t s) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// base + byte offset with a 32-bit offset: lets the compiler use the global_load
+// "v_offset, s_base" form instead of a 64-bit address add per load
+template <typename T>
+__device__ __forceinline__ const T* at_bytes(const T* base, uint32_t byte_off) {
+    return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
+}
 
 // Streaming (non-temporal) loads for packed weights, which are read exactly once.
 __device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }

@@ -4,7 +4,8 @@
 // (crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:15-32 GPTQ [K/8, N] packed along K;
 // awq_gemm_int4_typed.rs:10-31 AWQ [K, N/8] packed along N, slot order [0,4,1,5,2,6,3,7]),
 // split over K so that a launch has ~900 workgroups, with a deterministic in-kernel
-// split-K fix-up (the last workgroup of a column tile sums the fp32 partials in split order).
+// split-K hand-off (splitk.h: a workgroup that sees all splits published sums the fp32
+// partials in split order).
 //
 // Per lane the inner loop is: 128-bit (or 32-bit) coalesced loads of packed words, a
 // nibble unpack into fp16 with the 0x6400 exponent trick (1024 + q, or 1024 + 16 q for the
@@ -49,22 +50,8 @@ gemv_awq_kernel(GemvParams p) {
     const int k0 = split * R + rb * RL;            // first row of this lane
     const int g = k0 / p.G;
 
-    // ---- issue all weight loads (RL rows x CW words) up front
-    uint32_t w[RL][CW];
-    const uint32_t* qp = p.qweight + (size_t)k0 * NW + wc0;
-#pragma unroll
-    for (int j = 0; j < RL; ++j) {
-        if constexpr (CW == 4) {
-            const u32x4 v = ld_stream4(qp + (size_t)j * NW);
-            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
-        } else if constexpr (CW == 2) {
-            const u32x2 v = ld_stream2(qp + (size_t)j * NW);
-            w[j][0] = v.x; w[j][1] = v.y;
-        } else {
-            w[j][0] = ld_stream(qp + (size_t)j * NW);
-        }
-    }
-
+    // ---- x first (small, cached), so the weight loads below can be consumed in issue
+    // order while later rows are still in flight
     // ---- x pairs (rows 2i, 2i+1 of this lane) for every m, and X = sum of x
     half2_t xs[M][RL / 2];
     float X[M];
@@ -82,6 +69,24 @@ gemv_awq_kernel(GemvParams p) {
 #pragma unroll
         for (int i = 0; i < RL / 2; ++i) s = dot2(xs[m][i], one2, s);
         X[m] = s;
+    }
+
+    // ---- issue all weight loads (RL rows x CW words) up front
+    // 32-bit element offsets from the uniform base (global_load ... v_off, s_base)
+    uint32_t w[RL][CW];
+    const uint32_t off0 = (uint32_t)k0 * (uint32_t)NW + (uint32_t)wc0;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        const uint32_t off = off0 + (uint32_t)j * (uint32_t)NW;
+        if constexpr (CW == 4) {
+            const u32x4 v = ld_stream4(at_bytes(p.qweight, 4u * off));
+            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
+        } else if constexpr (CW == 2) {
+            const u32x2 v = ld_stream2(at_bytes(p.qweight, 4u * off));
+            w[j][0] = v.x; w[j][1] = v.y;
+        } else {
+            w[j][0] = ld_stream(at_bytes(p.qweight, 4u * off));
+        }
     }
 
     // ---- main loop: acc[m][cw][slot]
@@ -103,14 +108,14 @@ gemv_awq_kernel(GemvParams p) {
             const uint32_t hi = perm(b, a, 0x07060302u);
             const uint32_t lo8 = lo >> 8, hi8 = hi >> 8;
             half2_t h[8];
-            h[0] = as_h2((lo & 0x000F000Fu) | MAGIC2);   // slot 0: 1024 + q
-            h[1] = as_h2((lo & 0x00F000F0u) | MAGIC2);   // slot 1: 1024 + 16 q
-            h[2] = as_h2((lo8 & 0x000F000Fu) | MAGIC2);  // slot 2
-            h[3] = as_h2((lo8 & 0x00F000F0u) | MAGIC2);  // slot 3 (x16)
-            h[4] = as_h2((hi & 0x000F000Fu) | MAGIC2);   // slot 4
-            h[5] = as_h2((hi & 0x00F000F0u) | MAGIC2);   // slot 5 (x16)
-            h[6] = as_h2((hi8 & 0x000F000Fu) | MAGIC2);  // slot 6
-            h[7] = as_h2((hi8 & 0x00F000F0u) | MAGIC2);  // slot 7 (x16)
+            h[0] = nib_pair(lo);      // slot 0: 1024 + q
+            h[1] = nib_pair16(lo);    // slot 1: 1024 + 16 q
+            h[2] = nib_pair(lo8);     // slot 2
+            h[3] = nib_pair16(lo8);   // slot 3 (x16)
+            h[4] = nib_pair(hi);      // slot 4
+            h[5] = nib_pair16(hi);    // slot 5 (x16)
+            h[6] = nib_pair(hi8);     // slot 6
+            h[7] = nib_pair16(hi8);   // slot 7 (x16)
 #pragma unroll
             for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -156,8 +161,9 @@ gemv_awq_kernel(GemvParams p) {
         else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    if (splitk_arrive(p.counters + ct, p.splits, &flag))
-        splitk_finish<M>(p.ws, p.out, p.counters + ct, p.splits, p.N, n0, C);
+    uint32_t* flags = p.counters + (size_t)ct * p.splits;
+    if (splitk_arrive(flags, split, p.splits, &flag))
+        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
 }
 
 // ------------------------------------------------------------------ GPTQ GEMV
@@ -187,21 +193,6 @@ gemv_gptq_kernel(GemvParams p) {
     const int k0 = kp0 * 8;
     const int g = k0 / p.G;
 
-    uint32_t w[RL][CW];
-    const uint32_t* qp = p.qweight + (size_t)kp0 * p.N + c0;
-#pragma unroll
-    for (int j = 0; j < RL; ++j) {
-        if constexpr (CW == 4) {
-            const u32x4 v = ld_stream4(qp + (size_t)j * p.N);
-            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
-        } else if constexpr (CW == 2) {
-            const u32x2 v = ld_stream2(qp + (size_t)j * p.N);
-            w[j][0] = v.x; w[j][1] = v.y;
-        } else {
-            w[j][0] = ld_stream(qp + (size_t)j * p.N);
-        }
-    }
-
     // x for packed row j, rearranged to the unpack order: (x0,x4) (x1,x5) (x2,x6) (x3,x7)
     half2_t xs[M][RL][4];
     float X[M], B[M];
@@ -225,6 +216,22 @@ gemv_gptq_kernel(GemvParams p) {
         B[m] = 1024.0f * (x1 + x16 * (1.0f / 16.0f));
     }
 
+    uint32_t w[RL][CW];
+    const uint32_t off0 = (uint32_t)kp0 * (uint32_t)p.N + (uint32_t)c0;
+#pragma unroll
+    for (int j = 0; j < RL; ++j) {
+        const uint32_t off = off0 + (uint32_t)j * (uint32_t)p.N;
+        if constexpr (CW == 4) {
+            const u32x4 v = ld_stream4(at_bytes(p.qweight, 4u * off));
+            w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
+        } else if constexpr (CW == 2) {
+            const u32x2 v = ld_stream2(at_bytes(p.qweight, 4u * off));
+            w[j][0] = v.x; w[j][1] = v.y;
+        } else {
+            w[j][0] = ld_stream(at_bytes(p.qweight, 4u * off));
+        }
+    }
+
     float a1[M][CW], a16[M][CW];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -237,10 +244,10 @@ gemv_gptq_kernel(GemvParams p) {
         for (int c = 0; c < CW; ++c) {
             const uint32_t q = w[j][c];
             const uint32_t q8 = q >> 8;
-            const half2_t h0 = as_h2((q & 0x000F000Fu) | MAGIC2);   // k0, k4
-            const half2_t h1 = as_h2((q & 0x00F000F0u) | MAGIC2);   // k1, k5 (x16)
-            const half2_t h2 = as_h2((q8 & 0x000F000Fu) | MAGIC2);  // k2, k6
-            const half2_t h3 = as_h2((q8 & 0x00F000F0u) | MAGIC2);  // k3, k7 (x16)
+            const half2_t h0 = nib_pair(q);      // k0, k4
+            const half2_t h1 = nib_pair16(q);    // k1, k5 (x16)
+            const half2_t h2 = nib_pair(q8);     // k2, k6
+            const half2_t h3 = nib_pair16(q8);   // k3, k7 (x16)
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 a1[m][c] = dot2(h0, xs[m][j][0], a1[m][c]);
@@ -285,8 +292,9 @@ gemv_gptq_kernel(GemvParams p) {
         else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    if (splitk_arrive(p.counters + ct, p.splits, &flag))
-        splitk_finish<M>(p.ws, p.out, p.counters + ct, p.splits, p.N, n0, C);
+    uint32_t* flags = p.counters + (size_t)ct * p.splits;
+    if (splitk_arrive(flags, split, p.splits, &flag))
+        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
 }
 
 // ------------------------------------------------------------------ host launchers

@@ -29,10 +29,6 @@ namespace w4a16 {
 namespace {
 constexpr int SK = 128;        // k per A stage
 constexpr int LDA = SK + 8;    // halfs per LDS row of A (272-byte rows)
-constexpr uint32_t LO4 = 0x000F000Fu;
-
-__device__ __forceinline__ half2_t nib_pair(uint32_t v) { return as_h2((v & LO4) | MAGIC2); }
-
 // fp16 (q - z) * s for a pair built by nib_pair (1024 + q): exact subtract, one RNE multiply
 __device__ __forceinline__ half2_t deq2(half2_t h, half2_t hz, half2_t hs) { return (h - hz) * hs; }
 
@@ -269,10 +265,10 @@ __global__ void __launch_bounds__(256) mfma_gemm_kernel(MfmaParams p) {
             for (int c = 0; c < CPL; ++c) st_coherent(dst + c, acc[r][c][i]);
         }
     const int tile = mt * gridDim.x + ct;
-    if (splitk_arrive(p.counters + tile, p.splits, &flag)) {
+    uint32_t* flags = p.counters + (size_t)tile * p.splits;
+    if (splitk_arrive(flags, split, p.splits, &flag)) {
         const int rows = min(BM, p.M - m0);
-        splitk_finish_rows(p.ws, p.out, p.counters + tile, p.splits, p.M, p.N, m0, rows,
-                           ct * WGN, WGN);
+        splitk_finish_rows(p.ws, p.out, flags, p.splits, p.M, p.N, m0, rows, ct * WGN, WGN);
     }
 }
 
