@@ -146,10 +146,11 @@ def test_mfma_split_k_deterministic(torch_cuda, orc):
 # ------------------------------------------------------------------ strided / generic
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
-@pytest.mark.parametrize("M,K,N", [(16, 384, 264), (64, 1024, 384), (37, 384, 200)])
-def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N):
-    """Shapes the tiled kernels do not take (N not a multiple of 256, K not of 128)."""
-    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=1200 + M + fmt)
+@pytest.mark.parametrize("M,K,N,G", [(16, 384, 264, 128), (64, 960, 384, 64), (37, 384, 200, 128),
+                                     (300, 640, 136, 64)])
+def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N, G):
+    """Shapes the tiled kernels do not take (N not a multiple of their strip, K not of 128)."""
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1200 + M + fmt)
     assert pkg().plan(FMT_NAME[fmt], M, N, K, p.G) == "strided"
     y = _run_gemm(torch_cuda, p)
     assert_parity(y, _oracle(orc, p), what=f"strided fmt={fmt} M={M}")

@@ -120,8 +120,8 @@ static int device_cus() {
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) return W4A16_KERNEL_STRIDED;
     if (gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
-    if (mfma_shape(fmt, M, N, K, G, cus).ok)
-        return M <= 64 ? W4A16_KERNEL_SKINNY : W4A16_KERNEL_PREFILL;
+    if (M <= 64 && skinny_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_SKINNY;
+    if (mfma_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
     return W4A16_KERNEL_STRIDED;
 }
 
@@ -156,7 +156,28 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
 
-    if (kernel == W4A16_KERNEL_SKINNY || kernel == W4A16_KERNEL_PREFILL) {
+    if (kernel == W4A16_KERNEL_SKINNY) {
+        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus);
+        SkinnyParams p{};
+        p.x = static_cast<const half_t*>(x);
+        p.qweight = static_cast<const uint32_t*>(qweight);
+        p.scales = static_cast<const half_t*>(scales);
+        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
+        p.splits = s.splits; p.steps_per_wave = s.steps_per_wave;
+        if (s.splits > 1) {
+            if ((size_t)s.col_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
+                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K flag area");
+            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.flags, &p.ws);
+            if (rc) return rc;
+        }
+        hipError_t e = launch_skinny(fmt, p, s, st);
+        if (e != hipSuccess) return hip_fail(e, "skinny launch");
+        return W4A16_OK;
+    }
+
+    if (kernel == W4A16_KERNEL_PREFILL) {
         const MfmaShape s = mfma_shape(fmt, M, N, K, G, cus);
         MfmaParams p{};
         p.x = static_cast<const half_t*>(x);

@@ -1,0 +1,269 @@
+// Small-batch W4A16 GEMM (5 <= M <= 64) on MFMA: the weight stream is the cost (HBM-bound),
+// so the kernel is built to keep loads in flight and to need few workgroup-to-workgroup
+// reductions.
+//
+// A workgroup owns a strip of WN = 16*CPL columns; its 4 waves split the strip's K range
+// four ways and stream independently (no LDS staging, no barrier in the main loop). Each
+// lane keeps a ring of PF k32 steps of loads in flight: its packed words, the activation
+// fragments and the group's scales/zeros. Words are dequantised bit-exactly
+// (W16 = RNE_f16((q - z) * s), crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:246-260,
+// awq_gemm_int4_typed.rs:213-228) straight into MFMA B-operand registers and multiplied
+// with v_mfma_f32_16x16x32_f16 (fp32 accumulation, the reference's tt.dot). The four waves'
+// accumulators are summed in LDS; when the strip count alone cannot fill the GPU the K
+// range is also split across workgroups, joined by the flag hand-off of splitk.h.
+//
+// Operand layouts are those of kernels_mfma.hip: slot j of MFMA c is output column
+// n0 + CPL*j + c; GPTQ k-blocks are consumed in the unpack order (k0,k4)(k1,k5)(k2,k6)(k3,k7)
+// with A permuted to match, AWQ in natural order via row pairs.
+#include "device_common.h"
+#include "launch.h"
+#include "splitk.h"
+
+namespace w4a16 {
+
+namespace {
+__device__ __forceinline__ half2_t deq2(half2_t h, half2_t hz, half2_t hs) { return (h - hz) * hs; }
+__device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
+    return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+}  // namespace
+
+template <int FMT, int BM, int CPL, int PF>
+__global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
+    constexpr int RB = BM / 16;
+    constexpr int WN = 16 * CPL;
+    constexpr int WPS = (FMT == FMT_AWQ) ? 8 : CPL;   // packed words per lane per k32 step
+    constexpr int SW = (CPL + 1) / 2;                  // scale words (2 halfs each) per lane
+
+    __shared__ float red[4][BM][WN + 1];
+    __shared__ int flag;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, kb = lane >> 4;
+    const int ct = blockIdx.x, split = blockIdx.y;
+    const int n0 = ct * WN;
+    const int nl = n0 + CPL * j;              // first output column of this lane
+    const int NW = p.N >> 3;
+    const int spw = p.steps_per_wave;
+    const int step0 = (split * 4 + wave) * spw;  // first k32 step of this wave
+
+    // ------------------------------------------------ per-step loads into ring slot u
+    uint32_t bw[PF][WPS];
+    u32x4 areg[PF][RB];
+    uint32_t sreg[PF][SW], zreg[PF];
+
+    auto issue = [&](int u, int step) {
+        const int kg = 32 * step;
+        // packed weights
+        if constexpr (FMT == FMT_AWQ) {
+            const int wcol = (CPL == 8) ? (n0 >> 3) + j : (nl >> 3);
+            const uint32_t off0 = (uint32_t)(kg + 8 * kb) * (uint32_t)NW + (uint32_t)wcol;
+#pragma unroll
+            for (int r = 0; r < 8; ++r)
+                bw[u][r] = ld_stream(at_bytes(p.qweight, 4u * (off0 + (uint32_t)r * (uint32_t)NW)));
+        } else {
+            const uint32_t off = (uint32_t)((kg >> 3) + kb) * (uint32_t)p.N + (uint32_t)nl;
+            if constexpr (CPL == 2) {
+                const u32x2 v = ld_stream2(at_bytes(p.qweight, 4u * off));
+                bw[u][0] = v.x; bw[u][1] = v.y;
+            } else {
+#pragma unroll
+                for (int h = 0; h < CPL / 4; ++h) {
+                    const u32x4 v = ld_stream4(at_bytes(p.qweight, 4u * (off + 4 * h)));
+                    bw[u][4 * h + 0] = v.x; bw[u][4 * h + 1] = v.y;
+                    bw[u][4 * h + 2] = v.z; bw[u][4 * h + 3] = v.w;
+                }
+            }
+        }
+        // activation fragments: row 16 r + j, k = kg + 8 kb .. + 7 (rows >= M read as 0)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int m = 16 * r + j;
+            areg[u][r] = (m < p.M) ? *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + kg + 8 * kb)
+                                   : u32x4{0u, 0u, 0u, 0u};
+        }
+        // scales and zero word of the lane's columns for this step's group
+        const int g = kg / p.G;
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(p.scales + (size_t)g * p.N + nl);
+        if constexpr (CPL == 8) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(sp);
+            sreg[u][0] = v.x; sreg[u][1] = v.y; sreg[u][2] = v.z; sreg[u][3] = v.w;
+        } else if constexpr (CPL == 4) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(sp);
+            sreg[u][0] = v.x; sreg[u][1] = v.y;
+        } else {
+            sreg[u][0] = sp[0];
+        }
+        zreg[u] = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (nl >> 3)];
+    };
+
+    float4_t acc[RB][CPL];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int u = 0; u < PF; ++u)
+        if (u < spw) issue(u, step0 + u);
+
+    for (int s0 = 0; s0 < spw; s0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int s = s0 + u;
+            if (s >= spw) break;
+            // zero point (as fp16 1024 + z) and scale per column, splatted
+            half2_t hz[CPL], hs[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const int cw = (nl & 7) + c;   // column within its qzeros word
+                int z;
+                if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
+                else if constexpr (FMT == FMT_AWQ) z = nib(zreg[u], awq_slot(cw));
+                else z = nib(zreg[u], cw) + p.zero_offset;
+                const half_t zh = (half_t)(1024 + z);
+                hz[c] = half2_t{zh, zh};
+                const half2_t sv = as_h2(sreg[u][c >> 1]);
+                const half_t sc = (c & 1) ? sv.y : sv.x;
+                hs[c] = half2_t{sc, sc};
+            }
+            // dequantise B fragments
+            half8_t bf[CPL];
+            if constexpr (FMT == FMT_AWQ) {
+                half2_t pr[4][CPL];
+#pragma unroll
+                for (int rp = 0; rp < 4; ++rp) {
+                    const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
+                    const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
+                    const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
+                    if constexpr (CPL == 8) {
+#pragma unroll
+                        for (int sl = 0; sl < 8; ++sl) {
+                            const uint32_t src = sl < 4 ? p0 : p1;
+                            const int col = awq_col_of_slot(sl);
+                            pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
+                        }
+                    } else {
+                        // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
+                        const int sh = 8 * (j & 1);
+                        const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
+                        pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
+                        pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
+                        pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
+                        pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+            } else {
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t w = bw[u][c];
+                    bf[c] = cat8(deq2(nib_pair(w), hz[c], hs[c]), deq2(nib_pair(w >> 4), hz[c], hs[c]),
+                                 deq2(nib_pair(w >> 8), hz[c], hs[c]), deq2(nib_pair(w >> 12), hz[c], hs[c]));
+                }
+            }
+            // MFMAs
+#pragma unroll
+            for (int r = 0; r < RB; ++r) {
+                u32x4 a = areg[u][r];
+                if constexpr (FMT != FMT_AWQ)   // k order (0,4)(1,5)(2,6)(3,7) as in the GPTQ unpack
+                    a = u32x4{perm(a.z, a.x, 0x05040100u), perm(a.z, a.x, 0x07060302u),
+                              perm(a.w, a.y, 0x05040100u), perm(a.w, a.y, 0x07060302u)};
+                const half8_t af = __builtin_bit_cast(half8_t, a);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c)
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c], acc[r][c], 0, 0, 0);
+            }
+            if (s + PF < spw) issue(u, step0 + s + PF);
+        }
+    }
+
+    // ------------------------------------------------ reduce the 4 waves' K ranges
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) red[wave][16 * r + 4 * kb + i][CPL * j + c] = acc[r][c][i];
+    __syncthreads();
+    for (int o = threadIdx.x; o < BM * WN; o += 256) {
+        const int m = o / WN, col = o - m * WN;
+        if (m >= p.M) continue;
+        const float v = red[0][m][col] + red[1][m][col] + red[2][m][col] + red[3][m][col];
+        const size_t off = (size_t)m * p.N + n0 + col;
+        if (p.splits == 1) p.out[off] = (half_t)v;
+        else st_coherent(p.ws + (size_t)split * p.M * p.N + off, v);
+    }
+    if (p.splits == 1) return;
+    uint32_t* flags = p.flags + (size_t)ct * p.splits;
+    if (splitk_arrive(flags, split, p.splits, &flag))
+        splitk_finish_rows(p.ws, p.out, flags, p.splits, p.M, p.N, 0, p.M, n0, WN);
+}
+
+// ------------------------------------------------------------------ host side
+
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus) {
+    SkinnyShape s{};
+    if (M < 1 || M > 64 || K % 128 || G % 32 || K % G) return s;
+    s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+    const bool awq = fmt == FMT_AWQ;
+    // narrowest strip (most workgroups) the format supports; wide strips at BM=64 would
+    // not fit the cross-wave reduction buffer
+    int cpl = 0;
+    for (int c : {2, 4, 8}) {
+        if (awq && c < 4) continue;
+        if (s.bm == 64 && c > 4) continue;
+        if (N % (16 * c) == 0) { cpl = c; break; }
+    }
+    if (!cpl) return s;
+    s.cpl = cpl;
+    s.col_tiles = N / (16 * cpl);
+    // split K across workgroups until ~2 workgroups per CU, keeping the fp32 partials
+    // (splits * M * N * 4 bytes) under a quarter of the packed weights (K * N / 2 bytes)
+    int splits = 1;
+    while (s.col_tiles * splits < 2 * num_cus && K % (128 * 2 * splits) == 0 &&
+           2 * splits * 32 * M <= K)
+        splits *= 2;
+    s.splits = splits;
+    s.steps_per_wave = K / (128 * splits);
+    s.ok = true;
+    return s;
+}
+
+template <int FMT, int BM, int CPL>
+static void launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    constexpr int PF = (FMT == FMT_AWQ || CPL >= 8) ? 3 : 4;
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF>), dim3(s.col_tiles, s.splits), dim3(256), 0,
+                       st, p);
+}
+
+template <int FMT, int BM>
+static void launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    if constexpr (FMT != FMT_AWQ) {
+        if (s.cpl == 2) { launch_t<FMT, BM, 2>(p, s, st); return; }
+    }
+    if constexpr (BM < 64) {
+        if (s.cpl == 8) { launch_t<FMT, BM, 8>(p, s, st); return; }
+    }
+    launch_t<FMT, BM, 4>(p, s, st);
+}
+
+template <int FMT>
+static void launch_fmt(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    switch (s.bm) {
+        case 16: launch_bm<FMT, 16>(p, s, st); break;
+        case 32: launch_bm<FMT, 32>(p, s, st); break;
+        default: launch_bm<FMT, 64>(p, s, st); break;
+    }
+}
+
+hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
+    if (fmt == FMT_AWQ) launch_fmt<FMT_AWQ>(p, s, st);
+    else if (fmt == FMT_GPTQ) launch_fmt<FMT_GPTQ>(p, s, st);
+    else launch_fmt<FMT_GPTQ_SYM>(p, s, st);
+    return hipGetLastError();
+}
+
+}  // namespace w4a16

@@ -49,6 +49,26 @@ struct MfmaShape {
 MfmaShape mfma_shape(int fmt, int M, int N, int K, int G, int num_cus);
 hipError_t launch_mfma(int fmt, const MfmaParams& p, const MfmaShape& s, hipStream_t st);
 
+// Small-batch MFMA GEMM (5 <= M <= 64): waves split K inside a workgroup.
+struct SkinnyParams {
+    const half_t* x;
+    const uint32_t* qweight;
+    const half_t* scales;
+    const uint32_t* qzeros;
+    half_t* out;
+    float* ws;
+    uint32_t* flags;
+    int M, N, K, G, zero_offset, splits, steps_per_wave;
+};
+
+struct SkinnyShape {
+    bool ok;
+    int bm, cpl, col_tiles, splits, steps_per_wave;
+};
+
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus);
+hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st);
+
 // Generic strided GEMM with the reference kernels' parameter list
 // (w4a16_gptq_gemm_typed.rs:110-128, awq_gemm_int4_typed.rs:96-114) plus optional g_idx.
 struct StridedParams {
