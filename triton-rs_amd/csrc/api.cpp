@@ -121,7 +121,7 @@ static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DE
     if (has_gidx) return W4A16_KERNEL_STRIDED;
     if (gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
     if (M <= 64 && skinny_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_SKINNY;
-    if (mfma_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
+    if (prefill_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
     return W4A16_KERNEL_STRIDED;
 }
 
@@ -178,23 +178,16 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     }
 
     if (kernel == W4A16_KERNEL_PREFILL) {
-        const MfmaShape s = mfma_shape(fmt, M, N, K, G, cus);
-        MfmaParams p{};
+        const PrefillShape s = prefill_shape(fmt, M, N, K, G, cus);
+        PrefillParams p{};
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
         p.scales = static_cast<const half_t*>(scales);
         p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
-        p.splits = s.splits; p.k_per_split = s.k_per_split;
-        if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.row_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
-                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K flag area");
-            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
-            if (rc) return rc;
-        }
-        hipError_t e = launch_mfma(fmt, p, s, st);
-        if (e != hipSuccess) return hip_fail(e, "mfma launch");
+        hipError_t e = launch_prefill(fmt, p, s, st);
+        if (e != hipSuccess) return hip_fail(e, "prefill launch");
         return W4A16_OK;
     }
 

@@ -12,7 +12,7 @@
 // accumulators are summed in LDS; when the strip count alone cannot fill the GPU the K
 // range is also split across workgroups, joined by the flag hand-off of splitk.h.
 //
-// Operand layouts are those of kernels_mfma.hip: slot j of MFMA c is output column
+// Operand layouts: slot j of MFMA c is output column
 // n0 + CPL*j + c; GPTQ k-blocks are consumed in the unpack order (k0,k4)(k1,k5)(k2,k6)(k3,k7)
 // with A permuted to match, AWQ in natural order via row pairs.
 #include "device_common.h"

@@ -29,25 +29,24 @@ struct GemvShape {
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G);
 hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st);
 
-// MFMA GEMM (M >= 5): 4 waves along N, register-direct dequant, optional split-K.
-struct MfmaParams {
+// Prefill GEMM (large M): dequant-to-LDS MFMA tiles.
+struct PrefillParams {
     const half_t* x;
     const uint32_t* qweight;
     const half_t* scales;
     const uint32_t* qzeros;
     half_t* out;
-    float* ws;
-    uint32_t* counters;
-    int M, N, K, G, zero_offset, splits, k_per_split;
+    int M, N, K, G, zero_offset;
 };
 
-struct MfmaShape {
+struct PrefillShape {
     bool ok;
-    int bm, cpl, col_tiles, row_tiles, splits, k_per_split;
+    int bm, col_tiles, row_tiles;
+    size_t lds;
 };
 
-MfmaShape mfma_shape(int fmt, int M, int N, int K, int G, int num_cus);
-hipError_t launch_mfma(int fmt, const MfmaParams& p, const MfmaShape& s, hipStream_t st);
+PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus);
+hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st);
 
 // Small-batch MFMA GEMM (5 <= M <= 64): waves split K inside a workgroup.
 struct SkinnyParams {
