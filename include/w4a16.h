@@ -131,6 +131,66 @@ W4A16_API int w4a16_dequant(void* stream, int fmt, const void* qweight, const vo
                             int32_t N, int32_t group_size, int32_t gptq_zero_offset,
                             int transposed);
 
+/* ------------------------------------------------------------------ fused MoE
+ * Not in the reference (it has no MoE kernel; SURVEY/BASELINE config 4 asks for one). The
+ * pieces compose as: route -> align -> grouped GEMM (w1|w3) -> silu*mul -> grouped GEMM (w2)
+ * -> weighted sum. Pairs are (token t, slot j) with index p = t * topk + j, P = T * topk. */
+
+/* softmax over E fp32 logits per token, top-k (ties -> lower expert index); weights are the
+ * chosen probabilities, renormalised to sum to 1 when `renormalize` != 0.
+ * topk_ids int32 [T, topk], topk_weights fp32 [T, topk]. E <= 256, topk <= 8. */
+W4A16_API int w4a16_moe_route(void* stream, const float* logits, int32_t T, int32_t E,
+                              int32_t topk, int32_t renormalize, int32_t* topk_ids,
+                              float* topk_weights);
+
+/* Sort pairs by expert (stable in p), padding each expert to a multiple of block_m with the
+ * sentinel num_pairs. sorted_ids int32 [capacity], expert_ids int32 [capacity / block_m],
+ * *num_tokens_post_padded = padded length (device). capacity must be a multiple of block_m
+ * and >= num_pairs + E * (block_m - 1). */
+W4A16_API int w4a16_moe_align(void* stream, const int32_t* topk_ids, int32_t num_pairs, int32_t E,
+                              int32_t block_m, int32_t capacity, int32_t* sorted_ids,
+                              int32_t* expert_ids, int32_t* num_tokens_post_padded);
+
+/* Grouped W4A16 GEMM over expert-sorted blocks: for every block of block_m sorted pairs with
+ * expert e, out[p, :] = a[p / a_div, :] @ W16_e, W16_e from the e-th slice of the stacked
+ * qweight / scales / qzeros (expert strides in elements). out is [num_pairs, N]; padding rows
+ * are skipped. N % 256 == 0, K % 64 == 0, block_m in {64, 128}. */
+W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div,
+                             const void* qweight, const void* scales, const void* qzeros,
+                             int64_t qweight_expert_stride, int64_t scales_expert_stride,
+                             int64_t qzeros_expert_stride, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                             void* out, int32_t num_pairs, int32_t N, int32_t K,
+                             int32_t group_size, int32_t block_m, int32_t capacity,
+                             int32_t gptq_zero_offset);
+
+/* replaces fused_silu_mul_interleaved_f16 (crates/triton-kernels/src/elementwise.rs:188-212):
+ * out[b * inter + i] = f16(silu(g) * u), g = gate_up[b * 2 * inter + i],
+ * u = gate_up[b * 2 * inter + inter + i], silu(g) = g / (1 + exp(-g)) in f32.
+ * total = batch * inter; inter % 8 == 0. */
+W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, void* out,
+                                             int32_t inter, int32_t total);
+
+/* out[t, :] = f16(sum_j topk_weights[t, j] * f32 y_pairs[t * topk + j, :]); K % 8 == 0. */
+W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk_weights,
+                            void* out, int32_t T, int32_t topk, int32_t K);
+
+/* Bytes of workspace w4a16_fused_moe needs (routing tables and fp16 intermediates). */
+W4A16_API size_t w4a16_fused_moe_workspace_size(int32_t T, int32_t E, int32_t topk, int32_t I,
+                                                int32_t K, int32_t block_m);
+
+/* Whole MoE layer: y[T, K] from x[T, K] and router logits[T, E]. Expert weights are stacked
+ * along a leading expert dimension in the chosen packing: w13 is [E] x (K -> 2I) with columns
+ * [0, I) = w1 (gate) and [I, 2I) = w3 (up); w2 is [E] x (I -> K). `workspace` (256-byte
+ * aligned, w4a16_fused_moe_workspace_size bytes) is caller-owned. */
+W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float* router_logits,
+                              int32_t T, int32_t K, int32_t I, int32_t E, int32_t topk,
+                              int32_t renormalize, const void* w13_qweight, const void* w13_scales,
+                              const void* w13_qzeros, const void* w2_qweight,
+                              const void* w2_scales, const void* w2_qzeros, int32_t group_size,
+                              int32_t block_m, int32_t gptq_zero_offset, void* workspace,
+                              size_t workspace_bytes, void* out);
+
 /* ------------------------------------------------------------------ runtime
  * A HIP backend for the reference's DeviceRuntime trait (crates/triton-runtime/src/
  * lib.rs:64-85): load a code object, launch a kernel by name with KernelArg-style

@@ -198,12 +198,13 @@ def moe_align(ids, E, block_m):
     return sorted_ids[:n].copy(), expert_ids[: n // block_m].copy(), n
 
 
-def moe_forward(x, ids, weights, w13_list, w2_list):
-    """y[T, K] from dequantised per-expert w13 [K, 2I] and w2 [I, K] (float16 arrays)."""
+def moe_forward(x, ids, weights, w13_list, w2_list, inter=None):
+    """y[T, K] from dequantised per-expert w13 [K, 2I] and w2 [I, K] (float16 arrays).
+    Experts no token selects may be placeholders when `inter` (I) is given."""
     x = _u16(x)
     T, K = x.shape
     E = len(w13_list)
-    I = w2_list[0].shape[0]
+    I = inter if inter is not None else w2_list[0].shape[0]
     ids = np.ascontiguousarray(ids, dtype=np.int32)
     weights = np.ascontiguousarray(weights, dtype=np.float32)
     topk = ids.shape[1]

@@ -160,3 +160,28 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
         assert "v_dot2" in body, name
     for name, body in strided.items():
         assert "v_mfma_f32_16x16x32_f16" in body, name
+
+
+def test_moe_argument_errors():
+    P = pkg()
+    L = P.lib()
+    v = ctypes.c_void_p(256)
+    assert L.w4a16_moe_route(None, None, 4, 8, 2, 1, v, v) == P.ERR_INVALID_ARG
+    assert L.w4a16_moe_route(None, v, 4, 8, 9, 1, v, v) == P.ERR_INVALID_ARG      # topk > E
+    assert L.w4a16_moe_route(None, v, 4, 300, 2, 1, v, v) == P.ERR_UNSUPPORTED   # E > 256
+    # capacity below pairs + E * (block_m - 1)
+    assert L.w4a16_moe_align(None, v, 1024, 8, 64, 1024, v, v, v) == P.ERR_INVALID_ARG
+    assert "capacity" in L.w4a16_last_error().decode()
+    # grouped GEMM shape limits
+    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, v, v, v, v, 1024, 1004, 4096, 128, 64,
+                          1536, 1)
+    assert rc == P.ERR_INVALID_ARG        # N % 8
+    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, v, v, v, v, 1024, 1032, 4096, 128, 64,
+                          1536, 1)
+    assert rc == P.ERR_UNSUPPORTED        # N % 256
+    assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, 250) == P.ERR_INVALID_ARG
+    assert L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64) > 512 * 2 * 14336 * 2
+    ws = L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64)
+    rc = L.w4a16_fused_moe(None, 0, v, v, 512, 4096, 14336, 8, 2, 1, v, v, v, v, v, v, 128, 64, 1,
+                           v, ws - 1, v)
+    assert rc == P.ERR_INVALID_ARG and "workspace" in L.w4a16_last_error().decode()

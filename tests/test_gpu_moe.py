@@ -1,0 +1,158 @@
+"""GPU parity of the fused-MoE path (route, align, grouped GEMM, silu*mul, combine, whole
+layer) against the CPU oracle. The reference has no MoE kernel; the oracle defines the
+layer by composition of the pinned dense pieces (tests/test_oracle.py::test_moe_*)."""
+import numpy as np
+import pytest
+
+import synth
+from helpers import assert_parity, pkg, to_dev
+
+pytestmark = pytest.mark.gpu
+GPTQ, SYM, AWQ = 0, 1, 2
+FMT_NAME = {GPTQ: "gptq", SYM: "gptq_sym", AWQ: "awq"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def stacked_weights(fmt, E, K, N, G, seed):
+    """Per-expert packed weights stacked along a leading expert dimension. Uniform random
+    32-bit words are uniform nibbles in every slot, so the words are drawn directly."""
+    g = synth.rng(seed)
+    shape = (E, K, N // 8) if fmt == AWQ else (E, K // 8, N)
+    qw = g.integers(0, 2 ** 32, size=shape, dtype=np.uint32).view(np.int32)
+    qz = g.integers(0, 2 ** 32, size=(E, K // G, N // 8), dtype=np.uint32).view(np.int32)
+    sc = g.uniform(0.002, 0.02, size=(E, K // G, N)).astype(np.float32).astype(np.float16)
+    return qw, sc, qz
+
+
+def test_route_matches_oracle(torch_cuda, orc):
+    P = pkg()
+    g = np.random.default_rng(70)
+    for T, E, topk in ((512, 8, 2), (37, 16, 4), (5, 3, 1)):
+        logits = g.standard_normal((T, E)).astype(np.float32)
+        ids, w = P.moe_route(to_dev(logits), topk)
+        ids_ref, w_ref = orc.moe_route(logits, topk)
+        assert np.array_equal(ids.cpu().numpy(), ids_ref)
+        assert np.allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+    # ties go to the lower expert index
+    ids, _ = P.moe_route(to_dev(np.zeros((4, 8), dtype=np.float32)), 2)
+    assert ids.cpu().numpy().tolist() == [[0, 1]] * 4
+
+
+@pytest.mark.parametrize("T,E,topk,bm", [(512, 8, 2, 64), (100, 8, 2, 16), (3000, 16, 4, 128),
+                                         (7, 64, 2, 64)])
+def test_align_matches_oracle(torch_cuda, orc, T, E, topk, bm):
+    P = pkg()
+    g = np.random.default_rng(71 + T)
+    ids, _ = orc.moe_route(g.standard_normal((T, E)).astype(np.float32), topk)
+    sorted_ids, expert_ids, npp = P.moe_align(to_dev(ids), E, bm)
+    s_ref, e_ref, n_ref = orc.moe_align(ids, E, bm)
+    n = int(npp.cpu().numpy()[0])
+    assert n == n_ref
+    assert np.array_equal(sorted_ids.cpu().numpy()[:n], s_ref)
+    assert np.array_equal(expert_ids.cpu().numpy()[: n // bm], e_ref)
+    assert np.all(sorted_ids.cpu().numpy()[n:] == T * topk)
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, AWQ])
+@pytest.mark.parametrize("bm", [64, 128])
+def test_grouped_gemm_matches_per_expert_dense(torch_cuda, orc, fmt, bm):
+    """out[p] = a[p // topk] @ W16[expert of p] for every pair."""
+    P = pkg()
+    T, E, topk, K, N, G = 40, 4, 2, 256, 512, 128
+    g = np.random.default_rng(72)
+    x = synth.rand_x(g, T, K)
+    ids, _ = orc.moe_route(g.standard_normal((T, E)).astype(np.float32), topk)
+    qw, sc, qz = stacked_weights(fmt, E, K, N, G, 73)
+    sorted_ids, expert_ids, npp = P.moe_align(to_dev(ids), E, bm)
+    out = P.moe_gemm(to_dev(x), topk, to_dev(qw), to_dev(sc), to_dev(qz), sorted_ids, expert_ids,
+                     npp, T * topk, N, K, fmt=FMT_NAME[fmt], group_size=G, block_m=bm)
+    torch_cuda.cuda.synchronize()
+    got = out.cpu().numpy()
+    for e in range(E):
+        pairs = np.nonzero(ids.ravel() == e)[0]
+        if pairs.size == 0:
+            continue
+        ref = orc.w4a16_gemm(fmt, np.ascontiguousarray(x[pairs // topk]), qw[e], sc[e], qz[e], K, N,
+                             G, want_f32=True)[1]
+        assert_parity(got[pairs], ref, what=f"expert {e}")
+
+
+def test_silu_mul_reference_entry_point(torch_cuda, orc):
+    torch = torch_cuda
+    P = pkg()
+    g = np.random.default_rng(74)
+    rows, inter = 33, 1024
+    gu = (g.standard_normal((rows, 2 * inter)) * 3).astype(np.float16)
+    out = torch.empty((rows, inter), dtype=torch.float16, device="cuda:0")
+    P.fused_silu_mul_interleaved_f16(to_dev(gu), out, inter, rows * inter)
+    got = out.cpu().numpy().astype(np.float64)
+    ref = orc.silu_mul_f16(gu[:, :inter], gu[:, inter:]).reshape(rows, inter).astype(np.float64)
+    # both round one f32 result to fp16; expf implementations may differ by an f32 ulp, which
+    # moves the fp16 result by at most one fp16 ulp
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got - ref) <= ulp + 1e-7)
+    assert np.mean(got == ref) > 0.99
+
+
+def test_moe_sum(torch_cuda):
+    P = pkg()
+    g = np.random.default_rng(75)
+    T, topk, K = 64, 2, 512
+    yp = g.standard_normal((T * topk, K)).astype(np.float16)
+    w = g.random((T, topk)).astype(np.float32)
+    y = P.moe_sum(to_dev(yp), to_dev(w), T, topk, K).cpu().numpy()
+    ref = (yp.astype(np.float64).reshape(T, topk, K) * w[:, :, None]).sum(1)
+    assert_parity(y, ref, tol=2e-3)
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, AWQ])
+def test_fused_moe_small_vs_oracle(torch_cuda, orc, fmt):
+    P = pkg()
+    T, E, topk, K, I, G = 48, 4, 2, 256, 256, 128
+    g = np.random.default_rng(76)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    w13 = stacked_weights(fmt, E, K, 2 * I, G, 77)
+    w2 = stacked_weights(fmt, E, I, K, G, 78)
+    y = P.fused_moe(to_dev(x), to_dev(logits), tuple(to_dev(a) for a in w13),
+                    tuple(to_dev(a) for a in w2), topk=topk, fmt=FMT_NAME[fmt], group_size=G)
+    torch_cuda.cuda.synchronize()
+    ids, w = orc.moe_route(logits, topk)
+    w13d = [orc.dequant(fmt, w13[0][e], w13[1][e], w13[2][e], K, 2 * I, G) for e in range(E)]
+    w2d = [orc.dequant(fmt, w2[0][e], w2[1][e], w2[2][e], I, K, G) for e in range(E)]
+    ref = orc.moe_forward(x, ids, w, w13d, w2d, inter=I)
+    assert_parity(y.cpu().numpy(), ref.astype(np.float64), what="fused moe")
+
+
+def test_fused_moe_config4_sampled_tokens(torch_cuda, orc):
+    """Config 4 at full size (8 experts, top-2, T=512, K=4096, I=14336, GPTQ int4 G=128);
+    the oracle recomputes 6 sampled tokens through their experts."""
+    P = pkg()
+    T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
+    g = np.random.default_rng(0x5EED0004)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    w13 = stacked_weights(GPTQ, E, K, 2 * I, G, 0x5EED0104)
+    w2 = stacked_weights(GPTQ, E, I, K, G, 0x5EED0204)
+    y = P.fused_moe(to_dev(x), to_dev(logits), tuple(to_dev(a) for a in w13),
+                    tuple(to_dev(a) for a in w2), topk=topk, fmt="gptq", group_size=G)
+    y = y.cpu().numpy()
+    assert np.all(np.isfinite(y))
+    toks = np.array([0, 1, 255, 256, 400, 511])
+    ids, w = orc.moe_route(logits, topk)
+    used = sorted(set(ids[toks].ravel().tolist()))
+    dummy = np.zeros((8, 8), dtype=np.float16)
+    w13d = [orc.dequant(GPTQ, w13[0][e], w13[1][e], w13[2][e], K, 2 * I, G) if e in used else dummy
+            for e in range(E)]
+    w2d = [orc.dequant(GPTQ, w2[0][e], w2[1][e], w2[2][e], I, K, G) if e in used else dummy
+           for e in range(E)]
+    ref = orc.moe_forward(np.ascontiguousarray(x[toks]), np.ascontiguousarray(ids[toks]),
+                          np.ascontiguousarray(w[toks]), w13d, w2d, inter=I)
+    assert_parity(y[toks], ref.astype(np.float64), what="config 4 sampled tokens")

@@ -69,7 +69,9 @@ _ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, Module
 EXPORTED = (
     "w4a16_last_error", "w4a16_version", "w4a16_gemm", "w4a16_gemm_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
-    "dequant_int4_sym_to_fp16", "w4a16_dequant",
+    "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
+    "w4a16_moe_gemm", "fused_silu_mul_interleaved_f16", "w4a16_moe_sum",
+    "w4a16_fused_moe_workspace_size", "w4a16_fused_moe",
     "hiprt_create", "hiprt_destroy", "hiprt_module_load", "hiprt_module_unload", "hiprt_launch",
     "hiprt_stream_create", "hiprt_stream_destroy", "hiprt_stream_synchronize", "hiprt_malloc",
     "hiprt_free", "hiprt_memcpy_htod_async", "hiprt_memcpy_dtoh_async", "hiprt_memset_async",
@@ -98,6 +100,17 @@ def lib() -> ctypes.CDLL:
         L.dequant_int4_to_fp16.argtypes = [_P] * 5 + [_I] * 4
         L.dequant_int4_sym_to_fp16.argtypes = [_P] * 4 + [_I] * 3
         L.w4a16_dequant.argtypes = [_P, _I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.w4a16_moe_route.argtypes = [_P, _P, _I, _I, _I, _I, _P, _P]
+        L.w4a16_moe_align.argtypes = [_P, _P, _I, _I, _I, _I, _P, _P, _P]
+        _L = ctypes.c_int64
+        L.w4a16_moe_gemm.argtypes = [_P, _I, _P, _I, _P, _P, _P, _L, _L, _L, _P, _P, _P, _P,
+                                     _I, _I, _I, _I, _I, _I, _I]
+        L.fused_silu_mul_interleaved_f16.argtypes = [_P, _P, _P, _I, _I]
+        L.w4a16_moe_sum.argtypes = [_P, _P, _P, _P, _I, _I, _I]
+        L.w4a16_fused_moe_workspace_size.restype = ctypes.c_size_t
+        L.w4a16_fused_moe_workspace_size.argtypes = [_I] * 6
+        L.w4a16_fused_moe.argtypes = [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+                                      _P, _I, _I, _I, _P, _Z, _P]
         L.hiprt_create.argtypes = [_I, ctypes.POINTER(_P)]
         L.hiprt_destroy.argtypes = [_P]
         L.hiprt_module_load.argtypes = [_P, _P, _Z, ctypes.POINTER(_P)]
@@ -222,6 +235,90 @@ def dequant(qweight, scales, qzeros, fmt="gptq", K: int | None = None, group_siz
     check(lib().w4a16_dequant(_stream(qweight), f, _ptr(qweight), _ptr(scales), _ptr(qzeros),
                               _ptr(g_idx), _ptr(out), K, N, group_size, zero_offset,
                               int(transposed)))
+    return out
+
+
+# ------------------------------------------------------------------ fused MoE
+
+def moe_route(logits: torch.Tensor, topk: int, renormalize: bool = True):
+    """(topk_ids int32 [T, topk], topk_weights fp32 [T, topk]) from fp32 logits [T, E]."""
+    _require(logits, "logits", (torch.float32,))
+    T, E = logits.shape
+    ids = torch.empty((T, topk), dtype=torch.int32, device=logits.device)
+    w = torch.empty((T, topk), dtype=torch.float32, device=logits.device)
+    check(lib().w4a16_moe_route(_stream(logits), _ptr(logits.contiguous()), T, E, topk,
+                                int(renormalize), _ptr(ids), _ptr(w)))
+    return ids, w
+
+
+def moe_capacity(num_pairs: int, E: int, block_m: int) -> int:
+    cap = num_pairs + E * (block_m - 1)
+    return (cap + block_m - 1) // block_m * block_m
+
+
+def moe_align(topk_ids: torch.Tensor, E: int, block_m: int = 64):
+    """(sorted_ids [capacity], expert_ids [capacity / block_m], num_post_padded [1])."""
+    _require(topk_ids, "topk_ids", _INT32)
+    P = topk_ids.numel()
+    cap = moe_capacity(P, E, block_m)
+    dev = topk_ids.device
+    sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(cap // block_m, dtype=torch.int32, device=dev)
+    npp = torch.empty(1, dtype=torch.int32, device=dev)
+    check(lib().w4a16_moe_align(_stream(topk_ids), _ptr(topk_ids.contiguous()), P, E, block_m,
+                                cap, _ptr(sorted_ids), _ptr(expert_ids), _ptr(npp)))
+    return sorted_ids, expert_ids, npp
+
+
+def moe_gemm(a, a_div, qweight, scales, qzeros, sorted_ids, expert_ids, npp, num_pairs, N, K,
+             fmt="gptq", group_size=128, block_m=64, zero_offset=1, out=None):
+    """Grouped GEMM: out[p] = a[p // a_div] @ W16[expert of p]; weights stacked [E, ...]."""
+    f = _fmt(fmt)
+    if out is None:
+        out = torch.empty((num_pairs, N), dtype=torch.float16, device=a.device)
+    qs = qweight[0].numel()
+    ss = scales[0].numel()
+    zs = 0 if qzeros is None else qzeros[0].numel()
+    check(lib().w4a16_moe_gemm(_stream(a), f, _ptr(a), a_div, _ptr(qweight), _ptr(scales),
+                               _ptr(qzeros), qs, ss, zs, _ptr(sorted_ids), _ptr(expert_ids),
+                               _ptr(npp), _ptr(out), num_pairs, N, K, group_size, block_m,
+                               sorted_ids.numel(), zero_offset))
+    return out
+
+
+def fused_silu_mul_interleaved_f16(gate_up, out, inter, total, stream=None):
+    """elementwise.rs:188-212 parameter list: out[b*inter+i] = silu(g)*u."""
+    st = stream if stream is not None else _stream(gate_up)
+    check(lib().fused_silu_mul_interleaved_f16(st, _p(gate_up), _p(out), inter, total))
+
+
+def moe_sum(y_pairs, topk_weights, T, topk, K, out=None):
+    if out is None:
+        out = torch.empty((T, K), dtype=torch.float16, device=y_pairs.device)
+    check(lib().w4a16_moe_sum(_stream(y_pairs), _ptr(y_pairs), _ptr(topk_weights), _ptr(out), T,
+                              topk, K))
+    return out
+
+
+def fused_moe(x, router_logits, w13, w2, topk=2, fmt="gptq", group_size=128, block_m=64,
+              renormalize=True, zero_offset=1, out=None, workspace=None):
+    """Whole MoE layer through w4a16_fused_moe. w13 / w2 are (qweight, scales, qzeros) stacked
+    over experts; w13 columns [0, I) are w1 (gate) and [I, 2I) w3 (up)."""
+    f = _fmt(fmt)
+    T, K = x.shape
+    E = router_logits.shape[1]
+    q13, s13, z13 = w13
+    q2, s2, z2 = w2
+    I = s2.shape[1] * group_size
+    need = lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, block_m)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty((T, K), dtype=torch.float16, device=x.device)
+    check(lib().w4a16_fused_moe(_stream(x), f, _ptr(x), _ptr(router_logits.contiguous()), T, K, I,
+                                E, topk, int(renormalize), _ptr(q13), _ptr(s13), _ptr(z13),
+                                _ptr(q2), _ptr(s2), _ptr(z2), group_size, block_m, zero_offset,
+                                _ptr(workspace), workspace.numel(), _ptr(out)))
     return out
 
 

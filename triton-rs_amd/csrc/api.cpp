@@ -328,4 +328,181 @@ W4A16_API int w4a16_dequant(void* stream, int fmt, const void* qweight, const vo
                           transposed ? 1 : 0);
 }
 
+// ------------------------------------------------------------------ fused MoE
+
+static int check_moe_dims(int32_t T, int32_t E, int32_t topk) {
+    if (T < 1 || E < 1 || topk < 1 || topk > E)
+        return fail(W4A16_ERR_INVALID_ARG, "bad MoE sizes (T=%d E=%d topk=%d)", T, E, topk);
+    if (E > 256 || topk > 8)
+        return fail(W4A16_ERR_UNSUPPORTED, "MoE supports E <= 256 experts and topk <= 8");
+    return W4A16_OK;
+}
+
+W4A16_API int w4a16_moe_route(void* stream, const float* logits, int32_t T, int32_t E,
+                              int32_t topk, int32_t renormalize, int32_t* topk_ids,
+                              float* topk_weights) {
+    if (!logits || !topk_ids || !topk_weights)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (int rc = check_moe_dims(T, E, topk)) return rc;
+    hipError_t e = launch_moe_route(logits, T, E, topk, renormalize, topk_ids, topk_weights,
+                                    static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "moe route launch");
+}
+
+W4A16_API int w4a16_moe_align(void* stream, const int32_t* topk_ids, int32_t num_pairs, int32_t E,
+                              int32_t block_m, int32_t capacity, int32_t* sorted_ids,
+                              int32_t* expert_ids, int32_t* num_tokens_post_padded) {
+    if (!topk_ids || !sorted_ids || !expert_ids || !num_tokens_post_padded)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (num_pairs < 1 || E < 1 || block_m < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (pairs=%d E=%d block_m=%d)", num_pairs, E,
+                    block_m);
+    if (E > 1024) return fail(W4A16_ERR_UNSUPPORTED, "moe_align supports at most 1024 experts");
+    const int64_t need = (int64_t)num_pairs + (int64_t)E * (block_m - 1);
+    if (capacity < need || capacity % block_m)
+        return fail(W4A16_ERR_INVALID_ARG,
+                    "capacity (%d) must be a multiple of block_m and >= pairs + E*(block_m-1) = %lld",
+                    capacity, (long long)need);
+    hipError_t e = launch_moe_align(topk_ids, num_pairs, E, block_m, capacity, sorted_ids,
+                                    expert_ids, num_tokens_post_padded,
+                                    static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "moe align launch");
+}
+
+W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div,
+                             const void* qweight, const void* scales, const void* qzeros,
+                             int64_t qweight_expert_stride, int64_t scales_expert_stride,
+                             int64_t qzeros_expert_stride, const int32_t* sorted_ids,
+                             const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                             void* out, int32_t num_pairs, int32_t N, int32_t K, int32_t G,
+                             int32_t block_m, int32_t capacity, int32_t zero_offset) {
+    int rc = check_gemm_args(fmt, a, qweight, scales, qzeros, out, 1, N, K, G);
+    if (rc) return rc;
+    if (!sorted_ids || !expert_ids || !num_tokens_post_padded)
+        return fail(W4A16_ERR_INVALID_ARG, "null routing pointer");
+    if (a_div < 1 || num_pairs < 1 || capacity < 1 || capacity % block_m)
+        return fail(W4A16_ERR_INVALID_ARG, "bad grouped-GEMM sizes");
+    if (!moe_gemm_supported(N, K, G, block_m))
+        return fail(W4A16_ERR_UNSUPPORTED,
+                    "grouped GEMM needs N %% 256 == 0, K %% 64 == 0, group_size %% 8 == 0 and "
+                    "block_m in {64, 128} (N=%d K=%d G=%d block_m=%d)", N, K, G, block_m);
+    if (!aligned(a, 16) || !aligned(qweight, 16) || !aligned(scales, 16) || !aligned(out, 16))
+        return fail(W4A16_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+    PrefillParams p{};
+    p.x = static_cast<const half_t*>(a);
+    p.qweight = static_cast<const uint32_t*>(qweight);
+    p.scales = static_cast<const half_t*>(scales);
+    p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+    p.out = static_cast<half_t*>(out);
+    p.M = capacity; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
+    p.sorted_ids = sorted_ids; p.expert_ids = expert_ids;
+    p.num_post_padded = num_tokens_post_padded;
+    p.num_pairs = num_pairs; p.a_div = a_div;
+    p.qweight_stride = qweight_expert_stride; p.scales_stride = scales_expert_stride;
+    p.qzeros_stride = qzeros_expert_stride;
+    hipError_t e = launch_moe_gemm(fmt, p, block_m, capacity / block_m,
+                                   static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "moe gemm launch");
+}
+
+W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, void* out,
+                                             int32_t inter, int32_t total) {
+    if (!gate_up || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (inter < 1 || total < 0 || total % inter)
+        return fail(W4A16_ERR_INVALID_ARG, "total (%d) must be a multiple of inter (%d)", total,
+                    inter);
+    if (inter % 8 || !aligned(gate_up, 16) || !aligned(out, 16))
+        return fail(W4A16_ERR_UNSUPPORTED, "inter must be a multiple of 8 and pointers 16-byte aligned");
+    if (total == 0) return W4A16_OK;
+    hipError_t e = launch_silu_mul(static_cast<const half_t*>(gate_up), static_cast<half_t*>(out),
+                                   inter, total, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "silu_mul launch");
+}
+
+W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk_weights,
+                            void* out, int32_t T, int32_t topk, int32_t K) {
+    if (!y_pairs || !topk_weights || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (T < 1 || topk < 1 || K < 8 || K % 8)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (T=%d topk=%d K=%d)", T, topk, K);
+    hipError_t e = launch_moe_sum(static_cast<const half_t*>(y_pairs), topk_weights,
+                                  static_cast<half_t*>(out), T, topk, K,
+                                  static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "moe sum launch");
+}
+
+namespace {
+struct MoeLayout {
+    size_t ids, weights, sorted, experts, npp, h, a, yp, total;
+    int32_t capacity;
+};
+size_t up256(size_t v) { return (v + 255) / 256 * 256; }
+MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, int32_t block_m) {
+    MoeLayout L{};
+    const int64_t P = (int64_t)T * topk;
+    const int64_t cap = (P + (int64_t)E * (block_m - 1) + block_m - 1) / block_m * block_m;
+    L.capacity = (int32_t)cap;
+    size_t off = 0;
+    L.ids = off; off = up256(off + P * 4);
+    L.weights = off; off = up256(off + P * 4);
+    L.sorted = off; off = up256(off + cap * 4);
+    L.experts = off; off = up256(off + cap / block_m * 4);
+    L.npp = off; off = up256(off + 4);
+    L.h = off; off = up256(off + (size_t)P * 2 * I * 2);
+    L.a = off; off = up256(off + (size_t)P * I * 2);
+    L.yp = off; off = up256(off + (size_t)P * K * 2);
+    L.total = off;
+    return L;
+}
+}  // namespace
+
+W4A16_API size_t w4a16_fused_moe_workspace_size(int32_t T, int32_t E, int32_t topk, int32_t I,
+                                                int32_t K, int32_t block_m) {
+    if (T < 1 || E < 1 || topk < 1 || I < 1 || K < 1 || block_m < 1) return 0;
+    return moe_layout(T, E, topk, I, K, block_m).total;
+}
+
+W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float* router_logits,
+                              int32_t T, int32_t K, int32_t I, int32_t E, int32_t topk,
+                              int32_t renormalize, const void* w13_qweight, const void* w13_scales,
+                              const void* w13_qzeros, const void* w2_qweight,
+                              const void* w2_scales, const void* w2_qzeros, int32_t G,
+                              int32_t block_m, int32_t zero_offset, void* workspace,
+                              size_t workspace_bytes, void* out) {
+    if (!x || !router_logits || !workspace || !out)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (int rc = check_moe_dims(T, E, topk)) return rc;
+    if (I < 1 || K < 1) return fail(W4A16_ERR_INVALID_ARG, "bad sizes (K=%d I=%d)", K, I);
+    const MoeLayout L = moe_layout(T, E, topk, I, K, block_m);
+    if (workspace_bytes < L.total)
+        return fail(W4A16_ERR_INVALID_ARG, "workspace too small (%zu < %zu bytes)", workspace_bytes,
+                    L.total);
+    if (!aligned(workspace, 256)) return fail(W4A16_ERR_INVALID_ARG, "workspace must be 256-byte aligned");
+    char* ws = static_cast<char*>(workspace);
+    auto* ids = reinterpret_cast<int32_t*>(ws + L.ids);
+    auto* wts = reinterpret_cast<float*>(ws + L.weights);
+    auto* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
+    auto* experts = reinterpret_cast<int32_t*>(ws + L.experts);
+    auto* npp = reinterpret_cast<int32_t*>(ws + L.npp);
+    void* h = ws + L.h;
+    void* a = ws + L.a;
+    void* yp = ws + L.yp;
+    const int32_t P = T * topk;
+    int rc = w4a16_moe_route(stream, router_logits, T, E, topk, renormalize, ids, wts);
+    if (!rc) rc = w4a16_moe_align(stream, ids, P, E, block_m, L.capacity, sorted, experts, npp);
+    if (!rc) {
+        const int64_t n13 = 2 * (int64_t)I;
+        rc = w4a16_moe_gemm(stream, fmt, x, topk, w13_qweight, w13_scales, w13_qzeros,
+                            (int64_t)K * n13 / 8, (int64_t)(K / G) * n13, (int64_t)(K / G) * n13 / 8,
+                            sorted, experts, npp, h, P, (int32_t)n13, K, G, block_m, L.capacity,
+                            zero_offset);
+    }
+    if (!rc) rc = fused_silu_mul_interleaved_f16(stream, h, a, I, P * I);
+    if (!rc)
+        rc = w4a16_moe_gemm(stream, fmt, a, 1, w2_qweight, w2_scales, w2_qzeros,
+                            (int64_t)I * K / 8, (int64_t)(I / G) * K, (int64_t)(I / G) * K / 8,
+                            sorted, experts, npp, yp, P, K, I, G, block_m, L.capacity, zero_offset);
+    if (!rc) rc = w4a16_moe_sum(stream, yp, wts, out, T, topk, K);
+    return rc;
+}
+
 }  // extern "C"

@@ -1,0 +1,207 @@
+// Fused-MoE pieces around the grouped W4A16 GEMM (kernels_prefill.hip, grouped mode).
+// The reference has no MoE kernel; the only piece it defines is the activation between the
+// expert GEMMs, fused_silu_mul_interleaved_f16 (crates/triton-kernels/src/elementwise.rs:
+// 188-212), mirrored here with the same parameters and arithmetic. The rest follows the
+// composition the CPU oracle fixes:
+//   route:  softmax over the E logits, top-k (ties -> lower expert), weights renormalised
+//   align:  (token, slot) pairs sorted by expert, stable in pair index p = t * topk + j,
+//           each expert padded to a multiple of block_m with the sentinel P = T * topk
+//   gemm1:  h[p]  = f16(x[p / topk] @ W13[e])          (grouped, N = 2 I)
+//   act:    a[p]  = f16(silu(f32 h[p][:I]) * f32 h[p][I:])
+//   gemm2:  yp[p] = f16(a[p] @ W2[e])                  (grouped, N = K)
+//   sum:    y[t]  = f16(sum_j w[t, j] * f32 yp[t * topk + j])
+#include "device_common.h"
+#include "launch.h"
+
+namespace w4a16 {
+
+// ------------------------------------------------------------------ route
+
+// One thread per token. Top-k is taken on the logits (softmax is monotonic, so the choice
+// is the same and is exact); the weight of a chosen expert is its softmax probability, or,
+// renormalised over the chosen k, exp(l - l_max) / sum over the chosen of exp(l - l_max).
+__global__ void __launch_bounds__(256)
+moe_route_kernel(const float* __restrict__ logits, int T, int E, int topk, int renormalize,
+                 int32_t* __restrict__ ids, float* __restrict__ weights) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= T) return;
+    const float* l = logits + (size_t)t * E;
+    float mx = l[0];
+    for (int e = 1; e < E; ++e) mx = fmaxf(mx, l[e]);
+    float denom = 0.f;
+    for (int e = 0; e < E; ++e) denom += expf(l[e] - mx);
+    uint64_t used[4] = {0, 0, 0, 0};                 // E <= 256
+    float sel_sum = 0.f;
+    for (int j = 0; j < topk; ++j) {
+        int best = -1;
+        float bv = 0.f;
+        for (int e = 0; e < E; ++e) {
+            if ((used[e >> 6] >> (e & 63)) & 1ull) continue;
+            if (best < 0 || l[e] > bv) { best = e; bv = l[e]; }   // strict >: lower index wins ties
+        }
+        used[best >> 6] |= 1ull << (best & 63);
+        const float pe = expf(bv - mx);
+        ids[(size_t)t * topk + j] = best;
+        weights[(size_t)t * topk + j] = pe;
+        sel_sum += pe;
+    }
+    const float inv = 1.0f / (renormalize ? sel_sum : denom);
+    for (int j = 0; j < topk; ++j) weights[(size_t)t * topk + j] *= inv;
+}
+
+hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int renormalize,
+                            int32_t* ids, float* weights, hipStream_t st) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(moe_route_kernel, dim3((T + 255) / 256), dim3(256), 0, st, logits, T, E,
+                       topk, renormalize, ids, weights);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ align
+
+// One workgroup of 1024 threads. Counts per expert, pads, lays the experts out in order and
+// places every pair at start[e] + (number of earlier pairs of the same expert), which keeps
+// the order stable. The rank is built per chunk of 1024 pairs and per expert with wave
+// ballots and a prefix over the 16 waves.
+constexpr int ALIGN_THREADS = 1024;
+constexpr int ALIGN_MAX_E = 1024;
+
+__global__ void __launch_bounds__(ALIGN_THREADS)
+moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int capacity,
+                 int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                 int32_t* __restrict__ num_post_padded) {
+    __shared__ int cnt[ALIGN_MAX_E];
+    __shared__ int start[ALIGN_MAX_E];
+    __shared__ int wave_tot[ALIGN_THREADS / 64];
+    __shared__ int total_sh;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+    for (int e = tid; e < E; e += ALIGN_THREADS) cnt[e] = 0;
+    __syncthreads();
+    for (int p = tid; p < P; p += ALIGN_THREADS) atomicAdd(&cnt[ids[p]], 1);
+    __syncthreads();
+    if (tid == 0) {
+        int acc = 0;
+        for (int e = 0; e < E; ++e) {
+            start[e] = acc;
+            acc += (cnt[e] + block_m - 1) / block_m * block_m;
+        }
+        total_sh = acc;
+        *num_post_padded = acc;
+    }
+    __syncthreads();
+    const int total = total_sh;
+    // sentinel everywhere first, then expert ids per block
+    for (int i = tid; i < capacity; i += ALIGN_THREADS) sorted_ids[i] = P;
+    for (int e = tid; e < E; e += ALIGN_THREADS) {
+        const int b0 = start[e] / block_m;
+        const int nb = (cnt[e] + block_m - 1) / block_m;
+        for (int b = 0; b < nb; ++b) expert_ids[b0 + b] = e;
+        cnt[e] = 0;   // reused below as the running count of placed pairs
+    }
+    for (int b = total / block_m + tid; b < capacity / block_m; b += ALIGN_THREADS)
+        expert_ids[b] = 0;   // blocks past the padded count are never read; keep them valid
+    // the sentinel stores must land before any wave overwrites one of them below
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+
+    for (int c0 = 0; c0 < P; c0 += ALIGN_THREADS) {
+        const int p = c0 + tid;
+        const int mine = p < P ? ids[p] : -1;
+        int rank = 0;
+        for (int e = 0; e < E; ++e) {
+            const uint64_t bal = __ballot(mine == e);
+            if (lane == 0) wave_tot[wave] = __popcll(bal);
+            __syncthreads();
+            if (mine == e) {
+                int before = cnt[e];
+                for (int w = 0; w < wave; ++w) before += wave_tot[w];
+                before += __popcll(bal & ((1ull << lane) - 1ull));
+                rank = before;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                int s = 0;
+                for (int w = 0; w < ALIGN_THREADS / 64; ++w) s += wave_tot[w];
+                cnt[e] += s;
+            }
+            __syncthreads();
+        }
+        if (p < P) sorted_ids[start[mine] + rank] = p;
+    }
+}
+
+hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
+                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
+                            hipStream_t st) {
+    (void)hipGetLastError();
+    if (E > ALIGN_MAX_E) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(ALIGN_THREADS), 0, st, ids, P, E, block_m,
+                       capacity, sorted_ids, expert_ids, num_post_padded);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ activation
+
+// out[b, i] = f16(silu(g) * u), g = gate_up[b, i], u = gate_up[b, inter + i], silu computed
+// in f32 as g / (1 + exp(-g)) (elementwise.rs:188-212). Eight outputs per thread.
+__global__ void __launch_bounds__(256)
+silu_mul_kernel(const half_t* __restrict__ gate_up, half_t* __restrict__ out, int inter,
+                int64_t total) {
+    const int64_t i8 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i8 >= total) return;
+    const int64_t b = i8 / inter, i = i8 - b * inter;
+    const half_t* g = gate_up + b * 2 * inter + i;
+    const half8_t gv = *reinterpret_cast<const half8_t*>(g);
+    const half8_t uv = *reinterpret_cast<const half8_t*>(g + inter);
+    half8_t o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float gf = (float)gv[k];
+        const float s = gf / (1.0f + expf(-gf));
+        o[k] = (half_t)(s * (float)uv[k]);
+    }
+    *reinterpret_cast<half8_t*>(out + i8) = o;
+}
+
+hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
+                           hipStream_t st) {
+    (void)hipGetLastError();
+    const int64_t threads = total / 8;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       gate_up, out, inter, total);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ combine
+
+// y[t, n] = f16(sum_j w[t, j] * f32(yp[t * topk + j, n])), eight columns per thread.
+__global__ void __launch_bounds__(256)
+moe_sum_kernel(const half_t* __restrict__ yp, const float* __restrict__ w, half_t* __restrict__ y,
+               int T, int topk, int K) {
+    const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (idx >= (int64_t)T * K) return;
+    const int t = (int)(idx / K), n = (int)(idx - (int64_t)t * K);
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < topk; ++j) {
+        const float wj = w[(size_t)t * topk + j];
+        const half8_t v = *reinterpret_cast<const half8_t*>(yp + ((size_t)t * topk + j) * K + n);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += wj * (float)v[k];
+    }
+    half8_t o;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k] = (half_t)acc[k];
+    *reinterpret_cast<half8_t*>(y + idx) = o;
+}
+
+hipError_t launch_moe_sum(const half_t* y_pairs, const float* weights, half_t* out, int T,
+                          int topk, int K, hipStream_t st) {
+    (void)hipGetLastError();
+    const int64_t threads = (int64_t)T * K / 8;
+    hipLaunchKernelGGL(moe_sum_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       y_pairs, weights, out, T, topk, K);
+    return hipGetLastError();
+}
+
+}  // namespace w4a16

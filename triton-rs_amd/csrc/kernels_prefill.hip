@@ -36,7 +36,7 @@ __device__ __forceinline__ u32x4 pack8(half2_t a, half2_t b, half2_t c, half2_t 
 __device__ __forceinline__ int bswz(int n, int kc) { return kc ^ ((n >> 3) & 7); }
 }  // namespace
 
-template <int FMT, int BM, int D>
+template <int FMT, int BM, int D, bool MOE>
 __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     constexpr int WM = BM / 2;          // rows per wave
     constexpr int RB = WM / 16;         // row blocks per wave
@@ -54,6 +54,37 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int NW = p.N >> 3;
     const int nstages = p.K / BK;
+
+    // Grouped (fused-MoE) mode: row tile blockIdx.y is one BM-row block of expert-sorted
+    // (token, slot) pairs; its rows are gathered from the activations through sorted_ids and
+    // its results scattered back by pair index; the block's expert selects the weights.
+    if constexpr (MOE) {
+        if (m0 >= *p.num_post_padded) return;      // uniform: past the padded pair count
+        const int e = p.expert_ids[blockIdx.y];
+        p.qweight += (size_t)e * p.qweight_stride;
+        p.scales += (size_t)e * p.scales_stride;
+        if (p.qzeros) p.qzeros += (size_t)e * p.qzeros_stride;
+    }
+    // source row of tile row `row` (or -1: padding / past M)
+    auto src_row = [&](int row) -> int {
+        if constexpr (MOE) {
+            const int pair = p.sorted_ids[m0 + row];
+            return pair < p.num_pairs ? pair / p.a_div : -1;
+        } else {
+            return m0 + row < p.M ? m0 + row : -1;
+        }
+    };
+    auto dst_row = [&](int row) -> int {
+        if constexpr (MOE) {
+            const int pair = p.sorted_ids[m0 + row];
+            return pair < p.num_pairs ? pair : -1;
+        } else {
+            return m0 + row < p.M ? m0 + row : -1;
+        }
+    };
+    int arow[ACH];
+#pragma unroll
+    for (int q = 0; q < ACH; ++q) arow[q] = src_row((t + 256 * q) >> 3);
 
     // ---- per-thread B assignment: 8 columns (one qzeros word) x 8 k
     //   GPTQ: packed row br = t / 32 of the stage, columns 8 * (t % 32) + 0..7
@@ -73,10 +104,12 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
         for (int q = 0; q < ACH; ++q) {
             const int idx = t + 256 * q;
             const int row = idx >> 3, cc = idx & 7;
-            // rows past M are zero (a clamped, branch-free load measured 1.5x slower here)
-            const int m = m0 + row;
-            areg[u][q] = (m < p.M) ? *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + k0 + 8 * cc)
-                                   : u32x4{0u, 0u, 0u, 0u};
+            // rows past M (or padding pairs) are zero (a clamped, branch-free load measured
+            // 1.5x slower here)
+            const int m = arow[q];
+            (void)row;
+            areg[u][q] = (m >= 0) ? *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + k0 + 8 * cc)
+                                  : u32x4{0u, 0u, 0u, 0u};
         }
         int g;
         if constexpr (FMT == FMT_AWQ) {
@@ -222,8 +255,8 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = m0 + wm * WM + 16 * r + 4 * kb + i;
-            if (m >= p.M) continue;
+            const int m = dst_row(wm * WM + 16 * r + 4 * kb + i);
+            if (m < 0) continue;
             half_t* dst = p.out + (size_t)m * p.N + n0 + wn * 128 + j;
 #pragma unroll
             for (int c = 0; c < CB; ++c) dst[16 * c] = (half_t)acc[r][c][i];
@@ -245,33 +278,54 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
     return s;
 }
 
-template <int FMT, int BM>
-static void launch_t(const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
+template <int FMT, int BM, bool MOE>
+static void launch_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t st) {
     // stages of loads in flight: deeper rings do not fit beside the accumulators (they end
     // up in AGPRs and every use pays an AGPR->VGPR copy)
     constexpr int D = 1;
     static bool attr_set = false;   // dynamic LDS above 64 KiB must be allowed once
     if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<FMT, BM, D>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)s.lds);
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<FMT, BM, D, MOE>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         attr_set = true;
     }
-    hipLaunchKernelGGL((prefill_kernel<FMT, BM, D>), dim3(s.col_tiles, s.row_tiles), dim3(256),
-                       s.lds, st, p);
+    hipLaunchKernelGGL((prefill_kernel<FMT, BM, D, MOE>), grid, dim3(256), lds, st, p);
 }
 
-template <int FMT>
-static void launch_fmt(const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
-    if (s.bm == 256) launch_t<FMT, 256>(p, s, st);
-    else launch_t<FMT, 128>(p, s, st);
+template <int FMT, bool MOE>
+static void launch_fmt(const PrefillParams& p, int bm, dim3 grid, size_t lds, hipStream_t st) {
+    if constexpr (MOE) {
+        if (bm == 64) launch_t<FMT, 64, true>(p, grid, lds, st);
+        else launch_t<FMT, 128, true>(p, grid, lds, st);
+    } else {
+        if (bm == 256) launch_t<FMT, 256, false>(p, grid, lds, st);
+        else launch_t<FMT, 128, false>(p, grid, lds, st);
+    }
+}
+
+template <bool MOE>
+static hipError_t launch_any(int fmt, const PrefillParams& p, int bm, dim3 grid, size_t lds,
+                             hipStream_t st) {
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
+    if (fmt == FMT_AWQ) launch_fmt<FMT_AWQ, MOE>(p, bm, grid, lds, st);
+    else if (fmt == FMT_GPTQ) launch_fmt<FMT_GPTQ, MOE>(p, bm, grid, lds, st);
+    else launch_fmt<FMT_GPTQ_SYM, MOE>(p, bm, grid, lds, st);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
-    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
-    if (fmt == FMT_AWQ) launch_fmt<FMT_AWQ>(p, s, st);
-    else if (fmt == FMT_GPTQ) launch_fmt<FMT_GPTQ>(p, s, st);
-    else launch_fmt<FMT_GPTQ_SYM>(p, s, st);
-    return hipGetLastError();
+    return launch_any<false>(fmt, p, s.bm, dim3(s.col_tiles, s.row_tiles), s.lds, st);
+}
+
+bool moe_gemm_supported(int N, int K, int G, int block_m) {
+    return N % BN == 0 && K % BK == 0 && G % 8 == 0 && K % G == 0 &&
+           (block_m == 64 || block_m == 128);
+}
+
+hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
+                           hipStream_t st) {
+    const size_t lds = (size_t)2 * (block_m + BN) * LD * sizeof(half_t);
+    return launch_any<true>(fmt, p, block_m, dim3(p.N / BN, max_blocks), lds, st);
 }
 
 }  // namespace w4a16

@@ -37,6 +37,12 @@ struct PrefillParams {
     const uint32_t* qzeros;
     half_t* out;
     int M, N, K, G, zero_offset;
+    // grouped (fused-MoE) mode only
+    const int32_t* sorted_ids;       // [capacity] pair ids, padding = num_pairs
+    const int32_t* expert_ids;       // [capacity / block_m]
+    const int32_t* num_post_padded;  // device scalar
+    int num_pairs, a_div;            // x row of pair p is p / a_div
+    int64_t qweight_stride, scales_stride, qzeros_stride;   // per expert, in elements
 };
 
 struct PrefillShape {
@@ -47,6 +53,20 @@ struct PrefillShape {
 
 PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus);
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st);
+bool moe_gemm_supported(int N, int K, int G, int block_m);
+hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
+                           hipStream_t st);
+
+// Fused-MoE helpers (kernels_moe.hip).
+hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int renormalize,
+                            int32_t* ids, float* weights, hipStream_t st);
+hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
+                            int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
+                            hipStream_t st);
+hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
+                           hipStream_t st);
+hipError_t launch_moe_sum(const half_t* y_pairs, const float* weights, half_t* out, int T,
+                          int topk, int K, hipStream_t st);
 
 // Small-batch MFMA GEMM (5 <= M <= 64): waves split K inside a workgroup.
 struct SkinnyParams {
