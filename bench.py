@@ -1,24 +1,36 @@
 """Benchmark of the MI355X W4A16 path (one JSON line on stdout).
 
-Headline (BASELINE.json metric, config 1): AWQ int4 GEMV, M=1, K=4096 -> N=14336, G=128,
+Headline (the metric's M=1 case, config 1): AWQ int4 GEMV, M=1, K=4096 -> N=14336, G=128,
 weights rotated over enough distinct buffers (> 512 MB) that the 256 MB Infinity Cache
 cannot hold them; one step = one w4a16_gemm call through the C ABI. Launches are
 replayed from HIP graphs of GRAPH_CALLS calls each so that host launch cost does not
 gate the GPU. `value` is algorithmic GB/s (bytes of qweight + scales + qzeros + x + out,
 each counted once) over the timed region, measured with HIP events on the launch stream.
 
-Secondary (same line, "prefill"): AWQ M=2048, K=4096 -> N=14336 TFLOP/s (2*M*N*K).
+roofline.traffic: HBM bytes per launch of the headline kernel from two rocprofv3 --pmc
+passes (FETCH_SIZE, then WRITE_SIZE) over a child run of this script (--pmc-child), each
+divided by the ratio that the same counter reads for a plain streaming kernel of known
+size (torch's neg over 512 MiB of int32) in the same child run.
+
+Secondary figures (same line, "extra"): AWQ prefill M=2048 in both MLP shapes (TFLOP/s,
+2*M*N*K), the other decode/small-batch shapes, and the fused MoE layer of config 4.
 cpu_baseline: the CPU oracle (dequant + fp32-accumulate matmul, OpenMP) on a bounded
 sample of the same workload, timed on this host's cores.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import platform
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
+import zlib
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -26,6 +38,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP16_DENSE_PEAK_TFLOPS = 2516.6  # MI355X fp16 dense MFMA
 GRAPH_CALLS = 100
+PMC_WARM, PMC_MEASURED = 20, 40
+COPY_ELEMS = 128 * 1024 * 1024   # int32 elements streamed by the calibration kernel (512 MiB)
+
+HEADLINE = ("awq", 1, 4096, 14336, 128)
 
 
 def algorithmic_bytes(fmt: str, M: int, K: int, N: int, G: int) -> int:
@@ -49,13 +65,13 @@ def make_weight_sets(torch, fmt, K, N, G, count, dev, seed):
     return sets
 
 
-def time_graphs(torch, pkg, x, sets, out, fmt, G, steps, warmup, stream):
+def time_graphs(torch, pkg, x, sets, out, fmt, G, steps, warmup, stream, g_idx=None):
     """Capture GRAPH_CALLS calls (rotating weight sets) per graph; replay to cover `steps`."""
     n_sets = len(sets)
     with torch.cuda.stream(stream):
         for i in range(max(warmup, n_sets)):
             qw, sc, qz = sets[i % n_sets]
-            pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, out=out)
+            pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, g_idx=g_idx, out=out)
     stream.synchronize()
     graphs = []
     n_graphs = max(1, min(n_sets, 10))
@@ -64,7 +80,7 @@ def time_graphs(torch, pkg, x, sets, out, fmt, G, steps, warmup, stream):
         with torch.cuda.graph(g, stream=stream):
             for j in range(GRAPH_CALLS):
                 qw, sc, qz = sets[(gi * GRAPH_CALLS + j) % n_sets]
-                pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, out=out)
+                pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, g_idx=g_idx, out=out)
         graphs.append(g)
     reps = max(1, steps // GRAPH_CALLS)
     with torch.cuda.stream(stream):
@@ -84,19 +100,17 @@ def time_graphs(torch, pkg, x, sets, out, fmt, G, steps, warmup, stream):
     return ms / (reps * GRAPH_CALLS), reps * GRAPH_CALLS, wall
 
 
-def time_direct(torch, pkg, x, sets, out, fmt, G, calls, stream):
-    n_sets = len(sets)
+def time_direct(torch, fn, calls, stream, warm=3):
+    """Average ms of fn() launched `calls` times on `stream` (HIP events on that stream)."""
     with torch.cuda.stream(stream):
-        for i in range(n_sets):
-            qw, sc, qz = sets[i]
-            pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, out=out)
+        for i in range(warm):
+            fn(i)
     torch.cuda.synchronize()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         start.record(stream)
         for i in range(calls):
-            qw, sc, qz = sets[i % n_sets]
-            pkg.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, out=out)
+            fn(i)
         stop.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / calls
@@ -121,6 +135,10 @@ def cpu_baseline(fmt_id, x, qw, sc, qz, M, K, N, G, budget_s=15.0):
     return med, len(times), oracle.num_threads()
 
 
+def progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -132,6 +150,156 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+# ----------------------------------------------------------------------------- traffic
+
+def pmc_child(args) -> int:
+    """Workload profiled by the counter passes: PMC_WARM + PMC_MEASURED headline launches
+    over the rotated weight sets, then three launches of the calibration kernel."""
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    fmt, M, K, N, G = HEADLINE
+    sets = make_weight_sets(torch, fmt, K, N, G, args.sets, dev, seed=0x5EED0001)
+    x = torch.randn((M, K), device=dev).half()
+    out = torch.empty((M, N), dtype=torch.float16, device=dev)
+    for i in range(PMC_WARM + PMC_MEASURED):
+        pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G, out=out)
+    torch.cuda.synchronize()
+    del sets
+    src = torch.ones(COPY_ELEMS, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    print("pmc child done", flush=True)
+    return 0
+
+
+def _counter_means(csv_dir, counter):
+    """Per-dispatch mean of `counter` for the headline kernel (last PMC_MEASURED dispatches)
+    and for the calibration kernel."""
+    files = glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True)
+    ours, copy = [], []
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] != counter:
+                    continue
+                name = r["Kernel_Name"]
+                key = (int(r["Dispatch_Id"]), float(r["Counter_Value"]))
+                if "w4a16::" in name:
+                    ours.append(key)
+                elif "neg_kernel" in name:
+                    copy.append(key)
+    ours.sort()
+    ours = [v for _, v in ours[-PMC_MEASURED:]]
+    copy = [v for _, v in copy]
+    if not ours or not copy:
+        raise RuntimeError(f"{counter}: no samples (ours {len(ours)}, copy {len(copy)})")
+    return sum(ours) / len(ours), sum(copy) / len(copy)
+
+
+def measure_traffic(args):
+    """HBM bytes per headline launch from two rocprofv3 --pmc passes, calibrated."""
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(rocprof):
+        return None, {"traffic_note": "rocprofv3 not found"}
+    env = dict(os.environ, TMPDIR="/tmp")
+    outdir = tempfile.mkdtemp(prefix="w4a16_pmc_", dir="/tmp")
+    detail = {}
+    copy_bytes = COPY_ELEMS * 4
+    total = 0.0
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = os.path.join(outdir, counter)
+        cmd = ["timeout", "-s", "KILL", "90", rocprof, "--pmc", counter, "--output-format", "csv",
+               "-d", d, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__),
+               "--pmc-child", "--sets", str(args.sets)]
+        r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+        if r.returncode != 0:
+            tail = (r.stdout + r.stderr).strip().splitlines()[-3:]
+            return None, {"traffic_note": f"{counter} pass failed rc={r.returncode}: {tail}"}
+        ours_kib, copy_kib = _counter_means(d, counter)
+        factor = copy_kib * 1024.0 / copy_bytes
+        total += ours_kib * 1024.0 / factor
+        detail[counter] = {"headline_KiB_per_dispatch": round(ours_kib, 1),
+                           "copy_KiB_per_dispatch": round(copy_kib, 1),
+                           "calibration_factor": round(factor, 4)}
+    shutil.rmtree(outdir, ignore_errors=True)
+    return int(total), {"traffic_counters": detail,
+                        "traffic_calibration": f"torch.neg over {copy_bytes >> 20} MiB int32 "
+                                               f"(reads and writes {copy_bytes >> 20} MiB)"}
+
+
+# ----------------------------------------------------------------------------- extras
+
+def extras(torch, pkg, dev, stream, args):
+    """Secondary shapes: the other configs at the sizes the metric names."""
+    res = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0x5EED0003)
+
+    def gemm_case(tag, fmt, M, K, N, G, n_sets, calls, g_idx=None):
+        sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        if M <= 64:
+            ms = time_graphs(torch, pkg, x, sets, out, fmt, G, calls, 10, stream, g_idx=g_idx)[0]
+        else:
+            ms = time_direct(torch, lambda i: pkg.gemm(x, *sets[i % n_sets], fmt=fmt, group_size=G,
+                                                       g_idx=g_idx, out=out), calls, stream)
+        nbytes = algorithmic_bytes(fmt, M, K, N, G)
+        tfl = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+        res[tag] = {"kernel": pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None),
+                    "us_per_call": round(ms * 1e3, 2),
+                    "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "TFLOPs": round(tfl, 2),
+                    "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                    "frac_mfma": round(tfl / FP16_DENSE_PEAK_TFLOPS, 4)}
+        progress(f"{tag}: {res[tag]['us_per_call']} us")
+        del sets
+
+    gemm_case("c0_gptq_sym_m1_k4096_n4096", "gptq_sym", 1, 4096, 4096, 128, 60, 1000)
+    for M in (4, 8):
+        gemm_case(f"c1_awq_m{M}_k4096_n14336", "awq", M, 4096, 14336, 128, 20, 1000)
+    gemm_case("c1_awq_m1_k14336_n4096", "awq", 1, 14336, 4096, 128, 20, 1000)
+    gemm_case("c1_awq_m8_k14336_n4096", "awq", 8, 14336, 4096, 128, 20, 1000)
+    perm = torch.randperm(4096, generator=torch.Generator().manual_seed(2))
+    g_idx = (torch.arange(4096) // 128)[perm].to(torch.int32).to(dev)
+    for M in (16, 64):
+        gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 20, 500,
+                  g_idx=g_idx)
+        gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 20, 500)
+    gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 10)
+    gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 10)
+
+    # config 4: fused MoE layer, T=512, 8 experts, top-2, K=4096, I=14336, GPTQ G=128
+    T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
+
+    def words(*shape):
+        return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+
+    def scales(*shape):
+        return (torch.rand(shape, device=dev, generator=gen) * 0.018 + 0.002).half()
+
+    w13 = (words(E, K // 8, 2 * I), scales(E, K // G, 2 * I), words(E, K // G, 2 * I // 8))
+    w2 = (words(E, I // 8, K), scales(E, I // G, K), words(E, I // G, K // 8))
+    x = torch.randn((T, K), device=dev, generator=gen).half()
+    logits = torch.randn((T, E), device=dev, generator=gen)
+    out = torch.empty((T, K), dtype=torch.float16, device=dev)
+    flops = 2.0 * T * topk * (K * 2 * I + I * K)
+    for bm in (64, 128):
+        ws = torch.empty(pkg.lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, bm),
+                         dtype=torch.uint8, device=dev)
+        ms = time_direct(torch, lambda i: pkg.fused_moe(x, logits, w13, w2, topk=topk, block_m=bm,
+                                                        out=out, workspace=ws), 10, stream)
+        res[f"c4_fused_moe_block_m{bm}"] = {
+            "ms_per_layer": round(ms, 3), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+            "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
+        progress(f"fused moe block_m={bm}: {ms:.3f} ms")
+        del ws
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -139,23 +307,35 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--sets", type=int, default=20, help="distinct weight buffers rotated")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
+    ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the kernel runs on one GPU's share; see DESIGN.md on sharding)", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path; the kernels "
+              "run on one GPU's share of a sharded layer", file=sys.stderr)
         return 2
+    if args.pmc_child:
+        return pmc_child(args)
 
-    import numpy as np
+    # counter passes run first, in child processes, before this process touches the GPU
+    traffic, traffic_detail = (None, {"traffic_note": "skipped (--no-traffic)"})
+    if not args.no_traffic:
+        try:
+            traffic, traffic_detail = measure_traffic(args)
+            progress(f"counter passes done: traffic={traffic}")
+        except (RuntimeError, OSError, KeyError, ValueError) as e:
+            traffic, traffic_detail = None, {"traffic_note": f"counter pass unusable: {e}"}
+
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
-    fmt, M, K, N, G = "awq", 1, 4096, 14336, 128
+    fmt, M, K, N, G = HEADLINE
     sets = make_weight_sets(torch, fmt, K, N, G, args.sets, dev, seed=0x5EED0001)
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x5EED0001)
@@ -165,11 +345,13 @@ def main() -> int:
     kernel = pkg.plan(fmt, M, N, K, G)
 
     ms, calls, wall = time_graphs(torch, pkg, x, sets, out, fmt, G, args.steps, args.warmup, stream)
-    ms_direct = time_direct(torch, pkg, x, sets, out, fmt, G, min(args.steps, 1000), stream)
+    ms_direct = time_direct(torch, lambda i: pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G,
+                                                      out=out), min(args.steps, 1000), stream)
     # warm single buffer (Infinity-Cache resident), reported separately
     ms_warm = time_graphs(torch, pkg, x, sets[:1], out, fmt, G, 1000, 50, stream)[0]
     nbytes = algorithmic_bytes(fmt, M, K, N, G)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    progress(f"headline: {ms * 1e3:.2f} us/call, {gbs:.1f} GB/s")
 
     result = {
         "metric": "W4A16 GEMM GB/s (M=1) and TFLOP/s (M=2048), % of MI355X roofline",
@@ -184,45 +366,28 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (seeded torch RNG on device: uniform int4 nibbles, scales U[0.002,0.02], x~N(0,1))",
-        "config": {"workload": f"AWQ int4 GEMV M={M} K={K} N={N} group_size={G} (BASELINE config 1)",
+        "config": {"workload": f"AWQ int4 GEMV M={M} K={K} N={N} group_size={G} (config 1, M=1)",
                    "kernel": kernel, "weight_sets_rotated": len(sets),
                    "rotated_footprint_MB": round(len(sets) * nbytes / 1e6, 1),
-                   "timing": f"HIP events around graph replays of {GRAPH_CALLS} calls"},
+                   "timing": f"HIP events on the launch stream around graph replays of "
+                             f"{GRAPH_CALLS} calls"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": nbytes},
-        "extra": {"direct_launch_ms_per_call": ms_direct,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": nbytes, **traffic_detail},
+        "extra": {"direct_launch_us_per_call": round(ms_direct * 1e3, 2),
                   "direct_launch_GBps": round(nbytes / (ms_direct * 1e-3) / 1e9, 1),
-                  "warm_single_buffer_ms": ms_warm,
+                  "warm_single_buffer_us": round(ms_warm * 1e3, 2),
                   "warm_single_buffer_GBps": round(nbytes / (ms_warm * 1e-3) / 1e9, 1),
                   "timed_wall_s": round(wall, 3)},
     }
-
-    if not args.no_prefill:
-        Mp = 2048
-        psets = sets[:2]
-        xp = torch.randn((Mp, K), device=dev, generator=gen).half()
-        outp = torch.empty((Mp, N), dtype=torch.float16, device=dev)
-        with torch.cuda.stream(stream):
-            pkg.gemm(xp, *psets[0], fmt=fmt, group_size=G, out=outp)
-        torch.cuda.synchronize()
-        reps = 10
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        with torch.cuda.stream(stream):
-            start.record(stream)
-            for i in range(reps):
-                pkg.gemm(xp, *psets[i % 2], fmt=fmt, group_size=G, out=outp)
-            stop.record(stream)
-        torch.cuda.synchronize()
-        pms = start.elapsed_time(stop) / reps
-        tflops = 2.0 * Mp * N * K / (pms * 1e-3) / 1e12
-        result["prefill"] = {"workload": f"AWQ M={Mp} K={K} N={N} G={G} (BASELINE config 3)",
-                             "kernel": pkg.plan(fmt, Mp, N, K, G), "ms_per_call": pms,
-                             "TFLOPs": round(tflops, 2), "peak_TFLOPs": FP16_DENSE_PEAK_TFLOPS,
-                             "frac": round(tflops / FP16_DENSE_PEAK_TFLOPS, 4)}
+    if not args.no_extra:
+        del sets
+        torch.cuda.empty_cache()
+        result["extra"].update(extras(torch, pkg, dev, stream, args))
 
     if not args.no_cpu_baseline:
-        qw, sc, qz = (t.cpu().numpy() for t in sets[0])
+        qw, sc, qz = (t.cpu().numpy() for t in make_weight_sets(torch, fmt, K, N, G, 1, dev,
+                                                                 seed=0x5EED0001)[0])
         xh = x.cpu().numpy()
         med, n, threads = cpu_baseline(2, xh, qw, sc, qz, M, K, N, G, args.cpu_budget)
         result["cpu_baseline"] = {
