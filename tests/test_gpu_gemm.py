@@ -158,9 +158,56 @@ def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N, G):
 
 def test_act_order_gidx(torch_cuda, orc):
     p = Problem(GPTQ, M=16, K=1024, N=384, G=128, seed=1300, act_order=True)
-    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) in ("strided", "skinny")
+    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) == "skinny"
     y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
     assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what="act-order")
+
+
+@pytest.mark.parametrize("M", [16, 32, 64])
+def test_act_order_config2_full_size(torch_cuda, orc, M):
+    """Config 2 at full size: GPTQ act-order, K=4096, N=6144 (fused QKV), G=128."""
+    p = Problem(GPTQ, M=M, K=4096, N=6144, G=128, seed=0x5EED0002 + M, act_order=True)
+    assert pkg().plan("gptq", M, p.N, p.K, p.G, has_g_idx=True) == "skinny"
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"config 2 M={M}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N,G,zo", [(SYM, 8, 2048, 512, 128, 1), (GPTQ, 1, 1024, 256, 64, 0),
+                                            (GPTQ, 40, 1408, 640, 128, 1), (GPTQ, 5, 512, 64, 32, 1)])
+def test_act_order_shapes(torch_cuda, orc, fmt, M, K, N, G, zo):
+    """Act-order over formats, zero offsets, group sizes, strip widths and split counts."""
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1310 + M, act_order=True, zero_offset=zo)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, G, has_g_idx=True) == "skinny"
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"act-order fmt={fmt} M={M}")
+
+
+def test_act_order_identity_gidx_equals_plain(torch_cuda):
+    """g_idx[k] = k / G must give exactly the same output as no g_idx (same kernel, same
+    per-weight arithmetic and accumulation order)."""
+    p = Problem(GPTQ, M=16, K=2048, N=512, G=128, seed=1320)
+    plain = _run_gemm(torch_cuda, p)
+    ident = _run_gemm(torch_cuda, p, g_idx=(np.arange(p.K) // p.G).astype(np.int32))
+    assert np.array_equal(plain, ident)
+
+
+def test_act_order_large_m_uses_strided(torch_cuda, orc):
+    p = Problem(GPTQ, M=100, K=512, N=256, G=128, seed=1330, act_order=True)
+    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) == "strided"
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what="act-order strided")
+
+
+def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc):
+    """The device cannot report a bad g_idx without a host round trip; entries outside
+    [0, K/G) are clamped into the scale table (the oracle, which rejects them, is given the
+    clamped index)."""
+    p = Problem(GPTQ, M=16, K=1024, N=256, G=128, seed=1340, act_order=True)
+    bad = p.g_idx.copy()
+    bad[3], bad[700] = 99, -5
+    y = _run_gemm(torch_cuda, p, g_idx=bad)
+    ref = _oracle(orc, p, g_idx=np.clip(bad, 0, p.K // p.G - 1).astype(np.int32))
+    assert_parity(y, ref, what="clamped g_idx")
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, AWQ])

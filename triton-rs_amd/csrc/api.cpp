@@ -118,7 +118,8 @@ static int device_cus() {
 }
 
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
-    if (has_gidx) return W4A16_KERNEL_STRIDED;
+    if (has_gidx)
+        return skinny_shape(fmt, M, N, K, G, cus, true).ok ? W4A16_KERNEL_SKINNY : W4A16_KERNEL_STRIDED;
     if (gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
     if (M <= 64 && skinny_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_SKINNY;
     if (prefill_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
@@ -151,14 +152,16 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool vec_ok = aligned(x, 16) && aligned(qweight, 16) && aligned(scales, 16) &&
-                        aligned(out, 16) && (!qzeros || aligned(qzeros, 16));
+                        aligned(out, 16) && (!qzeros || aligned(qzeros, 16)) &&
+                        (!g_idx || aligned(g_idx, 16));
     const int cus = device_cus();
     int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
 
     if (kernel == W4A16_KERNEL_SKINNY) {
-        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus);
+        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr);
         SkinnyParams p{};
+        p.g_idx = g_idx;
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
         p.scales = static_cast<const half_t*>(scales);

@@ -15,6 +15,12 @@
 // Operand layouts: slot j of MFMA c is output column
 // n0 + CPL*j + c; GPTQ k-blocks are consumed in the unpack order (k0,k4)(k1,k5)(k2,k6)(k3,k7)
 // with A permuted to match, AWQ in natural order via row pairs.
+//
+// Act-order (GIDX, GPTQ formats): the group of row k is g_idx[k] instead of k / G, so the
+// scale and zero change from row to row. The workgroup first builds an LDS table holding,
+// for every group and every column of its strip, the scale and the zero (as fp16 1024 + z)
+// in one 32-bit entry; each k row then gathers its entries by g_idx[k]. The arithmetic per
+// weight is unchanged, (fp16(1024 + q) - fp16(1024 + z)) * s, so the weights stay bit-exact.
 #include "device_common.h"
 #include "launch.h"
 #include "splitk.h"
@@ -28,8 +34,9 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }
 }  // namespace
 
-template <int FMT, int BM, int CPL, int PF>
+template <int FMT, int BM, int CPL, int PF, bool GIDX>
 __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
+    static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     constexpr int RB = BM / 16;
     constexpr int WN = 16 * CPL;
     constexpr int WPS = (FMT == FMT_AWQ) ? 8 : CPL;   // packed words per lane per k32 step
@@ -37,6 +44,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
 
     __shared__ float red[4][BM][WN + 1];
     __shared__ int flag;
+    extern __shared__ uint32_t gtab[];   // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16)
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kb = lane >> 4;
@@ -51,6 +59,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
     uint32_t bw[PF][WPS];
     u32x4 areg[PF][RB];
     uint32_t sreg[PF][SW], zreg[PF];
+    int32_t greg[PF][GIDX ? 8 : 1];
 
     auto issue = [&](int u, int step) {
         const int kg = 32 * step;
@@ -82,6 +91,14 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
             areg[u][r] = (m < p.M) ? *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + kg + 8 * kb)
                                    : u32x4{0u, 0u, 0u, 0u};
         }
+        if constexpr (GIDX) {
+            // groups of the lane's 8 k rows
+            const u32x4* gp = reinterpret_cast<const u32x4*>(p.g_idx + kg + 8 * kb);
+            const u32x4 g0 = gp[0], g1 = gp[1];
+            greg[u][0] = g0.x; greg[u][1] = g0.y; greg[u][2] = g0.z; greg[u][3] = g0.w;
+            greg[u][4] = g1.x; greg[u][5] = g1.y; greg[u][6] = g1.z; greg[u][7] = g1.w;
+            return;
+        }
         // scales and zero word of the lane's columns for this step's group
         const int g = kg / p.G;
         const uint32_t* sp = reinterpret_cast<const uint32_t*>(p.scales + (size_t)g * p.N + nl);
@@ -107,6 +124,19 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
     for (int u = 0; u < PF; ++u)
         if (u < spw) issue(u, step0 + u);
 
+    const int ngroups = (p.K + p.G - 1) / p.G;
+    if constexpr (GIDX) {
+        for (int o = threadIdx.x; o < ngroups * WN; o += 256) {
+            const int g = o / WN, n = n0 + (o - g * WN);
+            const uint32_t sc = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
+            const int z = (FMT == FMT_GPTQ_SYM)
+                              ? 8 : nib(p.qzeros[(size_t)g * NW + (n >> 3)], n & 7) + p.zero_offset;
+            const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
+            gtab[o] = sc | (zf << 16);
+        }
+        __syncthreads();
+    }
+
     for (int s0 = 0; s0 < spw; s0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
@@ -115,7 +145,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
             // zero point (as fp16 1024 + z) and scale per column, splatted
             half2_t hz[CPL], hs[CPL];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) {
+            for (int c = 0; c < (GIDX ? 0 : CPL); ++c) {
                 const int cw = (nl & 7) + c;   // column within its qzeros word
                 int z;
                 if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
@@ -155,6 +185,39 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
                 }
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+            } else if constexpr (GIDX) {
+                // entries of rows k0..k7 for the lane's columns; a g_idx outside the table
+                // is clamped into [0, groups - 1], as in the generic kernel
+                uint32_t t[8][CPL];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t g = (uint32_t)min(max(greg[u][i], 0), ngroups - 1);
+                    const uint32_t* row = gtab + g * WN + CPL * j;
+                    if constexpr (CPL == 2) {
+                        const u32x2 v = *reinterpret_cast<const u32x2*>(row);
+                        t[i][0] = v.x; t[i][1] = v.y;
+                    } else {
+#pragma unroll
+                        for (int h = 0; h < CPL / 4; ++h) {
+                            const u32x4 v = *reinterpret_cast<const u32x4*>(row + 4 * h);
+                            t[i][4 * h + 0] = v.x; t[i][4 * h + 1] = v.y;
+                            t[i][4 * h + 2] = v.z; t[i][4 * h + 3] = v.w;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    const uint32_t w = bw[u][c];
+                    half2_t pr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        // the pair holds rows k_q (low half) and k_{q+4} (high half)
+                        const half2_t s2 = as_h2(perm(t[q + 4][c], t[q][c], 0x05040100u));
+                        const half2_t z2 = as_h2(perm(t[q + 4][c], t[q][c], 0x07060302u));
+                        pr[q] = deq2(nib_pair(w >> (4 * q)), z2, s2);
+                    }
+                    bf[c] = cat8(pr[0], pr[1], pr[2], pr[3]);
+                }
             } else {
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
@@ -203,9 +266,11 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
 
 // ------------------------------------------------------------------ host side
 
-SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus) {
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx) {
     SkinnyShape s{};
-    if (M < 1 || M > 64 || K % 128 || G % 32 || K % G) return s;
+    if (M < 1 || M > 64 || K % 128) return s;
+    // without g_idx a k32 step lies in one group; with it the group comes from the table
+    if (gidx ? (fmt == FMT_AWQ || G < 1) : (G % 32 || K % G)) return s;
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     const bool awq = fmt == FMT_AWQ;
     // narrowest strip (most workgroups) the format supports; wide strips at BM=64 would
@@ -217,6 +282,10 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus) {
         if (N % (16 * c) == 0) { cpl = c; break; }
     }
     if (!cpl) return s;
+    if (gidx) {
+        s.lds = (size_t)((K + G - 1) / G) * 16 * cpl * sizeof(uint32_t);
+        if (s.lds > SKINNY_GIDX_MAX_LDS) return s;
+    }
     s.cpl = cpl;
     s.col_tiles = N / (16 * cpl);
     // split K across workgroups until ~2 workgroups per CU, keeping the fp32 partials
@@ -232,38 +301,50 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus) {
 }
 
 template <int FMT, int BM, int CPL>
-static void launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+static hipError_t launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     constexpr int PF = (FMT == FMT_AWQ || CPL >= 8) ? 3 : 4;
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF>), dim3(s.col_tiles, s.splits), dim3(256), 0,
-                       st, p);
+    if constexpr (FMT != FMT_AWQ) {
+        if (p.g_idx) {
+            // static reduction buffer plus the group table may exceed the default 64 KiB
+            static const hipError_t attr = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
+            if (attr != hipSuccess) return attr;
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true>), dim3(s.col_tiles, s.splits),
+                               dim3(256), s.lds, st, p);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false>), dim3(s.col_tiles, s.splits),
+                       dim3(256), 0, st, p);
+    return hipGetLastError();
 }
 
 template <int FMT, int BM>
-static void launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+static hipError_t launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (FMT != FMT_AWQ) {
-        if (s.cpl == 2) { launch_t<FMT, BM, 2>(p, s, st); return; }
+        if (s.cpl == 2) return launch_t<FMT, BM, 2>(p, s, st);
     }
     if constexpr (BM < 64) {
-        if (s.cpl == 8) { launch_t<FMT, BM, 8>(p, s, st); return; }
+        if (s.cpl == 8) return launch_t<FMT, BM, 8>(p, s, st);
     }
-    launch_t<FMT, BM, 4>(p, s, st);
+    return launch_t<FMT, BM, 4>(p, s, st);
 }
 
 template <int FMT>
-static void launch_fmt(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+static hipError_t launch_fmt(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     switch (s.bm) {
-        case 16: launch_bm<FMT, 16>(p, s, st); break;
-        case 32: launch_bm<FMT, 32>(p, s, st); break;
-        default: launch_bm<FMT, 64>(p, s, st); break;
+        case 16: return launch_bm<FMT, 16>(p, s, st);
+        case 32: return launch_bm<FMT, 32>(p, s, st);
+        default: return launch_bm<FMT, 64>(p, s, st);
     }
 }
 
 hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
-    if (fmt == FMT_AWQ) launch_fmt<FMT_AWQ>(p, s, st);
-    else if (fmt == FMT_GPTQ) launch_fmt<FMT_GPTQ>(p, s, st);
-    else launch_fmt<FMT_GPTQ_SYM>(p, s, st);
-    return hipGetLastError();
+    if (fmt == FMT_AWQ) return launch_fmt<FMT_AWQ>(p, s, st);
+    if (fmt == FMT_GPTQ) return launch_fmt<FMT_GPTQ>(p, s, st);
+    return launch_fmt<FMT_GPTQ_SYM>(p, s, st);
 }
 
 }  // namespace w4a16

@@ -77,15 +77,20 @@ struct SkinnyParams {
     half_t* out;
     float* ws;
     uint32_t* flags;
+    const int32_t* g_idx;   // act-order groups [K], or null
     int M, N, K, G, zero_offset, splits, steps_per_wave;
 };
 
 struct SkinnyShape {
     bool ok;
     int bm, cpl, col_tiles, splits, steps_per_wave;
+    size_t lds;             // dynamic LDS bytes (act-order group table)
 };
 
-SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus);
+// Largest act-order group table a workgroup stages in LDS.
+constexpr size_t SKINNY_GIDX_MAX_LDS = 64 * 1024;
+
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx = false);
 hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st);
 
 // Generic strided GEMM with the reference kernels' parameter list
