@@ -74,8 +74,8 @@ W4A16_API const char* w4a16_version(void);
 /* out[M, N] = x[M, K] @ W16[K, N], W16 = RNE_f16((q - z) * scale[g, n]) with
  * g = g_idx ? g_idx[k] : k / group_size; fp32 accumulation; fp16 output.
  * Contiguous row-major tensors. qzeros is ignored (may be NULL) for GPTQ_SYM. g_idx
- * (int32 [K], values in [0, K/group_size)) is optional and, in the reference, absent:
- * it adds GPTQ act-order. Requirements: M, N, K, group_size >= 1; K % group_size == 0;
+ * (int32 [K], values in [0, K/group_size); values outside are clamped into it) is optional
+ * and, in the reference, absent: it adds GPTQ act-order. Requirements: M, N, K, group_size >= 1; K % group_size == 0;
  * N % 8 == 0; K % 8 == 0 for GPTQ formats. The kernel is chosen by shape (see
  * w4a16_gemm_plan). The decode kernels use a per-(device, stream) split-K workspace
  * that the library allocates on first use of a size and keeps; concurrent calls on
@@ -132,7 +132,7 @@ W4A16_API int w4a16_dequant(void* stream, int fmt, const void* qweight, const vo
                             int transposed);
 
 /* ------------------------------------------------------------------ fused MoE
- * Not in the reference (it has no MoE kernel; SURVEY/BASELINE config 4 asks for one). The
+ * Not in the reference (it has no MoE kernel; the benchmark's Mixtral-like layer needs one). The
  * pieces compose as: route -> align -> grouped GEMM (w1|w3) -> silu*mul -> grouped GEMM (w2)
  * -> weighted sum. Pairs are (token t, slot j) with index p = t * topk + j, P = T * topk. */
 

@@ -12,7 +12,7 @@ if ROOT not in sys.path:
 
 import __graft_entry__  # noqa: E402
 
-RTOL = 1e-2  # max relative error 1e-2 vs fp32 dequant-then-matmul
+RTOL = 1e-2  # the path's bar: max relative error 1e-2 vs fp32 dequant-then-matmul
 
 
 def pkg():

@@ -4,7 +4,7 @@ Packing is written here independently of any unpacking code (it goes from
 integer nibbles to packed int32 words), so the oracle's and the HIP kernels'
 unpackers can be checked against it.
 
-Value distributions follow BASELINE.json's configs: x ~ N(0,1) in fp16, nibbles
+Value distributions follow the benchmark configs: x ~ N(0,1) in fp16, nibbles
 uniform in 0..15, scales uniform in [0.002, 0.02] rounded to fp16, g_idx a seeded
 permutation of repeat(0..K/G-1, G). Seeds are 0x5EED0000 + config index.
 """
@@ -15,7 +15,7 @@ import numpy as np
 SEED_BASE = 0x5EED0000
 
 # AWQ pack order: slot i of a word holds column AWQ_PACK_ORDER[i] of its 8-column group
-# Reading column n back therefore uses slot AWQ_UNPACK_SLOT[n],
+# (the AWQ benchmark config). Reading column n back therefore uses slot AWQ_UNPACK_SLOT[n],
 # the inverse permutation [0,4,1,5,2,6,3,7]
 # (crates/triton-dsl/examples/awq_gemm_int4_typed.rs:26-31).
 AWQ_PACK_ORDER = (0, 2, 4, 6, 1, 3, 5, 7)
@@ -65,7 +65,7 @@ def rand_nibbles(g: np.random.Generator, shape) -> np.ndarray:
 
 
 def act_order_gidx(g: np.random.Generator, K: int, G: int) -> np.ndarray:
-    """Seeded permutation of repeat(0..K/G-1, G)."""
+    """Seeded permutation of repeat(0..K/G-1, G) (the act-order benchmark config)."""
     base = np.repeat(np.arange(K // G, dtype=np.int32), G)
     return g.permutation(base).astype(np.int32)
 

@@ -1,6 +1,6 @@
 """GPU parity: the HIP W4A16 kernels, called through the C ABI, against the CPU oracle.
 
-Bar (BASELINE.json north star): dequantised weights bit-exact; GEMM outputs within max
+Bar: dequantised weights bit-exact; GEMM outputs within max
 relative error 1e-2 (helpers.rel_err: |y - ref| / max(|ref|, rms(ref))) of the oracle's
 float64-accumulated dequant-then-matmul on identical seeded inputs.
 """
