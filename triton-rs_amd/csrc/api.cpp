@@ -43,7 +43,7 @@ struct Workspace {
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-constexpr size_t COUNTER_BYTES = 256 * 1024;  // room for 65536 (tile, split) flags
+constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES;  // room for SPLITK_MAX_PAIRS flags
 
 static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
     int dev = 0;
@@ -118,10 +118,16 @@ static int device_cus() {
 }
 
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
-    if (has_gidx)
-        return skinny_shape(fmt, M, N, K, G, cus, true).ok ? W4A16_KERNEL_SKINNY : W4A16_KERNEL_STRIDED;
-    if (gemv_shape(fmt, M, N, K, G).ok) return W4A16_KERNEL_GEMV;
-    if (M <= 64 && skinny_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_SKINNY;
+    if (has_gidx) {
+        const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus, true);
+        return sk.ok && (size_t)sk.col_tiles * sk.splits <= SPLITK_MAX_PAIRS ? W4A16_KERNEL_SKINNY
+                                                                          : W4A16_KERNEL_STRIDED;
+    }
+    const GemvShape gv = gemv_shape(fmt, M, N, K, G);
+    if (gv.ok && (size_t)gv.col_tiles * gv.splits <= SPLITK_MAX_PAIRS) return W4A16_KERNEL_GEMV;
+    const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);
+    if (M <= 64 && sk.ok && (size_t)sk.col_tiles * sk.splits <= SPLITK_MAX_PAIRS)
+        return W4A16_KERNEL_SKINNY;
     if (prefill_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
     return W4A16_KERNEL_STRIDED;
 }
@@ -170,7 +176,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.splits = s.splits; p.steps_per_wave = s.steps_per_wave;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
+            if ((size_t)s.col_tiles * s.splits > SPLITK_MAX_PAIRS)
                 return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K flag area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.flags, &p.ws);
             if (rc) return rc;
@@ -204,7 +210,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset; p.splits = s.splits;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.splits * sizeof(uint32_t) > COUNTER_BYTES)
+            if ((size_t)s.col_tiles * s.splits > SPLITK_MAX_PAIRS)
                 return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K flag area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;

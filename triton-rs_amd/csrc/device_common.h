@@ -34,19 +34,30 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
     return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
-// (a & mask) | bits in one v_and_or_b32. Written as inline asm with all operands in VGPRs:
-// left to itself the compiler emits v_and_b32 + v_or_b32, because a VOP3 instruction on
-// this target cannot encode the two literal constants.
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+// A constant in a VGPR that the compiler cannot see through. (a & mask) | bits with both
+// constants given this way is selected as one v_and_or_b32 (a VOP3 instruction on this
+// target cannot encode two literals, so with literals the compiler emits v_and + v_or).
+// Being an ordinary instruction, it is covered by the compiler's hazard handling: an
+// inline-asm v_and_or_b32 is not, and its result read by an MFMA one instruction later is
+// read stale. The asm has no side effects, so identical copies are merged and hoisted.
+__device__ __forceinline__ uint32_t vconst(uint32_t c) {
     uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(mask), "v"(bits));
+    asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(c));
     return r;
 }
 
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t mask, uint32_t bits) {
+    return (a & mask) | bits;
+}
+
 // fp16 pair (1024 + nibble at bit 0, 1024 + nibble at bit 16) from v
-__device__ __forceinline__ half2_t nib_pair(uint32_t v) { return as_h2(and_or(v, 0x000F000Fu, MAGIC2)); }
+__device__ __forceinline__ half2_t nib_pair(uint32_t v) {
+    return as_h2(and_or(v, vconst(0x000F000Fu), vconst(MAGIC2)));
+}
 // same for the nibbles at bits 4 and 20, left in place: (1024 + 16 q_lo, 1024 + 16 q_hi)
-__device__ __forceinline__ half2_t nib_pair16(uint32_t v) { return as_h2(and_or(v, 0x00F000F0u, MAGIC2)); }
+__device__ __forceinline__ half2_t nib_pair16(uint32_t v) {
+    return as_h2(and_or(v, vconst(0x00F000F0u), vconst(MAGIC2)));
+}
 
 // fp32 += a.x*b.x + a.y*b.y  (v_dot2c_f32_f16: f16 x f16 products, f32 accumulate)
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {

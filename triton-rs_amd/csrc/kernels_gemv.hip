@@ -161,7 +161,7 @@ gemv_awq_kernel(GemvParams p) {
         else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = p.counters + (size_t)ct * p.splits;
+    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
     if (splitk_arrive(flags, split, p.splits, &flag))
         splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
 }
@@ -292,7 +292,7 @@ gemv_gptq_kernel(GemvParams p) {
         else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = p.counters + (size_t)ct * p.splits;
+    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
     if (splitk_arrive(flags, split, p.splits, &flag))
         splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
 }

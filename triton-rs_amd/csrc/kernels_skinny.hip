@@ -259,7 +259,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         else st_coherent(p.ws + (size_t)split * p.M * p.N + off, v);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = p.flags + (size_t)ct * p.splits;
+    uint32_t* flags = splitk_flags(p.flags, ct, p.splits);
     if (splitk_arrive(flags, split, p.splits, &flag))
         splitk_finish_rows(p.ws, p.out, flags, p.splits, p.M, p.N, 0, p.M, n0, WN);
 }

@@ -10,6 +10,12 @@ typedef _Float16 half_t;
 
 constexpr int GEMV_MAX_M = 4;
 
+// Split-K flag area: one 32-bit flag per (tile, split), FLAG_STRIDE words apart (a
+// 256-byte line each), in the first SPLITK_FLAG_BYTES of a per-stream workspace.
+constexpr int FLAG_STRIDE = 64;
+constexpr size_t SPLITK_FLAG_BYTES = 2u << 20;
+constexpr size_t SPLITK_MAX_PAIRS = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
+
 struct GemvParams {
     const half_t* x;          // [M, K] contiguous
     const uint32_t* qweight;  // GPTQ [K/8, N] | AWQ [K, N/8]
