@@ -55,6 +55,8 @@ def _gemm(P, **over):
     (dict(G=0), "sizes must be positive"),
     (dict(fmt=7), "unknown weight format"),
     (dict(fmt=0, K=4100, G=4100), "multiple of 8 for GPTQ"),
+    (dict(fmt=0, zo=-1), "gptq_zero_offset"),
+    (dict(fmt=0, zo=17), "gptq_zero_offset"),
 ])
 def test_gemm_argument_errors_before_any_hip_call(over, needle):
     P = pkg()

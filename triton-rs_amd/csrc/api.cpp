@@ -96,6 +96,15 @@ static int check_gemm_args(int fmt, const void* x, const void* qweight, const vo
     return W4A16_OK;
 }
 
+// GPTQ zero point = nibble + zero_offset: 1 for the reference's GEMM, 0 for its dequant
+// kernel. The kernels form fp16(1024 + zero) exactly for zeros up to 1023; the accepted
+// range is kept to what a packed format can mean.
+static int check_zero_offset(int fmt, int32_t zero_offset) {
+    if (fmt == W4A16_FMT_GPTQ && (zero_offset < 0 || zero_offset > 16))
+        return fail(W4A16_ERR_INVALID_ARG, "gptq_zero_offset %d outside [0, 16]", zero_offset);
+    return W4A16_OK;
+}
+
 constexpr int DEFAULT_CUS = 256;  // MI355X
 
 // Compute units of the current device (cached per device; 256 when it cannot be queried).
@@ -155,6 +164,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
                          const void* scales, const void* qzeros, const int32_t* g_idx, void* out,
                          int32_t M, int32_t N, int32_t K, int32_t G, int32_t zero_offset) {
     int rc = check_gemm_args(fmt, x, qweight, scales, qzeros, out, M, N, K, G);
+    if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const bool vec_ok = aligned(x, 16) && aligned(qweight, 16) && aligned(scales, 16) &&
@@ -296,6 +306,7 @@ static int dequant_common(void* stream, int fmt, const void* qweight, const void
                           const void* qzeros, const int32_t* g_idx, void* out, int32_t K,
                           int32_t N, int32_t G, int32_t zero_offset, int transposed) {
     int rc = check_gemm_args(fmt, (void*)1, qweight, scales, qzeros, out, 1, N, K, G);
+    if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
     if (fmt == W4A16_FMT_AWQ && !aligned(out, 16) && !transposed)
         return fail(W4A16_ERR_INVALID_ARG, "out must be 16-byte aligned");
@@ -386,6 +397,7 @@ W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div
                              void* out, int32_t num_pairs, int32_t N, int32_t K, int32_t G,
                              int32_t block_m, int32_t capacity, int32_t zero_offset) {
     int rc = check_gemm_args(fmt, a, qweight, scales, qzeros, out, 1, N, K, G);
+    if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
     if (!sorted_ids || !expert_ids || !num_tokens_post_padded)
         return fail(W4A16_ERR_INVALID_ARG, "null routing pointer");

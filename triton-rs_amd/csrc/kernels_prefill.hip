@@ -263,19 +263,439 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
         }
 }
 
+// ------------------------------------------------------------------ pipelined variant
+//
+// Same tile work as prefill_kernel with the memory latency taken off the MFMA stream. All
+// global traffic goes straight to LDS with buffer_load ... lds (no registers held across
+// stages):
+//  * A (activations) into two LDS slots, one stage ahead. Rows past M (or padding pairs)
+//    get an offset past the buffer's end, which the buffer unit returns as zero.
+//  * the packed words, scales and zeros of B into a three-slot LDS ring, three stages
+//    ahead; each stage dequantises the next stage's B from that ring into one of two fp16
+//    B tiles.
+// Per stage the loads are issued A first, B second, and the stage ends waiting with a vmcnt
+// that leaves only the B loads just issued in flight: A(s+1) and everything older is in LDS
+// at the barrier, B gets two stages of latency. One stage is 64 k.
+//
+// LDS rows carry no padding. A: chunk kc of row r at slot kc ^ fa(r), fa(r) = (r & 7) ^
+// ((r >> 3) & 1), which depends on r % 16 only (fixed operand offsets per row block) and
+// keeps 16-row reads conflict-free. B: slot kc ^ fb(n), fb(n) = (n ^ (n >> 3)) & 7, which
+// also spreads the dequant writes (lanes 8 columns apart). A is staged in natural k order
+// (GPTQ's unpack order is undone on the B side with v_perm_b32).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+
+namespace {
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    return i32x4_t{__builtin_amdgcn_readfirstlane((int)(uint32_t)a),
+                   __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xFFFFu)),
+                   __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// LDS byte address of a pointer into the kernel's dynamic LDS
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>(
+        (__attribute__((address_space(3))) const char*)(p));
+}
+
+// buffer_load_dwordx4 ... lds: 16 bytes per lane from rsrc + voffset into LDS at M0 (the
+// wave's base) + lane * 16. Issued from asm so that the compiler, which cannot tell the ring
+// slots apart, does not wait for every LDS load before each LDS read; the kernel counts these
+// loads itself (vmcnt). s_nop: one wait state between the M0 write and its use. "memory":
+// the compiler must not move LDS accesses across it or assume the LDS unchanged.
+__device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds_wave_base, uint32_t voffset) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds_wave_base));
+    uint32_t saved;
+    // M0 is reserved to the compiler: saved and restored around the load
+    asm volatile(
+        "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\ts_nop 0\n\t"
+        "buffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(base), "v"(voffset), "s"(rsrc)
+        : "memory");
+}
+
+__device__ __forceinline__ int fa(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int fb(int n) { return (n ^ (n >> 3)) & 7; }
+
+// s_waitcnt vmcnt(n) leaving lgkmcnt and expcnt alone (gfx9 encoding: vmcnt in [3:0] and
+// [15:14])
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr uint32_t DMA_OOB = 0x80000000u;   // voffset of a zero (past any buffer)
+// One raw ring slot: packed words of a stage (64 k x 256 columns, 8 KB), then 1 KB for the
+// group's scales (256 halfs) and 1 KB for its zeros (32 words). Every LDS load instruction
+// writes all 64 lanes (lanes out of range write zeros), so each gets a 1 KB region of its own.
+constexpr int RAW_W = 8 * 1024;
+constexpr int RAW_S = 1024;
+constexpr int RAW_ST = RAW_W + 2 * 1024;
+}  // namespace
+
+// The B tiles are always 256 columns wide: with BN = 224 the lanes past the tile dequantise
+// into columns nobody reads instead of branching around the work.
+size_t prefill_dma_lds(int bm, int bn) {
+    (void)bn;
+    return (size_t)2 * bm * BK * 2 + (size_t)2 * BN * BK * 2 + (size_t)3 * RAW_ST;
+}
+
+// WGM x WGN waves: 2 x 2 (one wave per SIMD, wave tile (BM/2) x (BN/2)) or 4 x 2 (two per
+// SIMD, wave tile (BM/4) x (BN/2), so that one wave's dequantisation runs while the other's
+// MFMAs do). NT = 64 WGM WGN threads.
+template <int FMT, int BM, int BN, int WGM, bool MOE>
+__global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams p) {
+    constexpr int WGN = 2, NT = 64 * WGM * WGN, NWV = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
+    constexpr int RB = WM / 16, CB = WN / 16;
+    constexpr int A_ST = BM * BK, B_ST = 256 * BK;  // halfs per stage (B: 256 columns)
+    constexpr int ADMA = BM * 8 / NT;               // A chunks per thread per stage
+    constexpr int WDMA = 8 / NWV;                   // 1 KB blocks of raw words per wave
+    constexpr int BWC = BN / 8;                     // 8-column groups of the tile
+    // dequantisation unit per thread: AWQ: word column bi, DR consecutive rows;
+    // GPTQ: packed row br, DC consecutive columns
+    constexpr int DR = 8 * 256 / NT;                // 8 or 4
+    constexpr int DC = 8 * 256 / NT;
+    static_assert(BWC <= 32 && WN % 16 == 0 && ADMA >= 1 && WDMA >= 1, "tile shape");
+
+    extern __shared__ __attribute__((aligned(16))) half_t lds[];
+    half_t* As = lds;                                          // [2][BM][64]
+    half_t* Bs = lds + 2 * A_ST;                               // [2][256][64]
+    char* Raw = reinterpret_cast<char*>(lds + 2 * A_ST + 2 * B_ST);   // [3][RAW_ST]
+
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int j = lane & 15, kb = lane >> 4;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int NW = p.N >> 3;
+    const int ns = p.K / BK;
+
+    if constexpr (MOE) {
+        if (m0 >= *p.num_post_padded) return;
+        const int e = p.expert_ids[blockIdx.y];
+        p.qweight += (size_t)e * p.qweight_stride;
+        p.scales += (size_t)e * p.scales_stride;
+        if (p.qzeros) p.qzeros += (size_t)e * p.qzeros_stride;
+    }
+    auto src_row = [&](int row) -> int {
+        if constexpr (MOE) {
+            const int pair = p.sorted_ids[m0 + row];
+            return pair < p.num_pairs ? pair / p.a_div : -1;
+        } else {
+            return m0 + row < p.M ? m0 + row : -1;
+        }
+    };
+    auto dst_row = [&](int row) -> int {
+        if constexpr (MOE) {
+            const int pair = p.sorted_ids[m0 + row];
+            return pair < p.num_pairs ? pair : -1;
+        } else {
+            return m0 + row < p.M ? m0 + row : -1;
+        }
+    };
+
+    // ---- A: chunk (q, wave, lane) of a stage is LDS row idx / 8, slot idx % 8
+    const int a_rows = MOE ? (p.num_pairs + p.a_div - 1) / p.a_div : p.M;
+    const i32x4_t ars = buffer_rsrc(p.x, (uint32_t)a_rows * (uint32_t)p.K * 2u);
+    uint32_t aoff[ADMA];
+#pragma unroll
+    for (int q = 0; q < ADMA; ++q) {
+        const int idx = (q * NWV + wave) * 64 + lane;
+        const int row = idx >> 3, slot = idx & 7;
+        const int m = src_row(row);
+        aoff[q] = m >= 0 ? ((uint32_t)m * (uint32_t)p.K + 8u * (uint32_t)(slot ^ fa(row))) * 2u
+                         : DMA_OOB;
+    }
+    auto dma_a = [&](int slot, int s) {
+        half_t* dst = As + slot * A_ST;
+#pragma unroll
+        for (int q = 0; q < ADMA; ++q)
+            dma16(ars, dst + (q * NWV + wave) * 64 * 8, aoff[q] + (uint32_t)s * (BK * 2));
+    };
+
+    // ---- B raw: words of a stage as [64 rows][32 words] (AWQ) or [8 packed rows][256
+    // words] (GPTQ) in eight 1 KB blocks; scales by wave 0, zeros by the other waves
+    // (identical bytes to one place: a harmless race that keeps the stage free of branches)
+    const i32x4_t wrs = buffer_rsrc(p.qweight, (uint32_t)((size_t)p.K * p.N / 2));
+    const i32x4_t srs = buffer_rsrc(p.scales, (uint32_t)((size_t)(p.K / p.G) * p.N * 2));
+    const i32x4_t zrs = buffer_rsrc(p.qzeros ? (const void*)p.qzeros : (const void*)p.scales,
+                                    p.qzeros ? (uint32_t)((size_t)(p.K / p.G) * NW * 4) : 0u);
+    uint32_t woff[WDMA];
+#pragma unroll
+    for (int h = 0; h < WDMA; ++h) {
+        const int blk = WDMA * wave + h;
+        if constexpr (FMT == FMT_AWQ) {
+            const int row = blk * 8 + (lane >> 3), chunk = lane & 7;   // 4 words per lane
+            woff[h] = 4 * chunk < BWC
+                          ? ((uint32_t)row * (uint32_t)NW + (uint32_t)(n0 >> 3) + 4u * chunk) * 4u
+                          : DMA_OOB;
+        } else {
+            const int prow = blk, chunk = lane;                         // packed row blk
+            woff[h] = 4 * chunk < BN
+                          ? ((uint32_t)prow * (uint32_t)p.N + (uint32_t)n0 + 4u * chunk) * 4u
+                          : DMA_OOB;
+        }
+    }
+    const bool zw_wave = FMT != FMT_GPTQ_SYM && wave != 0;
+    const i32x4_t szrs = zw_wave ? zrs : srs;
+    const uint32_t szoff = zw_wave ? (lane * 4 < BWC ? ((uint32_t)(n0 >> 3) + 4u * lane) * 4u : DMA_OOB)
+                                   : (lane < BWC ? ((uint32_t)n0 + 8u * lane) * 2u : DMA_OOB);
+    const uint32_t szrow = zw_wave ? (uint32_t)NW * 4u : (uint32_t)p.N * 2u;   // bytes per group
+    const int szdst = RAW_W + (zw_wave ? RAW_S : 0);
+    auto dma_b = [&](int slot, int s) {
+        char* dst = Raw + slot * RAW_ST;
+        const int k0 = s * BK, g = k0 / p.G;
+        const uint32_t wstep = (FMT == FMT_AWQ) ? (uint32_t)k0 * (uint32_t)NW * 4u
+                                                : (uint32_t)(k0 >> 3) * (uint32_t)p.N * 4u;
+        dma16(szrs, dst + szdst, szoff + (uint32_t)g * szrow);
+#pragma unroll
+        for (int h = 0; h < WDMA; ++h) dma16(wrs, dst + (WDMA * wave + h) * 1024, woff[h] + wstep);
+    };
+
+    // ---- dequantisation into the fp16 B tile [256][64] (columns past BN are never read)
+    auto dequant_b = [&](int slot, int buf) {
+        const char* src = Raw + slot * RAW_ST;
+        half_t* B = Bs + buf * B_ST;
+        if constexpr (FMT == FMT_AWQ) {
+            const int bi = t & 31, br = t >> 5;          // word column, DR-row group
+            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src) + DR * br * 32 + bi;
+            uint32_t bw[DR];
+#pragma unroll
+            for (int r = 0; r < DR; ++r) bw[r] = wp[32 * r];
+            const u32x4 sv = *reinterpret_cast<const u32x4*>(src + RAW_W + 16 * bi);
+            const uint32_t zw = *reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S + 4 * bi);
+            half2_t hz[8], hs[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const uint32_t zb = 0x6400u + (uint32_t)nib(zw, awq_slot(c));
+                hz[c] = as_h2(zb | (zb << 16));
+                hs[c] = as_h2(perm(sv[c >> 1], sv[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
+            }
+            half2_t pr[DR / 2][8];
+#pragma unroll
+            for (int rp = 0; rp < DR / 2; ++rp) {
+                const uint32_t a = bw[2 * rp], b = bw[2 * rp + 1];
+                const uint32_t p0 = perm(b, a, 0x05040100u);
+                const uint32_t p1 = perm(b, a, 0x07060302u);
+#pragma unroll
+                for (int sl = 0; sl < 8; ++sl) {
+                    const uint32_t src2 = sl < 4 ? p0 : p1;
+                    const int c = awq_col_of_slot(sl);
+                    pr[rp][c] = deq2(nib_pair(src2 >> (4 * (sl & 3))), hz[c], hs[c]);
+                }
+            }
+            // rows DR br .. DR br + DR - 1: chunk DR br / 8, offset DR br % 8 halfs in it
+            const int kc = (DR * br) >> 3, ko = (DR * br) & 7;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const int n = 8 * bi + c;
+                half_t* dst = B + n * BK + 8 * (kc ^ fb(n)) + ko;
+                if constexpr (DR == 8)
+                    *reinterpret_cast<u32x4*>(dst) = pack8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+                else
+                    *reinterpret_cast<u32x2*>(dst) = u32x2{as_u32(pr[0][c]), as_u32(pr[1][c])};
+            }
+        } else {
+            const int bi = t % (256 / DC), br = t / (256 / DC);   // column group, packed row
+            const u32x4* wp = reinterpret_cast<const u32x4*>(src + br * 1024 + 4 * DC * bi);
+            uint32_t bw[DC];
+#pragma unroll
+            for (int h = 0; h < DC / 4; ++h) {
+                const u32x4 v = wp[h];
+                bw[4 * h + 0] = v.x; bw[4 * h + 1] = v.y; bw[4 * h + 2] = v.z; bw[4 * h + 3] = v.w;
+            }
+            const half_t* sp = reinterpret_cast<const half_t*>(src + RAW_W) + DC * bi;
+            uint32_t sw[DC / 2];
+#pragma unroll
+            for (int h = 0; h < DC / 2; ++h) sw[h] = reinterpret_cast<const uint32_t*>(sp)[h];
+            const uint32_t zw = (FMT == FMT_GPTQ_SYM)
+                                    ? 0u
+                                    : *reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S +
+                                                                         4 * ((DC * bi) >> 3));
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                const int n = DC * bi + c;
+                uint32_t z;
+                if constexpr (FMT == FMT_GPTQ_SYM) z = 8u;
+                else z = (uint32_t)(nib(zw, n & 7) + p.zero_offset);
+                const uint32_t zb = 0x6400u + z;
+                const half2_t hz = as_h2(zb | (zb << 16));
+                const half2_t hs = as_h2(perm(sw[c >> 1], sw[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
+                const uint32_t w = bw[c];
+                const uint32_t q0 = as_u32(deq2(nib_pair(w), hz, hs));         // k0, k4
+                const uint32_t q1 = as_u32(deq2(nib_pair(w >> 4), hz, hs));    // k1, k5
+                const uint32_t q2 = as_u32(deq2(nib_pair(w >> 8), hz, hs));    // k2, k6
+                const uint32_t q3 = as_u32(deq2(nib_pair(w >> 12), hz, hs));   // k3, k7
+                *reinterpret_cast<u32x4*>(B + n * BK + 8 * (br ^ fb(n))) =
+                    u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
+                          perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
+            }
+        }
+    };
+
+    float4_t acc[RB][CB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int c = 0; c < CB; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int a_slot, int buf) {
+        const half_t* A = As + a_slot * A_ST + (wm * WM + j) * BK;
+        const half_t* B = Bs + buf * B_ST;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            const int kc = 4 * ks + kb;
+            half8_t af[RB], bf[CB];
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+                af[r] = *reinterpret_cast<const half8_t*>(A + 16 * r * BK + 8 * (kc ^ fa(j)));
+#pragma unroll
+            for (int c = 0; c < CB; ++c) {
+                const int n = wn * WN + 16 * c + j;
+                bf[c] = *reinterpret_cast<const half8_t*>(B + n * BK + 8 * (kc ^ fb(n)));
+            }
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int c = 0; c < CB; ++c)
+                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[r], bf[c], acc[r][c], 0, 0, 0);
+        }
+    };
+
+    // ---- prologue: raw B of stages 0, 1, 2 and A(0) in flight; dequantise B(0)
+    dma_b(0, 0);
+    dma_b(1, min(1, ns - 1));
+    dma_b(2, min(2, ns - 1));
+    dma_a(0, 0);
+    wait_vmcnt<0>();
+    __syncthreads();
+    dequant_b(0, 0);
+    __syncthreads();
+
+    // ---- stage s: issue A(s+1), then raw B(s+3) into the ring slot B(s) vacated; MFMAs
+    // of stage s and the dequantisation of B(s+1); wait for all but the raw word loads just
+    // issued; barrier. Indices past the end are clamped (their loads land in slots nobody
+    // reads any more).
+    for (int s = 0; s < ns; ++s) {
+        const int rs = s % 3;
+        dma_a((s + 1) & 1, min(s + 1, ns - 1));
+        dma_b(rs, min(s + 3, ns - 1));
+        compute(s & 1, s & 1);
+        dequant_b(rs == 2 ? 0 : rs + 1, (s + 1) & 1);
+        wait_vmcnt<WDMA>();
+        __syncthreads();
+    }
+    wait_vmcnt<0>();   // no LDS write may be in flight when the workgroup ends
+
+    // ---- epilogue: lane holds D[4 kb + i][j] of each 16 x 16 block
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = dst_row(wm * WM + 16 * r + 4 * kb + i);
+            if (m < 0) continue;
+            half_t* dst = p.out + (size_t)m * p.N + n0 + wn * WN + j;
+#pragma unroll
+            for (int c = 0; c < CB; ++c) dst[16 * c] = (half_t)acc[r][c][i];
+        }
+}
+
 // ------------------------------------------------------------------ host side
+
+// The pipelined kernel addresses its buffers with 32-bit byte offsets and marks zero rows
+// with offsets from 2^31 up, so every buffer it reads must stay below 2 GiB.
+static bool dma_ok(int N, int K, int G, long long a_rows) {
+    const long long lim = 1ll << 31;
+    return G % BK == 0 && K % G == 0 && (long long)K * N / 2 < lim && a_rows * K * 2 < lim &&
+           (long long)(K / G) * N * 2 < lim;
+}
 
 PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
     PrefillShape s{};
-    if (M < 1 || N % BN || K % BK || G % 8 || K % G) return s;
+    (void)fmt;
+    if (M < 1 || N % 8 || K % BK || G % 8 || K % G) return s;
+    if (dma_ok(N, K, G, M)) {
+        // tile minimising (rounds of tiles over the CUs) x (tile area); ties to larger BM
+        long long best = -1;
+        for (int bn : {256, 224}) {
+            if (N % bn) continue;
+            for (int bm : {256, 128}) {
+                const long long tiles = (long long)(N / bn) * ((M + bm - 1) / bm);
+                const long long cost = (tiles + num_cus - 1) / num_cus * bm * bn;
+                if (best < 0 || cost < best) {
+                    best = cost; s.bm = bm; s.bn = bn;
+                }
+            }
+        }
+        if (best >= 0) {
+            s.dma = true;
+            s.col_tiles = N / s.bn;
+            s.row_tiles = (M + s.bm - 1) / s.bm;
+            s.lds = prefill_dma_lds(s.bm, s.bn);
+            s.ok = true;
+            return s;
+        }
+    }
+    if (N % BN) return s;
     const int col_tiles = N / BN;
     // 256-row tiles when they still give every CU a workgroup, else 128
     s.bm = ((M + 255) / 256) * col_tiles >= num_cus ? 256 : 128;
+    s.bn = BN;
     s.col_tiles = col_tiles;
     s.row_tiles = (M + s.bm - 1) / s.bm;
     s.lds = (size_t)2 * (s.bm + BN) * LD * sizeof(half_t);
     s.ok = true;
     return s;
+}
+
+template <typename F>
+static void allow_lds(F* kernel, size_t lds) {
+    // dynamic LDS above 64 KiB must be allowed once per kernel
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+}
+
+// waves per workgroup along M (x 2 along N): 4 gives two waves per SIMD, so that one wave's
+// dequantisation VALU runs while the other's MFMAs do (one wave does not overlap the two)
+constexpr int PF_WGM = 4;
+
+template <int FMT, int BM, int BN2, bool MOE>
+static void launch_dma_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t st) {
+    constexpr int WGM = (BM / PF_WGM >= 16) ? PF_WGM : 2;
+    static bool attr_set = false;
+    if (!attr_set) {
+        allow_lds(&prefill_dma_kernel<FMT, BM, BN2, WGM, MOE>, prefill_dma_lds(BM, BN2));
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, WGM, MOE>), grid, dim3(128 * WGM), lds,
+                       st, p);
+}
+
+template <int FMT, bool MOE>
+static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, size_t lds,
+                           hipStream_t st) {
+    if constexpr (MOE) {
+        if (bm == 64) launch_dma_t<FMT, 64, 256, true>(p, grid, lds, st);
+        else launch_dma_t<FMT, 128, 256, true>(p, grid, lds, st);
+    } else {
+        if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false>(p, grid, lds, st);
+        else if (bm == 256) launch_dma_t<FMT, 256, 256, false>(p, grid, lds, st);
+        else if (bn == 224) launch_dma_t<FMT, 128, 224, false>(p, grid, lds, st);
+        else launch_dma_t<FMT, 128, 256, false>(p, grid, lds, st);
+    }
+}
+
+template <bool MOE>
+static hipError_t launch_dma_any(int fmt, const PrefillParams& p, int bm, int bn, dim3 grid,
+                                 size_t lds, hipStream_t st) {
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
+    if (fmt == FMT_AWQ) launch_dma_fmt<FMT_AWQ, MOE>(p, bm, bn, grid, lds, st);
+    else if (fmt == FMT_GPTQ) launch_dma_fmt<FMT_GPTQ, MOE>(p, bm, bn, grid, lds, st);
+    else launch_dma_fmt<FMT_GPTQ_SYM, MOE>(p, bm, bn, grid, lds, st);
+    return hipGetLastError();
 }
 
 template <int FMT, int BM, bool MOE>
@@ -314,6 +734,8 @@ static hipError_t launch_any(int fmt, const PrefillParams& p, int bm, dim3 grid,
 }
 
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
+    if (s.dma)
+        return launch_dma_any<false>(fmt, p, s.bm, s.bn, dim3(s.col_tiles, s.row_tiles), s.lds, st);
     return launch_any<false>(fmt, p, s.bm, dim3(s.col_tiles, s.row_tiles), s.lds, st);
 }
 
@@ -324,6 +746,10 @@ bool moe_gemm_supported(int N, int K, int G, int block_m) {
 
 hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
                            hipStream_t st) {
+    const long long a_rows = (p.num_pairs + p.a_div - 1) / p.a_div;
+    if (dma_ok(p.N, p.K, p.G, a_rows) && (long long)p.K * p.N / 2 < (1ll << 31))
+        return launch_dma_any<true>(fmt, p, block_m, BN, dim3(p.N / BN, max_blocks),
+                                    prefill_dma_lds(block_m, BN), st);
     const size_t lds = (size_t)2 * (block_m + BN) * LD * sizeof(half_t);
     return launch_any<true>(fmt, p, block_m, dim3(p.N / BN, max_blocks), lds, st);
 }

@@ -53,9 +53,12 @@ struct PrefillParams {
 
 struct PrefillShape {
     bool ok;
-    int bm, col_tiles, row_tiles;
+    bool dma;               // pipelined kernel (LDS-DMA); else the register-staged one
+    int bm, bn, col_tiles, row_tiles;
     size_t lds;
 };
+
+size_t prefill_dma_lds(int bm, int bn);
 
 PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus);
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st);
