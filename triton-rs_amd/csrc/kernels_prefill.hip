@@ -265,9 +265,9 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
 
 // ------------------------------------------------------------------ pipelined variant
 //
-// Same tile work as prefill_kernel with the memory latency taken off the MFMA stream. All
-// global traffic goes straight to LDS with buffer_load ... lds (no registers held across
-// stages):
+// Same tile work as prefill_kernel with the memory latency taken off the MFMA stream and two
+// waves per SIMD. All global traffic goes straight to LDS with buffer_load ... lds (no
+// registers held across stages):
 //  * A (activations) into two LDS slots, one stage ahead. Rows past M (or padding pairs)
 //    get an offset past the buffer's end, which the buffer unit returns as zero.
 //  * the packed words, scales and zeros of B into a three-slot LDS ring, three stages
@@ -275,13 +275,14 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
 //    B tiles.
 // Per stage the loads are issued A first, B second, and the stage ends waiting with a vmcnt
 // that leaves only the B loads just issued in flight: A(s+1) and everything older is in LDS
-// at the barrier, B gets two stages of latency. One stage is 64 k.
+// at the barrier, B gets two stages of latency. One stage is 64 k. 8 waves (4 along M, 2
+// along N): with one wave per SIMD the dequantisation VALU and the MFMAs do not overlap.
 //
-// LDS rows carry no padding. A: chunk kc of row r at slot kc ^ fa(r), fa(r) = (r & 7) ^
-// ((r >> 3) & 1), which depends on r % 16 only (fixed operand offsets per row block) and
-// keeps 16-row reads conflict-free. B: slot kc ^ fb(n), fb(n) = (n ^ (n >> 3)) & 7, which
-// also spreads the dequant writes (lanes 8 columns apart). A is staged in natural k order
-// (GPTQ's unpack order is undone on the B side with v_perm_b32).
+// LDS layouts (measured conflict-free for the operand reads and the dequant writes):
+//  A [BM][8 chunks of 8 k]: chunk kc of row r at slot kc ^ (r & 7);
+//  B [8 chunks][256 columns] of 8 k each: column n at position n ^ ((n >> 3) & 7).
+// A is staged in natural k order (GPTQ's unpack order is undone on the B side with
+// v_perm_b32).
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
@@ -315,8 +316,7 @@ __device__ __forceinline__ void dma16(i32x4_t rsrc, const void* lds_wave_base, u
         : "memory");
 }
 
-__device__ __forceinline__ int fa(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int fb(int n) { return (n ^ (n >> 3)) & 7; }
+__device__ __forceinline__ int bpos(int n) { return n ^ ((n >> 3) & 7); }
 
 // s_waitcnt vmcnt(n) leaving lgkmcnt and expcnt alone (gfx9 encoding: vmcnt in [3:0] and
 // [15:14])
@@ -342,27 +342,21 @@ size_t prefill_dma_lds(int bm, int bn) {
     return (size_t)2 * bm * BK * 2 + (size_t)2 * BN * BK * 2 + (size_t)3 * RAW_ST;
 }
 
-// WGM x WGN waves: 2 x 2 (one wave per SIMD, wave tile (BM/2) x (BN/2)) or 4 x 2 (two per
-// SIMD, wave tile (BM/4) x (BN/2), so that one wave's dequantisation runs while the other's
-// MFMAs do). NT = 64 WGM WGN threads.
-template <int FMT, int BM, int BN, int WGM, bool MOE>
-__global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams p) {
-    constexpr int WGN = 2, NT = 64 * WGM * WGN, NWV = WGM * WGN;
+constexpr int PF_THREADS = 512;   // 8 waves: 4 along M x 2 along N
+
+template <int FMT, int BM, int BN, bool MOE>
+__global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p) {
+    constexpr int WGM = 4, WGN = 2, NWV = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
     constexpr int RB = WM / 16, CB = WN / 16;
     constexpr int A_ST = BM * BK, B_ST = 256 * BK;  // halfs per stage (B: 256 columns)
-    constexpr int ADMA = BM * 8 / NT;               // A chunks per thread per stage
-    constexpr int WDMA = 8 / NWV;                   // 1 KB blocks of raw words per wave
+    constexpr int ADMA = BM * 8 / PF_THREADS;       // A chunks per thread per stage
     constexpr int BWC = BN / 8;                     // 8-column groups of the tile
-    // dequantisation unit per thread: AWQ: word column bi, DR consecutive rows;
-    // GPTQ: packed row br, DC consecutive columns
-    constexpr int DR = 8 * 256 / NT;                // 8 or 4
-    constexpr int DC = 8 * 256 / NT;
-    static_assert(BWC <= 32 && WN % 16 == 0 && ADMA >= 1 && WDMA >= 1, "tile shape");
+    static_assert(BWC <= 32 && WN % 16 == 0 && WM % 16 == 0 && ADMA >= 1, "tile shape");
 
     extern __shared__ __attribute__((aligned(16))) half_t lds[];
     half_t* As = lds;                                          // [2][BM][64]
-    half_t* Bs = lds + 2 * A_ST;                               // [2][256][64]
+    half_t* Bs = lds + 2 * A_ST;                               // [2][8][256][8]
     char* Raw = reinterpret_cast<char*>(lds + 2 * A_ST + 2 * B_ST);   // [3][RAW_ST]
 
     const int t = threadIdx.x;
@@ -406,7 +400,7 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
         const int idx = (q * NWV + wave) * 64 + lane;
         const int row = idx >> 3, slot = idx & 7;
         const int m = src_row(row);
-        aoff[q] = m >= 0 ? ((uint32_t)m * (uint32_t)p.K + 8u * (uint32_t)(slot ^ fa(row))) * 2u
+        aoff[q] = m >= 0 ? ((uint32_t)m * (uint32_t)p.K + 8u * (uint32_t)(slot ^ (row & 7))) * 2u
                          : DMA_OOB;
     }
     auto dma_a = [&](int slot, int s) {
@@ -417,27 +411,22 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
     };
 
     // ---- B raw: words of a stage as [64 rows][32 words] (AWQ) or [8 packed rows][256
-    // words] (GPTQ) in eight 1 KB blocks; scales by wave 0, zeros by the other waves
-    // (identical bytes to one place: a harmless race that keeps the stage free of branches)
+    // words] (GPTQ) in eight 1 KB blocks, one per wave; scales by wave 0, zeros by the other
+    // waves (identical bytes to one place: a harmless race that keeps the stage free of
+    // branches)
     const i32x4_t wrs = buffer_rsrc(p.qweight, (uint32_t)((size_t)p.K * p.N / 2));
     const i32x4_t srs = buffer_rsrc(p.scales, (uint32_t)((size_t)(p.K / p.G) * p.N * 2));
     const i32x4_t zrs = buffer_rsrc(p.qzeros ? (const void*)p.qzeros : (const void*)p.scales,
                                     p.qzeros ? (uint32_t)((size_t)(p.K / p.G) * NW * 4) : 0u);
-    uint32_t woff[WDMA];
-#pragma unroll
-    for (int h = 0; h < WDMA; ++h) {
-        const int blk = WDMA * wave + h;
-        if constexpr (FMT == FMT_AWQ) {
-            const int row = blk * 8 + (lane >> 3), chunk = lane & 7;   // 4 words per lane
-            woff[h] = 4 * chunk < BWC
-                          ? ((uint32_t)row * (uint32_t)NW + (uint32_t)(n0 >> 3) + 4u * chunk) * 4u
-                          : DMA_OOB;
-        } else {
-            const int prow = blk, chunk = lane;                         // packed row blk
-            woff[h] = 4 * chunk < BN
-                          ? ((uint32_t)prow * (uint32_t)p.N + (uint32_t)n0 + 4u * chunk) * 4u
-                          : DMA_OOB;
-        }
+    uint32_t woff;
+    if constexpr (FMT == FMT_AWQ) {
+        const int row = wave * 8 + (lane >> 3), chunk = lane & 7;   // 4 words per lane
+        woff = 4 * chunk < BWC
+                   ? ((uint32_t)row * (uint32_t)NW + (uint32_t)(n0 >> 3) + 4u * chunk) * 4u
+                   : DMA_OOB;
+    } else {
+        woff = 4 * lane < BN ? ((uint32_t)wave * (uint32_t)p.N + (uint32_t)n0 + 4u * lane) * 4u
+                             : DMA_OOB;                          // packed row `wave`
     }
     const bool zw_wave = FMT != FMT_GPTQ_SYM && wave != 0;
     const i32x4_t szrs = zw_wave ? zrs : srs;
@@ -451,89 +440,74 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
         const uint32_t wstep = (FMT == FMT_AWQ) ? (uint32_t)k0 * (uint32_t)NW * 4u
                                                 : (uint32_t)(k0 >> 3) * (uint32_t)p.N * 4u;
         dma16(szrs, dst + szdst, szoff + (uint32_t)g * szrow);
-#pragma unroll
-        for (int h = 0; h < WDMA; ++h) dma16(wrs, dst + (WDMA * wave + h) * 1024, woff[h] + wstep);
+        dma16(wrs, dst + wave * 1024, woff + wstep);
     };
 
-    // ---- dequantisation into the fp16 B tile [256][64] (columns past BN are never read)
+    // ---- dequantisation into the fp16 B tile: thread t owns k chunk kq = t / 64 (8 k) and
+    // columns 8 bw + 4 h + 0..3, bw = t % 32, h = (t / 32) % 2 (lanes 8 columns apart)
+    const int bw = t & 31, hh = (t >> 5) & 1, kq = t >> 6;
     auto dequant_b = [&](int slot, int buf) {
         const char* src = Raw + slot * RAW_ST;
-        half_t* B = Bs + buf * B_ST;
+        half_t* B = Bs + buf * B_ST + kq * 256 * 8;
+        const uint32_t sv2[2] = {
+            reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh],
+            reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh + 1]};
+        uint32_t zw = 0u;
+        if constexpr (FMT != FMT_GPTQ_SYM) zw = reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S)[bw];
+        u32x4 col[4];
         if constexpr (FMT == FMT_AWQ) {
-            const int bi = t & 31, br = t >> 5;          // word column, DR-row group
-            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src) + DR * br * 32 + bi;
-            uint32_t bw[DR];
+            // rows 8 kq .. 8 kq + 7 of word column bw; columns 4 hh .. 4 hh + 3 of the word
+            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src) + 8 * kq * 32 + bw;
+            uint32_t w8[8];
 #pragma unroll
-            for (int r = 0; r < DR; ++r) bw[r] = wp[32 * r];
-            const u32x4 sv = *reinterpret_cast<const u32x4*>(src + RAW_W + 16 * bi);
-            const uint32_t zw = *reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S + 4 * bi);
-            half2_t hz[8], hs[8];
+            for (int r = 0; r < 8; ++r) w8[r] = wp[32 * r];
+            half2_t hz[4], hs[4];
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const uint32_t zb = 0x6400u + (uint32_t)nib(zw, awq_slot(c));
+            for (int c = 0; c < 4; ++c) {
+                const int cc = 4 * hh + c;
+                const uint32_t zb = 0x6400u + (uint32_t)nib(zw, awq_slot(cc));
                 hz[c] = as_h2(zb | (zb << 16));
-                hs[c] = as_h2(perm(sv[c >> 1], sv[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
+                hs[c] = as_h2(perm(sv2[c >> 1], sv2[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
             }
-            half2_t pr[DR / 2][8];
+            half2_t pr[4][4];
 #pragma unroll
-            for (int rp = 0; rp < DR / 2; ++rp) {
-                const uint32_t a = bw[2 * rp], b = bw[2 * rp + 1];
-                const uint32_t p0 = perm(b, a, 0x05040100u);
-                const uint32_t p1 = perm(b, a, 0x07060302u);
-#pragma unroll
-                for (int sl = 0; sl < 8; ++sl) {
-                    const uint32_t src2 = sl < 4 ? p0 : p1;
-                    const int c = awq_col_of_slot(sl);
-                    pr[rp][c] = deq2(nib_pair(src2 >> (4 * (sl & 3))), hz[c], hs[c]);
-                }
+            for (int rp = 0; rp < 4; ++rp) {
+                const uint32_t a = w8[2 * rp], b = w8[2 * rp + 1];
+                // slots of columns 4 hh + c: hh = 0 -> 0, 4, 1, 5 ; hh = 1 -> 2, 6, 3, 7
+                const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
+                const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
+                const int sh = 8 * hh;                          // slots 2hh, 2hh+1 (and +4)
+                pr[rp][0] = deq2(nib_pair(p0 >> sh), hz[0], hs[0]);
+                pr[rp][1] = deq2(nib_pair(p1 >> sh), hz[1], hs[1]);
+                pr[rp][2] = deq2(nib_pair(p0 >> (sh + 4)), hz[2], hs[2]);
+                pr[rp][3] = deq2(nib_pair(p1 >> (sh + 4)), hz[3], hs[3]);
             }
-            // rows DR br .. DR br + DR - 1: chunk DR br / 8, offset DR br % 8 halfs in it
-            const int kc = (DR * br) >> 3, ko = (DR * br) & 7;
 #pragma unroll
-            for (int c = 0; c < 8; ++c) {
-                const int n = 8 * bi + c;
-                half_t* dst = B + n * BK + 8 * (kc ^ fb(n)) + ko;
-                if constexpr (DR == 8)
-                    *reinterpret_cast<u32x4*>(dst) = pack8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
-                else
-                    *reinterpret_cast<u32x2*>(dst) = u32x2{as_u32(pr[0][c]), as_u32(pr[1][c])};
-            }
+            for (int c = 0; c < 4; ++c) col[c] = pack8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
         } else {
-            const int bi = t % (256 / DC), br = t / (256 / DC);   // column group, packed row
-            const u32x4* wp = reinterpret_cast<const u32x4*>(src + br * 1024 + 4 * DC * bi);
-            uint32_t bw[DC];
+            // packed row kq (8 k) of columns 8 bw + 4 hh + 0..3
+            const u32x4 w4 = *reinterpret_cast<const u32x4*>(src + kq * 1024 + 4 * (8 * bw + 4 * hh));
+            const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-            for (int h = 0; h < DC / 4; ++h) {
-                const u32x4 v = wp[h];
-                bw[4 * h + 0] = v.x; bw[4 * h + 1] = v.y; bw[4 * h + 2] = v.z; bw[4 * h + 3] = v.w;
-            }
-            const half_t* sp = reinterpret_cast<const half_t*>(src + RAW_W) + DC * bi;
-            uint32_t sw[DC / 2];
-#pragma unroll
-            for (int h = 0; h < DC / 2; ++h) sw[h] = reinterpret_cast<const uint32_t*>(sp)[h];
-            const uint32_t zw = (FMT == FMT_GPTQ_SYM)
-                                    ? 0u
-                                    : *reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S +
-                                                                         4 * ((DC * bi) >> 3));
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                const int n = DC * bi + c;
+            for (int c = 0; c < 4; ++c) {
                 uint32_t z;
                 if constexpr (FMT == FMT_GPTQ_SYM) z = 8u;
-                else z = (uint32_t)(nib(zw, n & 7) + p.zero_offset);
+                else z = (uint32_t)(nib(zw, 4 * hh + c) + p.zero_offset);
                 const uint32_t zb = 0x6400u + z;
                 const half2_t hz = as_h2(zb | (zb << 16));
-                const half2_t hs = as_h2(perm(sw[c >> 1], sw[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
-                const uint32_t w = bw[c];
+                const half2_t hs = as_h2(perm(sv2[c >> 1], sv2[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
+                const uint32_t w = ws[c];
                 const uint32_t q0 = as_u32(deq2(nib_pair(w), hz, hs));         // k0, k4
                 const uint32_t q1 = as_u32(deq2(nib_pair(w >> 4), hz, hs));    // k1, k5
                 const uint32_t q2 = as_u32(deq2(nib_pair(w >> 8), hz, hs));    // k2, k6
                 const uint32_t q3 = as_u32(deq2(nib_pair(w >> 12), hz, hs));   // k3, k7
-                *reinterpret_cast<u32x4*>(B + n * BK + 8 * (br ^ fb(n))) =
-                    u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
-                          perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
+                col[c] = u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
+                               perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
             }
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            *reinterpret_cast<u32x4*>(B + 8 * bpos(8 * bw + 4 * hh + c)) = col[c];
     };
 
     float4_t acc[RB][CB];
@@ -542,8 +516,13 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
+    // operand offsets (halfs) within a stage: A row block r at +16 r rows; B column block c
+    int boff[CB];
+#pragma unroll
+    for (int c = 0; c < CB; ++c) boff[c] = (kb * 256 + bpos(wn * WN + 16 * c + j)) * 8;
+    const int aoff_l = (wm * WM + j) * BK;
     auto compute = [&](int a_slot, int buf) {
-        const half_t* A = As + a_slot * A_ST + (wm * WM + j) * BK;
+        const half_t* A = As + a_slot * A_ST + aoff_l;
         const half_t* B = Bs + buf * B_ST;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -551,12 +530,10 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
             half8_t af[RB], bf[CB];
 #pragma unroll
             for (int r = 0; r < RB; ++r)
-                af[r] = *reinterpret_cast<const half8_t*>(A + 16 * r * BK + 8 * (kc ^ fa(j)));
+                af[r] = *reinterpret_cast<const half8_t*>(A + 16 * r * BK + 8 * (kc ^ (j & 7)));
 #pragma unroll
-            for (int c = 0; c < CB; ++c) {
-                const int n = wn * WN + 16 * c + j;
-                bf[c] = *reinterpret_cast<const half8_t*>(B + n * BK + 8 * (kc ^ fb(n)));
-            }
+            for (int c = 0; c < CB; ++c)
+                bf[c] = *reinterpret_cast<const half8_t*>(B + boff[c] + ks * 4 * 256 * 8);
 #pragma unroll
             for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -576,7 +553,7 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
     __syncthreads();
 
     // ---- stage s: issue A(s+1), then raw B(s+3) into the ring slot B(s) vacated; MFMAs
-    // of stage s and the dequantisation of B(s+1); wait for all but the raw word loads just
+    // of stage s and the dequantisation of B(s+1); wait for all but the raw word load just
     // issued; barrier. Indices past the end are clamped (their loads land in slots nobody
     // reads any more).
     for (int s = 0; s < ns; ++s) {
@@ -585,7 +562,7 @@ __global__ void __launch_bounds__(64 * WGM * 2) prefill_dma_kernel(PrefillParams
         dma_b(rs, min(s + 3, ns - 1));
         compute(s & 1, s & 1);
         dequant_b(rs == 2 ? 0 : rs + 1, (s + 1) & 1);
-        wait_vmcnt<WDMA>();
+        wait_vmcnt<1>();
         __syncthreads();
     }
     wait_vmcnt<0>();   // no LDS write may be in flight when the workgroup ends
@@ -658,20 +635,14 @@ static void allow_lds(F* kernel, size_t lds) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
-// waves per workgroup along M (x 2 along N): 4 gives two waves per SIMD, so that one wave's
-// dequantisation VALU runs while the other's MFMAs do (one wave does not overlap the two)
-constexpr int PF_WGM = 4;
-
 template <int FMT, int BM, int BN2, bool MOE>
 static void launch_dma_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t st) {
-    constexpr int WGM = (BM / PF_WGM >= 16) ? PF_WGM : 2;
     static bool attr_set = false;
     if (!attr_set) {
-        allow_lds(&prefill_dma_kernel<FMT, BM, BN2, WGM, MOE>, prefill_dma_lds(BM, BN2));
+        allow_lds(&prefill_dma_kernel<FMT, BM, BN2, MOE>, prefill_dma_lds(BM, BN2));
         attr_set = true;
     }
-    hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, WGM, MOE>), grid, dim3(128 * WGM), lds,
-                       st, p);
+    hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, MOE>), grid, dim3(PF_THREADS), lds, st, p);
 }
 
 template <int FMT, bool MOE>
