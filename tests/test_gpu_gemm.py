@@ -53,6 +53,16 @@ def test_gemv_small(torch_cuda, orc, fmt, M):
     assert_parity(y, _oracle(orc, p), what=f"gemv fmt={fmt} M={M}")
 
 
+@pytest.mark.parametrize("M", [5, 6, 7, 8])
+@pytest.mark.parametrize("K,N,G", [(1024, 512, 128), (2048, 768, 64), (512, 256, 256)])
+def test_gemv_awq_matrix_core(torch_cuda, orc, M, K, N, G):
+    """AWQ decode for 5 <= M <= 8: dot products on the matrix cores (block-diagonal x)."""
+    p = Problem(AWQ, M=M, K=K, N=N, G=G, seed=1050 + M + K // 64)
+    assert pkg().plan("awq", M, N, K, G) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"awq gemv M={M} K={K} N={N} G={G}")
+
+
 @pytest.mark.parametrize("fmt,G", [(AWQ, 32), (AWQ, 64), (GPTQ, 32), (GPTQ, 64), (GPTQ, 256)])
 def test_gemv_group_sizes(torch_cuda, orc, fmt, G):
     p = Problem(fmt, M=1, K=2048, N=256, G=G, seed=1100 + G)
@@ -95,7 +105,8 @@ def test_gemv_deterministic_and_reusable(torch_cuda, orc):
                                    (200, 512, 1024)])
 def test_mfma_shapes(torch_cuda, orc, fmt, M, K, N):
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2000 + M + 7 * fmt)
-    assert pkg().plan(FMT_NAME[fmt], M, N, K, p.G) in ("skinny", "prefill")
+    expect = ("gemv",) if fmt == AWQ and M <= 8 else ("skinny", "prefill")
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, p.G) in expect
     y = _run_gemm(torch_cuda, p)
     assert_parity(y, _oracle(orc, p), what=f"mfma fmt={fmt} M={M} K={K} N={N}")
 

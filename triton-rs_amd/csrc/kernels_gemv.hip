@@ -297,6 +297,186 @@ gemv_gptq_kernel(GemvParams p) {
         splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
 }
 
+// ------------------------------------------------------------------ AWQ, M = 5..8: matrix-core dot
+
+// For 5 <= M <= 8 the VALU dot products above would cost M dot2 per nibble pair. Here the
+// dot products run on v_mfma_f32_16x16x32_f16 and the vector ALUs only unpack. An AWQ word
+// holds 8 columns of one row while the MFMA B operand wants 8 k of one column per lane, so
+// instead of transposing nibbles the MFMA contraction index is made (row, nibble class) and
+// the A operand carries x block-diagonally:
+//   lane (j, q) of B supplies, for word column j of its row r_q, the 8 values
+//     e = 0..7: fp16(1024 + c_e q[slot(e)]), slot = [0,4,1,5,2,6,3,7][e], c_e in {1, 16}
+//     (v_and_or_b32 of w and w >> 8 with 0x000F000F / 0x00F000F0 and the 0x6400 exponent);
+//   lane (i, q) of A supplies x[m][r_q] at element e = i % 8 (m = 2 set + i / 8), else 0.
+// Then D[8 (m % 2) + e][j] = sum_q x[m][r_q] (1024 + c_e q[r_q][slot(e)]): one MFMA covers 4
+// rows x 16 words x 8 slots for two rows of x. After the wave's R rows (one quantisation
+// group) the zero and scale are applied once, as in the kernel above:
+//   sum_k x_k (q_k - z) s = s ((A - 1024 X) / c - z X).
+// Per 8 weights: one shift and four v_and_or_b32; per step and pair of x rows four
+// v_perm_b32 place x into A.
+//
+// Tile: WW = 16 CW words (8 WW columns) x WAVES * R rows; lane (j, q) streams rows
+// r0 + (R/4) q + s, s = 0 .. R/4 - 1, of word columns CW j .. CW j + CW - 1 with PF steps of
+// loads in flight.
+template <int M, int CW, int R, int WAVES, int PF>
+__global__ void __launch_bounds__(64 * WAVES)
+gemv_awq_mfma_kernel(GemvParams p) {
+    constexpr int S = R / 4;          // steps per wave
+    constexpr int MS = (M + 1) / 2;   // MFMA sets: two rows of x each
+    constexpr int WW = 16 * CW;       // words per tile row
+    constexpr int C = 8 * WW;         // columns per tile
+    static_assert(S % 8 == 0 && PF <= S && (CW == 2 || CW == 4), "tile shape");
+
+    __shared__ float red[WAVES][M][C];
+    __shared__ int flag;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int j = lane & 15, q = lane >> 4;
+    const int ct = blockIdx.x, split = blockIdx.y;
+    const int NW = p.N >> 3;
+    const int wc = ct * WW + CW * j;                   // first word column of this lane
+    const int rw0 = (split * WAVES + wave) * R;        // first row of this wave
+    const int rl0 = rw0 + S * q;                       // rows of this lane: rl0 + s
+    const int g = rw0 / p.G;
+
+    // ---- weight ring: step s of the lane lives in slot s % PF
+    uint32_t bw[PF][CW];
+    const uint32_t off0 = (uint32_t)rl0 * (uint32_t)NW + (uint32_t)wc;
+    auto issue = [&](int u, int s) {
+        const uint32_t off = off0 + (uint32_t)s * (uint32_t)NW;
+        if constexpr (CW == 4) {
+            const u32x4 v = ld_stream4(at_bytes(p.qweight, 4u * off));
+            bw[u][0] = v.x; bw[u][1] = v.y; bw[u][2] = v.z; bw[u][3] = v.w;
+        } else {
+            const u32x2 v = ld_stream2(at_bytes(p.qweight, 4u * off));
+            bw[u][0] = v.x; bw[u][1] = v.y;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < PF; ++u) issue(u, u);
+
+    // ---- x of the lane's rows for its A row (m = 2 ms + j / 8), S halfs per set
+    uint32_t xr[MS][S / 2];
+    float xsum[MS];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+        const int m = 2 * ms + (j >> 3);
+        xsum[ms] = 0.f;
+        if (m < M) {
+            const u32x4* xp = reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + rl0);
+#pragma unroll
+            for (int h = 0; h < S / 8; ++h) {
+                const u32x4 v = xp[h];
+                xr[ms][4 * h + 0] = v.x; xr[ms][4 * h + 1] = v.y;
+                xr[ms][4 * h + 2] = v.z; xr[ms][4 * h + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int h = 0; h < S / 2; ++h) xr[ms][h] = 0u;
+        }
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int h = 0; h < S / 2; ++h) xsum[ms] = dot2(as_h2(xr[ms][h]), one2, xsum[ms]);
+    }
+    // v_perm_b32 selectors placing half (s % 2) of an x word at element e = j % 8 of the A
+    // operand (selector byte 0x0C yields zero)
+    uint32_t sel[2][4];
+    {
+        const int e = j & 7;
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+            const uint32_t b0 = 2u * par, b1 = b0 + 1u;
+            const uint32_t half_sel = (e & 1) ? ((b1 << 24) | (b0 << 16) | 0x0C0Cu)
+                                              : (0x0C0C0000u | (b1 << 8) | b0);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sel[par][t] = (t == (e >> 1)) ? half_sel : 0x0C0C0C0Cu;
+        }
+    }
+
+    float4_t acc[MS][CW];
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+        for (int c = 0; c < CW; ++c) acc[ms][c] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int s0 = 0; s0 < S; s0 += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; ++u) {
+            const int s = s0 + u;
+            half8_t af[MS];
+#pragma unroll
+            for (int ms = 0; ms < MS; ++ms) {
+                const uint32_t xw = xr[ms][s >> 1];
+                const u32x4 a = {perm(xw, xw, sel[s & 1][0]), perm(xw, xw, sel[s & 1][1]),
+                                 perm(xw, xw, sel[s & 1][2]), perm(xw, xw, sel[s & 1][3])};
+                af[ms] = __builtin_bit_cast(half8_t, a);
+            }
+#pragma unroll
+            for (int c = 0; c < CW; ++c) {
+                const uint32_t w = bw[u][c], w8 = w >> 8;
+                const u32x4 b = {as_u32(nib_pair(w)), as_u32(nib_pair16(w)), as_u32(nib_pair(w8)),
+                                 as_u32(nib_pair16(w8))};
+                const half8_t bf = __builtin_bit_cast(half8_t, b);
+#pragma unroll
+                for (int ms = 0; ms < MS; ++ms)
+                    acc[ms][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[ms], bf, acc[ms][c], 0, 0, 0);
+            }
+            if (s + PF < S) issue(u, s + PF);
+        }
+    }
+
+    // ---- lane (j, q) holds D rows 4 q .. 4 q + 3 of each set: m = 2 ms + q / 2, classes
+    // e = 4 (q % 2) + r, i.e. columns 4 (q % 2) + r of its words
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+        float tsum = xsum[ms];
+        tsum += __shfl_xor(tsum, 16);
+        tsum += __shfl_xor(tsum, 32);
+        xsum[ms] = __shfl(tsum, 8 * (q >> 1));
+    }
+    const int hq = q & 1;
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+        const int word = wc + c;
+        const uint32_t qz = p.qzeros[(size_t)g * NW + word];
+        const u32x2 sv = *reinterpret_cast<const u32x2*>(p.scales + (size_t)g * p.N + 8 * word + 4 * hq);
+        const half2_t s01 = as_h2(sv.x), s23 = as_h2(sv.y);
+        const float scl[4] = {(float)s01.x, (float)s01.y, (float)s23.x, (float)s23.y};
+#pragma unroll
+        for (int ms = 0; ms < MS; ++ms) {
+            const int m = 2 * ms + (q >> 1);
+            if (m >= M) continue;
+            const float X = xsum[ms];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int col = 4 * hq + r;                 // column within the word
+                const float z = (float)nib(qz, awq_slot(col));
+                const float inv_c = (r & 2) ? (1.0f / 16.0f) : 1.0f;
+                const float u = (acc[ms][c][r] - 1024.0f * X) * inv_c - z * X;
+                red[wave][m][8 * (CW * j + c) + col] = scl[r] * u;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- reduce over waves; write partial (or the output when there is one split)
+    const int n0 = ct * C;
+    for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
+        const int m = i / C, cidx = i - m * C;
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += red[w][m][cidx];
+        const size_t off = (size_t)m * p.N + n0 + cidx;
+        if (p.splits == 1) p.out[off] = (half_t)sum;
+        else st_coherent(p.ws + (size_t)split * M * p.N + off, sum);
+    }
+    if (p.splits == 1) return;
+    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
+    if (splitk_arrive(flags, split, p.splits, &flag))
+        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
+}
+
 // ------------------------------------------------------------------ host launchers
 
 namespace {
@@ -307,10 +487,18 @@ constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
 constexpr int GQ_CW = 4, GQ_RL = 4, GQ_WAVES = 4, GQ_LPR = 32;
 constexpr int GQ_COLS = GQ_LPR * GQ_CW;
 constexpr int GQ_ROWS = (64 / GQ_LPR) * GQ_WAVES * GQ_RL * 8;
+// AWQ, M = 5..8, matrix-core dot: CW = 2 words per lane (256 columns), R = 64 rows per wave
+constexpr int AM_CW = 2, AM_R = 64, AM_WAVES = 4, AM_PF = 16;
+constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES;
 }  // namespace
 
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G) {
     GemvShape s{};
+    if (fmt == FMT_AWQ && M > GEMV_MAX_M && M <= GEMV_MFMA_MAX_M) {
+        if (N % AM_COLS || K % AM_ROWS || G % AM_R || K % G) return s;
+        s.ok = true; s.col_tiles = N / AM_COLS; s.splits = K / AM_ROWS; s.threads = 64 * AM_WAVES;
+        return s;
+    }
     if (M < 1 || M > GEMV_MAX_M) return s;
     if (fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
@@ -320,6 +508,14 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G) {
         s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / GQ_ROWS; s.threads = 64 * GQ_WAVES;
     }
     return s;
+}
+
+template <int M>
+static hipError_t launch_gemv_mfma(const GemvParams& p, const GemvShape& s, hipStream_t st) {
+    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
+    hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF>),
+                       dim3(s.col_tiles, s.splits), dim3(s.threads), 0, st, p);
+    return hipGetLastError();
 }
 
 template <int M>
@@ -341,6 +537,10 @@ hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStre
         case 2: return launch_gemv_m<2>(fmt, p, s, st);
         case 3: return launch_gemv_m<3>(fmt, p, s, st);
         case 4: return launch_gemv_m<4>(fmt, p, s, st);
+        case 5: return fmt == FMT_AWQ ? launch_gemv_mfma<5>(p, s, st) : hipErrorInvalidValue;
+        case 6: return fmt == FMT_AWQ ? launch_gemv_mfma<6>(p, s, st) : hipErrorInvalidValue;
+        case 7: return fmt == FMT_AWQ ? launch_gemv_mfma<7>(p, s, st) : hipErrorInvalidValue;
+        case 8: return fmt == FMT_AWQ ? launch_gemv_mfma<8>(p, s, st) : hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }

@@ -8,7 +8,8 @@ namespace w4a16 {
 
 typedef _Float16 half_t;
 
-constexpr int GEMV_MAX_M = 4;
+constexpr int GEMV_MAX_M = 4;        // VALU dot products
+constexpr int GEMV_MFMA_MAX_M = 8;   // AWQ with matrix-core dot products
 
 // Split-K flag area: one 32-bit flag per (tile, split), FLAG_STRIDE words apart (a
 // 256-byte line each), in the first SPLITK_FLAG_BYTES of a per-stream workspace.
