@@ -34,8 +34,8 @@ static inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) 
 
 // ------------------------------------------------------------------ workspace
 
-// One split-K workspace per (device, stream): per-(tile, split) flags (zeroed at
-// allocation, cleared again by the kernels themselves) followed by fp32 partials.
+// One split-K workspace per (device, stream): per-tile counters (zeroed at allocation,
+// returned to zero by the kernels themselves) followed by fp32 partials.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
@@ -43,7 +43,7 @@ struct Workspace {
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES;  // room for SPLITK_MAX_PAIRS flags
+constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES;  // room for SPLITK_MAX_TILES counters
 
 static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
     int dev = 0;
@@ -126,16 +126,34 @@ static int device_cus() {
     return cus;
 }
 
+// Whether workgroup b of a launch runs on XCD b mod 8 on the current device (the GEMV's
+// L2-local split-K hand-off relies on it). Probed once per device with a small kernel;
+// false when the probe fails or placement differs, and the kernels then use the
+// device-scope hand-off.
+static bool xcd_placement() {
+    static std::mutex mu;
+    static std::map<int, bool> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) { (void)hipGetLastError(); return false; }
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    bool ok = false;
+    if (check_xcd_placement(&ok) != hipSuccess) { (void)hipGetLastError(); ok = false; }
+    cache[dev] = ok;
+    return ok;
+}
+
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) {
         const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus, true);
-        return sk.ok && (size_t)sk.col_tiles * sk.splits <= SPLITK_MAX_PAIRS ? W4A16_KERNEL_SKINNY
-                                                                          : W4A16_KERNEL_STRIDED;
+        return sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES ? W4A16_KERNEL_SKINNY
+                                                                : W4A16_KERNEL_STRIDED;
     }
-    const GemvShape gv = gemv_shape(fmt, M, N, K, G);
-    if (gv.ok && (size_t)gv.col_tiles * gv.splits <= SPLITK_MAX_PAIRS) return W4A16_KERNEL_GEMV;
+    const GemvShape gv = gemv_shape(fmt, M, N, K, G, false);
+    if (gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
     const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);
-    if (M <= 64 && sk.ok && (size_t)sk.col_tiles * sk.splits <= SPLITK_MAX_PAIRS)
+    if (M <= 64 && sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES)
         return W4A16_KERNEL_SKINNY;
     if (prefill_shape(fmt, M, N, K, G, cus).ok) return W4A16_KERNEL_PREFILL;
     return W4A16_KERNEL_STRIDED;
@@ -186,8 +204,8 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.splits = s.splits; p.steps_per_wave = s.steps_per_wave;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.splits > SPLITK_MAX_PAIRS)
-                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K flag area");
+            if ((size_t)s.col_tiles > SPLITK_MAX_TILES)
+                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.flags, &p.ws);
             if (rc) return rc;
         }
@@ -211,7 +229,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     }
 
     if (kernel == W4A16_KERNEL_GEMV) {
-        const GemvShape s = gemv_shape(fmt, M, N, K, G);
+        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd_placement());
         GemvParams p{};
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
@@ -219,9 +237,10 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset; p.splits = s.splits;
+        p.col_tiles = s.col_tiles;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles * s.splits > SPLITK_MAX_PAIRS)
-                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K flag area");
+            if ((size_t)s.col_tiles > SPLITK_MAX_TILES)
+                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K counter area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;
         }

@@ -1,20 +1,23 @@
-// Decode-regime W4A16 GEMV (M <= 4): HBM-bound, no MFMA.
+// Decode-regime W4A16 GEMV (M <= 8): HBM-bound.
 //
 // Computes out[m, n] = sum_k x[m, k] * W16[k, n] for the reference's two packings
 // (crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:15-32 GPTQ [K/8, N] packed along K;
 // awq_gemm_int4_typed.rs:10-31 AWQ [K, N/8] packed along N, slot order [0,4,1,5,2,6,3,7]),
 // split over K so that a launch has ~900 workgroups, with a deterministic in-kernel
-// split-K hand-off (splitk.h: a workgroup that sees all splits published sums the fp32
-// partials in split order).
+// split-K hand-off (splitk.h: the workgroup that arrives last at the tile's counter sums
+// the fp32 partials in split order). At M = 1 all splits of a tile run on one XCD and the
+// hand-off stays in that XCD's L2.
 //
-// Per lane the inner loop is: 128-bit (or 32-bit) coalesced loads of packed words, a
-// nibble unpack into fp16 with the 0x6400 exponent trick (1024 + q, or 1024 + 16 q for the
-// odd nibble of each byte, so no shift is needed for it), and v_dot2c_f32_f16 against
-// pairs of x. All rows a lane touches lie in one quantisation group, so the zero point and
-// the scale are applied once per lane and column to the fp32 sum:
+// VALU kernels (AWQ M = 1, GPTQ M <= 4): per lane the inner loop is 128-bit (or 32-bit)
+// coalesced loads of packed words, a nibble unpack into fp16 with the 0x6400 exponent
+// trick (1024 + q, or 1024 + 16 q for the odd nibble of each byte, so no shift is needed
+// for it), and v_dot2c_f32_f16 against pairs of x. No MFMA. All rows a lane touches lie
+// in one quantisation group, so the zero point and the scale are applied once per lane
+// and column to the fp32 sum:
 //     sum_k x_k (q_k - z) s = s * (A - 1024 X - z X),   A = sum_k x_k (1024 + q_k)
 // which equals the reference's dequant-then-dot up to fp32 rounding (the reference rounds
 // each dequantised weight to fp16 first; the difference is < 2^-11 relative per term).
+// The AWQ matrix-core kernel (M = 2..8) moves the dot products to v_mfma (below).
 #include "device_common.h"
 #include "launch.h"
 #include "splitk.h"
@@ -26,7 +29,7 @@ namespace w4a16 {
 // Tile: 256 columns (32 words per row) x R rows. Lane mapping: LPR = 32 / CW lanes per row,
 // each owning CW words (8*CW columns); RPW = 64 / LPR row-lanes per wave; a lane walks RL
 // consecutive rows (all in one group: G % RL == 0).
-template <int M, int CW, int RL, int WAVES>
+template <int M, int CW, int RL, int WAVES, bool XCD>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_awq_kernel(GemvParams p) {
     constexpr int LPR = 32 / CW;
@@ -43,8 +46,9 @@ gemv_awq_kernel(GemvParams p) {
     const int wave = threadIdx.x >> 6;
     const int cl = lane % LPR;
     const int rb = wave * RPW + lane / LPR;
-    const int ct = blockIdx.x;
-    const int split = blockIdx.y;
+    int ct, split;
+    tile_of_block<XCD>(p.col_tiles, p.splits, ct, split);
+    constexpr int SC = XCD ? SCOPE_XCD : SCOPE_DEVICE;
     const int NW = p.N >> 3;                       // words per qweight row
     const int wc0 = ct * 32 + cl * CW;             // first word column of this lane
     const int k0 = split * R + rb * RL;            // first row of this lane
@@ -158,19 +162,18 @@ gemv_awq_kernel(GemvParams p) {
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
         if (p.splits == 1) p.out[off] = (half_t)s;
-        else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
+        else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
-    if (splitk_arrive(flags, split, p.splits, &flag))
-        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
+    if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
+        splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
 }
 
 // ------------------------------------------------------------------ GPTQ GEMV
 
 // Tile: C = LPR * CW columns x R k-rows. A lane owns CW consecutive columns (one 128-bit
 // load per packed row for CW = 4) and RL consecutive packed rows (8*RL k, one group).
-template <int FMT, int M, int CW, int RL, int WAVES, int LPR>
+template <int FMT, int M, int CW, int RL, int WAVES, int LPR, bool XCD>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_gptq_kernel(GemvParams p) {
     constexpr int RPW = 64 / LPR;
@@ -185,8 +188,9 @@ gemv_gptq_kernel(GemvParams p) {
     const int wave = threadIdx.x >> 6;
     const int cl = lane % LPR;
     const int rb = wave * RPW + lane / LPR;
-    const int ct = blockIdx.x;
-    const int split = blockIdx.y;
+    int ct, split;
+    tile_of_block<XCD>(p.col_tiles, p.splits, ct, split);
+    constexpr int SC = XCD ? SCOPE_XCD : SCOPE_DEVICE;
     const int n0 = ct * C;
     const int c0 = n0 + cl * CW;                       // first column of this lane
     const int kp0 = (split * RK) / 8 + rb * RL;        // first packed row
@@ -289,12 +293,11 @@ gemv_gptq_kernel(GemvParams p) {
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
         if (p.splits == 1) p.out[off] = (half_t)s;
-        else st_coherent(p.ws + (size_t)split * M * p.N + off, s);
+        else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
-    if (splitk_arrive(flags, split, p.splits, &flag))
-        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
+    if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
+        splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
 }
 
 // ------------------------------------------------------------------ AWQ, M = 5..8: matrix-core dot
@@ -318,7 +321,7 @@ gemv_gptq_kernel(GemvParams p) {
 // Tile: WW = 16 CW words (8 WW columns) x WAVES * R rows; lane (j, q) streams rows
 // r0 + (R/4) q + s, s = 0 .. R/4 - 1, of word columns CW j .. CW j + CW - 1 with PF steps of
 // loads in flight.
-template <int M, int CW, int R, int WAVES, int PF>
+template <int M, int CW, int R, int WAVES, int PF, bool XCD>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_awq_mfma_kernel(GemvParams p) {
     constexpr int S = R / 4;          // steps per wave
@@ -332,7 +335,9 @@ gemv_awq_mfma_kernel(GemvParams p) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, q = lane >> 4;
-    const int ct = blockIdx.x, split = blockIdx.y;
+    int ct, split;
+    tile_of_block<XCD>(p.col_tiles, p.splits, ct, split);
+    constexpr int SC = XCD ? SCOPE_XCD : SCOPE_DEVICE;
     const int NW = p.N >> 3;
     const int wc = ct * WW + CW * j;                   // first word column of this lane
     const int rw0 = (split * WAVES + wave) * R;        // first row of this wave
@@ -469,12 +474,11 @@ gemv_awq_mfma_kernel(GemvParams p) {
         for (int w = 0; w < WAVES; ++w) sum += red[w][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
         if (p.splits == 1) p.out[off] = (half_t)sum;
-        else st_coherent(p.ws + (size_t)split * M * p.N + off, sum);
+        else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, sum);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = splitk_flags(p.counters, ct, p.splits);
-    if (splitk_arrive(flags, split, p.splits, &flag))
-        splitk_finish<M>(p.ws, p.out, flags, p.splits, p.N, n0, C);
+    if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
+        splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
 }
 
 // ------------------------------------------------------------------ host launchers
@@ -492,42 +496,53 @@ constexpr int AM_CW = 2, AM_R = 64, AM_WAVES = 4, AM_PF = 16;
 constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES;
 }  // namespace
 
-GemvShape gemv_shape(int fmt, int M, int N, int K, int G) {
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     GemvShape s{};
-    if (fmt == FMT_AWQ && M > GEMV_MAX_M && M <= GEMV_MFMA_MAX_M) {
-        if (N % AM_COLS || K % AM_ROWS || G % AM_R || K % G) return s;
-        s.ok = true; s.col_tiles = N / AM_COLS; s.splits = K / AM_ROWS; s.threads = 64 * AM_WAVES;
-        return s;
-    }
-    if (M < 1 || M > GEMV_MAX_M) return s;
-    if (fmt == FMT_AWQ) {
+    // AWQ: matrix-core dot for M = 2..8 (M = 2: 10.3 vs 11.4 us, M = 4: 12.0 vs 14.5 us at
+    // K=4096, N=14336), VALU dot2 for M = 1 and for shapes the matrix-core tile rejects
+    const bool mfma_fits = N % AM_COLS == 0 && K % AM_ROWS == 0 && G % AM_R == 0 && K % G == 0;
+    if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
+        s.ok = true; s.mfma = true; s.col_tiles = N / AM_COLS; s.splits = K / AM_ROWS;
+        s.threads = 64 * AM_WAVES;
+    } else if (M >= 1 && M <= GEMV_MAX_M && fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
         s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
-    } else {
+    } else if (M >= 1 && M <= GEMV_MAX_M) {
         if (N % GQ_COLS || K % GQ_ROWS || G % (GQ_RL * 8) || K % G) return s;
         s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / GQ_ROWS; s.threads = 64 * GQ_WAVES;
+    } else {
+        return s;
     }
+    // The XCD-local hand-off pays off at M = 1 (partials stay in L2: 9.8 vs 10.1 us for
+    // K=4096, N=14336). With more rows the dirty partials the L2s write back at the end of
+    // the kernel cost more than the shorter round trips save, so M > 1 keeps device scope.
+    s.xcd = xcd_placement && M == 1 && s.splits > 1 && s.col_tiles % 8 == 0;
     return s;
 }
 
-template <int M>
-static hipError_t launch_gemv_mfma(const GemvParams& p, const GemvShape& s, hipStream_t st) {
-    (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
-    hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF>),
-                       dim3(s.col_tiles, s.splits), dim3(s.threads), 0, st, p);
-    return hipGetLastError();
+template <int M, bool XCD>
+static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
+    const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
+    const dim3 block(s.threads);
+    if (fmt == FMT_AWQ && s.mfma) {
+        if constexpr (M <= GEMV_MFMA_MAX_M)
+            hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+    } else if constexpr (M <= GEMV_MAX_M) {
+        if (fmt == FMT_AWQ)
+            hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD>), grid, block, 0, st, p);
+        else if (fmt == FMT_GPTQ)
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+        else
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+    }
 }
 
 template <int M>
 static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
-    const dim3 grid(s.col_tiles, s.splits), block(s.threads);
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
-    if (fmt == FMT_AWQ)
-        hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES>), grid, block, 0, st, p);
-    else if (fmt == FMT_GPTQ)
-        hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR>), grid, block, 0, st, p);
-    else
-        hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR>), grid, block, 0, st, p);
+    if (M > GEMV_MAX_M && !(fmt == FMT_AWQ && s.mfma)) return hipErrorInvalidValue;
+    if (s.xcd) launch_gemv_mx<M, true>(fmt, p, s, st);
+    else launch_gemv_mx<M, false>(fmt, p, s, st);
     return hipGetLastError();
 }
 
@@ -537,12 +552,39 @@ hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStre
         case 2: return launch_gemv_m<2>(fmt, p, s, st);
         case 3: return launch_gemv_m<3>(fmt, p, s, st);
         case 4: return launch_gemv_m<4>(fmt, p, s, st);
-        case 5: return fmt == FMT_AWQ ? launch_gemv_mfma<5>(p, s, st) : hipErrorInvalidValue;
-        case 6: return fmt == FMT_AWQ ? launch_gemv_mfma<6>(p, s, st) : hipErrorInvalidValue;
-        case 7: return fmt == FMT_AWQ ? launch_gemv_mfma<7>(p, s, st) : hipErrorInvalidValue;
-        case 8: return fmt == FMT_AWQ ? launch_gemv_mfma<8>(p, s, st) : hipErrorInvalidValue;
+        case 5: return launch_gemv_m<5>(fmt, p, s, st);
+        case 6: return launch_gemv_m<6>(fmt, p, s, st);
+        case 7: return launch_gemv_m<7>(fmt, p, s, st);
+        case 8: return launch_gemv_m<8>(fmt, p, s, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+// Workgroup -> XCD placement probe: workgroup b records its XCC_ID.
+__global__ void xcc_probe_kernel(uint32_t* out) {
+    if (threadIdx.x == 0) {
+        uint32_t x;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+        out[blockIdx.x] = x & 0xFu;
+    }
+}
+
+hipError_t check_xcd_placement(bool* ok) {
+    constexpr int B = 4096;
+    *ok = false;
+    uint32_t* d = nullptr;
+    hipError_t e = hipMalloc(&d, B * sizeof(uint32_t));
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(xcc_probe_kernel, dim3(B), dim3(64), 0, 0, d);
+    e = hipGetLastError();
+    uint32_t h[B];
+    if (e == hipSuccess) e = hipMemcpy(h, d, sizeof h, hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    if (e != hipSuccess) return e;
+    bool same = true;
+    for (int b = 8; b < B; ++b) same = same && h[b] == h[b % 8];
+    *ok = same;
+    return hipSuccess;
 }
 
 }  // namespace w4a16

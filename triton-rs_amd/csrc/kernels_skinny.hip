@@ -10,7 +10,7 @@
 // awq_gemm_int4_typed.rs:213-228) straight into MFMA B-operand registers and multiplied
 // with v_mfma_f32_16x16x32_f16 (fp32 accumulation, the reference's tt.dot). The four waves'
 // accumulators are summed in LDS; when the strip count alone cannot fill the GPU the K
-// range is also split across workgroups, joined by the flag hand-off of splitk.h.
+// range is also split across workgroups, joined by the counter hand-off of splitk.h.
 //
 // Operand layouts: slot j of MFMA c is output column
 // n0 + CPL*j + c; GPTQ k-blocks are consumed in the unpack order (k0,k4)(k1,k5)(k2,k6)(k3,k7)
@@ -256,12 +256,11 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         const float v = red[0][m][col] + red[1][m][col] + red[2][m][col] + red[3][m][col];
         const size_t off = (size_t)m * p.N + n0 + col;
         if (p.splits == 1) p.out[off] = (half_t)v;
-        else st_coherent(p.ws + (size_t)split * p.M * p.N + off, v);
+        else st_partial<SCOPE_DEVICE>(p.ws + (size_t)split * p.M * p.N + off, v);
     }
     if (p.splits == 1) return;
-    uint32_t* flags = splitk_flags(p.flags, ct, p.splits);
-    if (splitk_arrive(flags, split, p.splits, &flag))
-        splitk_finish_rows(p.ws, p.out, flags, p.splits, p.M, p.N, 0, p.M, n0, WN);
+    if (splitk_arrive(splitk_counter(p.flags, ct), p.splits, &flag))
+        splitk_finish_rows<SCOPE_DEVICE>(p.ws, p.out, p.splits, p.M, p.N, 0, p.M, n0, WN);
 }
 
 // ------------------------------------------------------------------ host side

@@ -11,11 +11,12 @@ typedef _Float16 half_t;
 constexpr int GEMV_MAX_M = 4;        // VALU dot products
 constexpr int GEMV_MFMA_MAX_M = 8;   // AWQ with matrix-core dot products
 
-// Split-K flag area: one 32-bit flag per (tile, split), FLAG_STRIDE words apart (a
-// 256-byte line each), in the first SPLITK_FLAG_BYTES of a per-stream workspace.
+// Split-K counter area: one 32-bit counter per output tile, FLAG_STRIDE words apart (a
+// 256-byte line each), in the first SPLITK_FLAG_BYTES of a per-stream workspace; zero
+// between calls.
 constexpr int FLAG_STRIDE = 64;
 constexpr size_t SPLITK_FLAG_BYTES = 2u << 20;
-constexpr size_t SPLITK_MAX_PAIRS = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
+constexpr size_t SPLITK_MAX_TILES = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
 
 struct GemvParams {
     const half_t* x;          // [M, K] contiguous
@@ -24,17 +25,23 @@ struct GemvParams {
     const uint32_t* qzeros;   // [K/G, N/8] (null for GPTQ_SYM)
     half_t* out;              // [M, N]
     float* ws;                // split-K partials [splits, M, N]
-    uint32_t* counters;       // [col_tiles], zero between calls
-    int M, N, K, G, zero_offset, splits;
+    uint32_t* counters;       // one per column tile (FLAG_STRIDE apart), zero between calls
+    int M, N, K, G, zero_offset, splits, col_tiles;
 };
 
 struct GemvShape {
     bool ok;
+    bool mfma;              // AWQ matrix-core kernel (else VALU dot products)
+    bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     int col_tiles, splits, threads;
 };
 
-GemvShape gemv_shape(int fmt, int M, int N, int K, int G);
+// xcd_placement: the device hands workgroup b to XCD b mod 8 (check_xcd_placement).
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement);
 hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st);
+// Runs a probe kernel on the current device and reports whether workgroups whose ids are
+// congruent mod 8 always share an XCD (synchronous; not for use under graph capture).
+hipError_t check_xcd_placement(bool* ok);
 
 // Prefill GEMM (large M): dequant-to-LDS MFMA tiles.
 struct PrefillParams {

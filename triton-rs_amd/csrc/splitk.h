@@ -1,104 +1,158 @@
-// Split-K hand-off shared by the GEMV and MFMA kernels: the workgroups of one output tile
-// each store fp32 partial sums; a workgroup that sees every split of the tile published
-// sums them in a fixed order (deterministic) and writes fp16.
+// Split-K hand-off shared by the GEMV and small-batch MFMA kernels: the workgroups of one
+// output tile each store fp32 partial sums; the workgroup that arrives last sums them in a
+// fixed order (deterministic) and writes fp16.
 //
-// The protocol avoids both whole-cache maintenance and contended atomics, which on this
-// part cost more than the weight stream itself (a __threadfence() emits an L2 write-back
-// and invalidate in every wave; a returning atomic on a counter shared by 16 workgroups
-// serialises at ~0.25 us each):
-//  1. partials are stored with agent-scope atomic stores (global_store ... sc1, written
-//     through to the level all XCDs share) and the wave waits for them (vmcnt(0));
-//  2. the workgroup then publishes its own flag the same way, and waits again. Each flag
-//     has a 256-byte line of its own: with a tile's flags packed in one line, every flag
-//     store and load of the tile queues at the same memory channel;
-//  3. wave 0 reads all flags of the tile with agent-scope loads (sc1: not served from a
-//     stale L1/L2) in one batch. The workgroup whose flag store completed last reads after
-//     every other flag store completed, so at least one workgroup sees all flags set.
-//     Several may: they compute and store identical values.
-//  4. a finisher reads the partials (sc1), sums them in a fixed order, stores fp16 and
-//     clears the tile's flags. No flag of this call can be set after that: every split had
-//     published before the finisher saw them all.
+// Protocol (one 32-bit counter per tile, zero between calls):
+//  1. every thread stores its partials, and the workgroup waits until they have completed
+//     (s_waitcnt vmcnt(0): the stores are acknowledged by the level named below);
+//  2. one thread adds 1 to the tile's counter with a returning atomic (performed at L2, the
+//     same instruction at every scope on this target). The workgroup that reads
+//     `splits - 1` arrived last: every other split had completed its stores before its own
+//     add, so all partials are visible to it. It resets the counter to 0 for the next call;
+//  3. the last workgroup reads the partials, sums them in split order and stores fp16.
+//
+// Where the partials live (template parameter SC):
+//  * SCOPE_DEVICE: stores and loads at agent scope (global_store/load ... sc1), coherent
+//    between the XCDs' L2 caches. Works for any workgroup placement.
+//  * SCOPE_XCD: stores and loads at workgroup scope (sc0: past the CU's L1, coherent in its
+//    XCD's L2). Correct only when every split of a tile runs on the same XCD. The
+//    dispatcher hands workgroup b of a launch to XCD b mod 8 (checked once per device at
+//    run time, api.cpp); the kernels using this mode give all splits of a tile block ids
+//    that are congruent mod 8. The hand-off then never leaves the L2: measured on the
+//    AWQ GEMV (K=4096, N=14336) 9.2 us per call against 10.4 us for a device-scope flag
+//    protocol, with the same kernels.
+//
+// A __threadfence() is not used: on this part it emits an L2 write-back and invalidate in
+// every wave, which costs more than the weight stream itself.
 #pragma once
 #include "device_common.h"
 #include "launch.h"
 
 namespace w4a16 {
 
-__device__ __forceinline__ void st_coherent(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+constexpr int SCOPE_DEVICE = __HIP_MEMORY_SCOPE_AGENT;
+constexpr int SCOPE_XCD = __HIP_MEMORY_SCOPE_WORKGROUP;
+
+template <int SC>
+__device__ __forceinline__ void st_partial(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, SC);
 }
 
-__device__ __forceinline__ float ld_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Four partials (16-byte aligned) as two 64-bit loads at scope SC.
+template <int SC>
+__device__ __forceinline__ float4_t ld_partial4(const float* p) {
+    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
+    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, SC);
+    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, SC);
+    return float4_t{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
+                    __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32))};
 }
 
 __device__ __forceinline__ void wait_vm_stores() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
 }
 
-// The flags of a tile (FLAG_STRIDE words apart, launch.h).
-__device__ __forceinline__ uint32_t* splitk_flags(uint32_t* base, int tile, int splits) {
-    return base + (size_t)tile * splits * FLAG_STRIDE;
+// The counter of a tile (FLAG_STRIDE words apart: a 256-byte line each, launch.h).
+__device__ __forceinline__ uint32_t* splitk_counter(uint32_t* base, int tile) {
+    return base + (size_t)tile * FLAG_STRIDE;
 }
 
-// Called by every thread after storing its partials with st_coherent. `flags` are the
-// tile's `splits` flags (zero between calls). Returns true in a finishing workgroup.
-__device__ __forceinline__ bool splitk_arrive(uint32_t* flags, int split, int splits,
-                                              int* lds_flag) {
+// Called by every thread after storing its partials with st_partial. Returns true in the
+// workgroup that arrived last.
+__device__ __forceinline__ bool splitk_arrive(uint32_t* counter, int splits, int* lds_flag) {
     wait_vm_stores();
     __syncthreads();
-    if (threadIdx.x < 64) {
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(flags + (size_t)split * FLAG_STRIDE, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            wait_vm_stores();
-        }
-        uint32_t seen = 1u;
-        for (int i = threadIdx.x; i < splits; i += 64)
-            seen &= __hip_atomic_load(flags + (size_t)i * FLAG_STRIDE, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-        const bool all = __all(seen != 0u);
-        if (threadIdx.x == 0) *lds_flag = all ? 1 : 0;
+    if (threadIdx.x == 0) {
+        const uint32_t before =
+            __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = before == (uint32_t)splits - 1u;
+        if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *lds_flag = last ? 1 : 0;
     }
     __syncthreads();
     return *lds_flag != 0;
 }
 
-__device__ __forceinline__ void splitk_clear(uint32_t* flags, int splits) {
-    for (int i = threadIdx.x; i < splits; i += blockDim.x)
-        __hip_atomic_store(flags + (size_t)i * FLAG_STRIDE, 0u, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Four partials (16-byte aligned) as two 64-bit agent-scope loads.
-__device__ __forceinline__ float4_t ld_coherent4(const float* p) {
-    const uint64_t* q = reinterpret_cast<const uint64_t*>(p);
-    const uint64_t a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return float4_t{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
-                    __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32))};
+// Workgroup-id -> (tile, split). XCD mode: a 1-D grid of tiles * splits workgroups; XCD
+// c = b mod 8 owns tiles [c * T/8, (c+1) * T/8) with all their splits, neighbouring tiles
+// on one XCD (they share DRAM pages through its L2: the 128-byte-per-row weight stream
+// of the GEMV reads as fast as 256-byte rows this way). Requires tiles % 8 == 0.
+// Otherwise: blockIdx.x = tile, blockIdx.y = split.
+template <bool XCD>
+__device__ __forceinline__ void tile_of_block(int tiles, int splits, int& tile, int& split) {
+    if constexpr (XCD) {
+        const int b = blockIdx.x, c = b & 7, u = b >> 3;
+        const int t = u / splits;
+        tile = c * (tiles >> 3) + t;
+        split = u - t * splits;
+    } else {
+        tile = blockIdx.x;
+        split = blockIdx.y;
+    }
 }
 
 // Finish columns [n0, n0 + C) of rows [m0, m0 + rows) of an [M, N] output whose partials
-// are ws[split][M][N] (C % 4 == 0, N % 4 == 0). Work is cut into float4 column chunks;
-// when a workgroup has more threads than chunks, the splits are divided into groups summed
-// by different threads and combined through LDS. Each thread issues the loads of a batch
-// of up to FB splits before its first add, so a chunk costs ceil(splits / groups / FB)
-// memory round trips. Summation order: splits in order within a group, groups in order.
+// are ws[split][M][N]. Two layouts of the work, chosen by size:
+//  * at most one entry (row, column) per thread: a thread sums its entry's partials with
+//    scalar loads, FB in flight before the first add (a remainder of fewer than FB splits
+//    in batches of FB/4); spare threads take groups of splits, combined through LDS;
+//  * more entries than threads: float4 column chunks (C % 4 == 0, N % 4 == 0), up to FB4
+//    splits in flight per chunk, groups of splits when threads outnumber chunks.
+// Summation order: splits in order within a group, groups in order.
 constexpr int FB = 16;
+constexpr int FB4 = 16;
 constexpr int FINISH_MAX_THREADS = 512;
 
+template <int SC>
 __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
-                                                   half_t* __restrict__ out, uint32_t* flags,
-                                                   int splits, int M, int N, int m0, int rows,
-                                                   int n0, int C) {
+                                                   half_t* __restrict__ out, int splits, int M,
+                                                   int N, int m0, int rows, int n0, int C) {
     __shared__ float4_t part[FINISH_MAX_THREADS];
     const int T = blockDim.x;   // <= FINISH_MAX_THREADS
+    const size_t stride = (size_t)M * N;
+    if (rows * C <= T) {
+        const int entries = rows * C;
+        const int groups = min(splits, T / entries);
+        const int per = (splits + groups - 1) / groups;
+        const int e = (int)threadIdx.x % entries, gi = (int)threadIdx.x / entries;
+        const int r = e / C, c = e - r * C;
+        const size_t off = (size_t)(m0 + r) * N + n0 + c;
+        float acc = 0.f;
+        if (gi < groups) {
+            const int s0 = gi * per, s1 = min(splits, s0 + per);
+            int sb = s0;
+            for (; sb + FB <= s1; sb += FB) {   // full batches: loads without conditions
+                float v[FB];
+#pragma unroll
+                for (int t = 0; t < FB; ++t)
+                    v[t] = __hip_atomic_load(ws + (size_t)(sb + t) * stride + off, __ATOMIC_RELAXED, SC);
+#pragma unroll
+                for (int t = 0; t < FB; ++t) acc += v[t];
+            }
+            for (; sb < s1; sb += FB / 4) {
+                float v[FB / 4];
+#pragma unroll
+                for (int t = 0; t < FB / 4; ++t)
+                    v[t] = sb + t < s1 ? __hip_atomic_load(ws + (size_t)(sb + t) * stride + off,
+                                                           __ATOMIC_RELAXED, SC)
+                                       : 0.f;
+#pragma unroll
+                for (int t = 0; t < FB / 4; ++t) acc += v[t];
+            }
+        }
+        if (groups > 1) {
+            reinterpret_cast<float*>(part)[threadIdx.x] = acc;
+            __syncthreads();
+            if (gi == 0)
+                for (int g = 1; g < groups; ++g) acc += reinterpret_cast<float*>(part)[g * entries + e];
+        }
+        if (gi == 0) out[off] = (half_t)acc;
+        return;
+    }
     const int cpr = C / 4;                       // chunks per row
     const int chunks = rows * cpr;
     const int groups = chunks >= T ? 1 : min(splits, T / chunks);
     const int per = (splits + groups - 1) / groups;
-    const size_t stride = (size_t)M * N;
     const int span = groups == 1 ? T : chunks;   // chunks handled per pass
     for (int c0 = 0; c0 < chunks; c0 += span) {
         const int ch = c0 + (int)threadIdx.x % span;
@@ -109,13 +163,13 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
             const int r = ch / cpr, c = ch - r * cpr;
             off = (size_t)(m0 + r) * N + n0 + 4 * c;
             const int s0 = gi * per, s1 = min(splits, s0 + per);
-            for (int sb = s0; sb < s1; sb += FB) {
-                float4_t v[FB];
+            for (int sb = s0; sb < s1; sb += FB4) {
+                float4_t v[FB4];
 #pragma unroll
-                for (int t = 0; t < FB; ++t)
-                    if (sb + t < s1) v[t] = ld_coherent4(ws + (size_t)(sb + t) * stride + off);
+                for (int t = 0; t < FB4; ++t)
+                    if (sb + t < s1) v[t] = ld_partial4<SC>(ws + (size_t)(sb + t) * stride + off);
 #pragma unroll
-                for (int t = 0; t < FB; ++t)
+                for (int t = 0; t < FB4; ++t)
                     if (sb + t < s1) acc += v[t];
             }
         }
@@ -133,13 +187,12 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
             *reinterpret_cast<u32x2*>(out + off) = u32x2{as_u32(lo), as_u32(hi)};
         }
     }
-    splitk_clear(flags, splits);
 }
 
-template <int M>
+template <int M, int SC>
 __device__ __forceinline__ void splitk_finish(const float* __restrict__ ws, half_t* __restrict__ out,
-                                              uint32_t* flags, int splits, int N, int n0, int C) {
-    splitk_finish_rows(ws, out, flags, splits, M, N, 0, M, n0, C);
+                                              int splits, int N, int n0, int C) {
+    splitk_finish_rows<SC>(ws, out, splits, M, N, 0, M, n0, C);
 }
 
 }  // namespace w4a16
