@@ -243,11 +243,8 @@ def extras(torch, pkg, dev, stream, args):
         sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
         x = torch.randn((M, K), device=dev, generator=gen).half()
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        if M <= 64:
-            ms = time_graphs(torch, pkg, x, sets, out, fmt, G, calls, 10, stream, g_idx=g_idx)[0]
-        else:
-            ms = time_direct(torch, lambda i: pkg.gemm(x, *sets[i % n_sets], fmt=fmt, group_size=G,
-                                                       g_idx=g_idx, out=out), calls, stream)
+        # graph replays for every size: steady-state clocks, no host launch gaps
+        ms = time_graphs(torch, pkg, x, sets, out, fmt, G, calls, 10, stream, g_idx=g_idx)[0]
         nbytes = algorithmic_bytes(fmt, M, K, N, G)
         tfl = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         res[tag] = {"kernel": pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None),
@@ -269,8 +266,8 @@ def extras(torch, pkg, dev, stream, args):
         gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 20, 500,
                   g_idx=g_idx)
         gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 20, 500)
-    gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 10)
-    gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 10)
+    gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
+    gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
 
     # config 4: fused MoE layer, T=512, 8 experts, top-2, K=4096, I=14336, GPTQ G=128
     T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
@@ -291,7 +288,7 @@ def extras(torch, pkg, dev, stream, args):
         ws = torch.empty(pkg.lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, bm),
                          dtype=torch.uint8, device=dev)
         ms = time_direct(torch, lambda i: pkg.fused_moe(x, logits, w13, w2, topk=topk, block_m=bm,
-                                                        out=out, workspace=ws), 10, stream)
+                                                        out=out, workspace=ws), 50, stream, warm=5)
         res[f"c4_fused_moe_block_m{bm}"] = {
             "ms_per_layer": round(ms, 3), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
