@@ -145,6 +145,24 @@ def test_prefill_full_size_sampled_rows(torch_cuda, orc, K, N):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N", [(300, 640, 384), (512, 1024, 128), (2048, 1024, 4096)])
+def test_prefill_narrow_tiles(torch_cuda, orc, fmt, M, K, N):
+    """256-row x 128-column prefill tiles (two dequantised columns per thread), chosen when
+    N is a multiple of 128 but not of 224 or 256, or when they balance the CUs best."""
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2300 + M + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, 128) == "prefill"
+    y = _run_gemm(torch_cuda, p)
+    if M <= 512:
+        assert_parity(y, _oracle(orc, p), what=f"prefill 128-wide fmt={fmt} M={M} N={N}")
+    else:
+        rows = np.random.default_rng(4).choice(M, 16, replace=False).astype(np.int32)
+        rows[:2] = [0, M - 1]
+        ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows)
+        assert_parity(y[rows], ref.astype(np.float64), what=f"prefill 128-wide fmt={fmt} M={M}")
+
+
 def test_mfma_split_k_deterministic(torch_cuda, orc):
     P = pkg()
     p = Problem(AWQ, M=8, K=4096, N=1024, G=128, seed=2200)
@@ -157,7 +175,7 @@ def test_mfma_split_k_deterministic(torch_cuda, orc):
 # ------------------------------------------------------------------ strided / generic
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
-@pytest.mark.parametrize("M,K,N,G", [(16, 384, 264, 128), (64, 960, 384, 64), (37, 384, 200, 128),
+@pytest.mark.parametrize("M,K,N,G", [(16, 384, 264, 128), (64, 960, 392, 64), (37, 384, 200, 128),
                                      (300, 640, 136, 64)])
 def test_strided_kernel_via_op(torch_cuda, orc, fmt, M, K, N, G):
     """Shapes the tiled kernels do not take (N not a multiple of their strip, K not of 128)."""

@@ -444,128 +444,89 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     };
 
     // ---- dequantisation into the fp16 B tile: thread t owns k chunk kq = t / 64 (8 k) and
-    // columns 8 bw + 4 h + 0..3, bw = t % 32, h = (t / 32) % 2 (lanes 8 columns apart)
-    const int bw = t & 31, hh = (t >> 5) & 1, kq = t >> 6;
-    auto dequant_b = [&](int slot, int buf) {
-        const char* src = Raw + slot * RAW_ST;
-        half_t* B = Bs + buf * B_ST + kq * 256 * 8;
-        const uint32_t sv2[2] = {
-            reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh],
-            reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh + 1]};
-        uint32_t zw = 0u;
-        if constexpr (FMT != FMT_GPTQ_SYM) zw = reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S)[bw];
-        u32x4 col[4];
-        if constexpr (FMT == FMT_AWQ) {
-            // rows 8 kq .. 8 kq + 7 of word column bw; columns 4 hh .. 4 hh + 3 of the word
-            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src) + 8 * kq * 32 + bw;
-            uint32_t w8[8];
-#pragma unroll
-            for (int r = 0; r < 8; ++r) w8[r] = wp[32 * r];
-            half2_t hz[4], hs[4];
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int cc = 4 * hh + c;
-                const uint32_t zb = 0x6400u + (uint32_t)nib(zw, awq_slot(cc));
-                hz[c] = as_h2(zb | (zb << 16));
-                hs[c] = as_h2(perm(sv2[c >> 1], sv2[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
-            }
-            half2_t pr[4][4];
-#pragma unroll
-            for (int rp = 0; rp < 4; ++rp) {
-                const uint32_t a = w8[2 * rp], b = w8[2 * rp + 1];
-                // slots of columns 4 hh + c: hh = 0 -> 0, 4, 1, 5 ; hh = 1 -> 2, 6, 3, 7
-                const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
-                const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
-                const int sh = 8 * hh;                          // slots 2hh, 2hh+1 (and +4)
-                pr[rp][0] = deq2(nib_pair(p0 >> sh), hz[0], hs[0]);
-                pr[rp][1] = deq2(nib_pair(p1 >> sh), hz[1], hs[1]);
-                pr[rp][2] = deq2(nib_pair(p0 >> (sh + 4)), hz[2], hs[2]);
-                pr[rp][3] = deq2(nib_pair(p1 >> (sh + 4)), hz[3], hs[3]);
-            }
-#pragma unroll
-            for (int c = 0; c < 4; ++c) col[c] = pack8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
-        } else {
-            // packed row kq (8 k) of columns 8 bw + 4 hh + 0..3
-            const u32x4 w4 = *reinterpret_cast<const u32x4*>(src + kq * 1024 + 4 * (8 * bw + 4 * hh));
-            const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                uint32_t z;
-                if constexpr (FMT == FMT_GPTQ_SYM) z = 8u;
-                else z = (uint32_t)(nib(zw, 4 * hh + c) + p.zero_offset);
-                const uint32_t zb = 0x6400u + z;
-                const half2_t hz = as_h2(zb | (zb << 16));
-                const half2_t hs = as_h2(perm(sv2[c >> 1], sv2[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
-                const uint32_t w = ws[c];
-                const uint32_t q0 = as_u32(deq2(nib_pair(w), hz, hs));         // k0, k4
-                const uint32_t q1 = as_u32(deq2(nib_pair(w >> 4), hz, hs));    // k1, k5
-                const uint32_t q2 = as_u32(deq2(nib_pair(w >> 8), hz, hs));    // k2, k6
-                const uint32_t q3 = as_u32(deq2(nib_pair(w >> 12), hz, hs));   // k3, k7
-                col[c] = u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
-                               perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<u32x4*>(B + 8 * bpos(8 * bw + 4 * hh + c)) = col[c];
-    };
+    // DQC columns of one 8-column word group bw: columns 8 bw + DQC hh + 0..DQC-1. A tile of
+    // 256 (or 224) columns gives each thread 4 columns (bw = t % 32, hh = (t / 32) % 2); a
+    // 128-column tile 2 (bw = t % 16, hh = (t / 16) % 4), so no thread dequantises columns
+    // outside the tile.
+    constexpr int DQC = BN <= 128 ? 2 : 4;
+    constexpr int DQW = 8 / DQC;   // column groups per word
+    const int bw = DQC == 4 ? (t & 31) : (t & 15);
+    const int hh = DQC == 4 ? ((t >> 5) & 1) : ((t >> 4) & 3);
+    const int kq = t >> 6;
+    static_assert(BN <= 128 || BN > 192, "tile width");
+    (void)DQW;
 
-    // ---- the same dequantisation in three parts, so that its VALU work can be placed
-    // between the MFMAs of a stage: raw reads, per-column arithmetic, LDS writes
-    struct DqRaw { uint32_t sv2[2]; uint32_t zw; uint32_t w[8]; };
+    // The dequantisation comes in three parts, so that its VALU work can be placed between
+    // the MFMAs of a stage: raw reads from the ring slot, per-column arithmetic, LDS writes.
+    struct DqRaw { uint32_t sv[2]; uint32_t zw; uint32_t w[8]; };
     auto dq_load = [&](int slot) {
         DqRaw d;
         const char* src = Raw + slot * RAW_ST;
-        d.sv2[0] = reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh];
-        d.sv2[1] = reinterpret_cast<const uint32_t*>(src + RAW_W)[4 * bw + 2 * hh + 1];
+        const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(src + RAW_W);
+        if constexpr (DQC == 4) { d.sv[0] = sc32[4 * bw + 2 * hh]; d.sv[1] = sc32[4 * bw + 2 * hh + 1]; }
+        else { d.sv[0] = sc32[4 * bw + hh]; d.sv[1] = 0u; }
         d.zw = 0u;
         if constexpr (FMT != FMT_GPTQ_SYM) d.zw = reinterpret_cast<const uint32_t*>(src + RAW_W + RAW_S)[bw];
         if constexpr (FMT == FMT_AWQ) {
+            // rows 8 kq .. 8 kq + 7 of word column bw
             const uint32_t* wp = reinterpret_cast<const uint32_t*>(src) + 8 * kq * 32 + bw;
 #pragma unroll
             for (int r = 0; r < 8; ++r) d.w[r] = wp[32 * r];
-        } else {
+        } else if constexpr (DQC == 4) {
+            // packed row kq (8 k) of columns 8 bw + 4 hh + 0..3
             const u32x4 w4 = *reinterpret_cast<const u32x4*>(src + kq * 1024 + 4 * (8 * bw + 4 * hh));
             d.w[0] = w4.x; d.w[1] = w4.y; d.w[2] = w4.z; d.w[3] = w4.w;
+        } else {
+            const u32x2 w2 = *reinterpret_cast<const u32x2*>(src + kq * 1024 + 4 * (8 * bw + 2 * hh));
+            d.w[0] = w2.x; d.w[1] = w2.y;
         }
         return d;
     };
-    // column c (0..3) of the thread's four
+    // column c (0 .. DQC-1) of the thread's columns, as the 8 k of one B-operand chunk
     auto dq_col = [&](const DqRaw& d, int c) -> u32x4 {
-        const half2_t hs = as_h2(perm(d.sv2[c >> 1], d.sv2[c >> 1], (c & 1) ? 0x07060706u : 0x05040504u));
+        const int cc = DQC * hh + c;   // column within its 8-column group
+        const uint32_t sw = DQC == 4 ? d.sv[c >> 1] : d.sv[0];
+        const half2_t hs = as_h2(perm(sw, sw, (c & 1) ? 0x07060706u : 0x05040504u));
         if constexpr (FMT == FMT_AWQ) {
-            const int cc = 4 * hh + c;
-            const uint32_t zb = 0x6400u + (uint32_t)nib(d.zw, awq_slot(cc));
+            const int slot = awq_slot(cc);
+            const uint32_t zb = 0x6400u + (uint32_t)nib(d.zw, slot);
             const half2_t hz = as_h2(zb | (zb << 16));
             half2_t pr[4];
 #pragma unroll
             for (int rp = 0; rp < 4; ++rp) {
+                // slots 0-3 (or 4-7) of rows 2 rp and 2 rp + 1 in the low and high halves
                 const uint32_t a = d.w[2 * rp], b = d.w[2 * rp + 1];
-                const uint32_t pp = perm(b, a, (c & 1) ? 0x07060302u : 0x05040100u);
-                const int sh = 8 * hh + ((c & 2) ? 4 : 0);
-                pr[rp] = deq2(nib_pair(pp >> sh), hz, hs);
+                const uint32_t pp = perm(b, a, (slot & 4) ? 0x07060302u : 0x05040100u);
+                pr[rp] = deq2(nib_pair(pp >> (4 * (slot & 3))), hz, hs);
             }
             return pack8(pr[0], pr[1], pr[2], pr[3]);
         } else {
             uint32_t z;
             if constexpr (FMT == FMT_GPTQ_SYM) z = 8u;
-            else z = (uint32_t)(nib(d.zw, 4 * hh + c) + p.zero_offset);
+            else z = (uint32_t)(nib(d.zw, cc) + p.zero_offset);
             const uint32_t zb = 0x6400u + z;
             const half2_t hz = as_h2(zb | (zb << 16));
             const uint32_t w = d.w[c];
-            const uint32_t q0 = as_u32(deq2(nib_pair(w), hz, hs));
-            const uint32_t q1 = as_u32(deq2(nib_pair(w >> 4), hz, hs));
-            const uint32_t q2 = as_u32(deq2(nib_pair(w >> 8), hz, hs));
-            const uint32_t q3 = as_u32(deq2(nib_pair(w >> 12), hz, hs));
+            const uint32_t q0 = as_u32(deq2(nib_pair(w), hz, hs));         // k0, k4
+            const uint32_t q1 = as_u32(deq2(nib_pair(w >> 4), hz, hs));    // k1, k5
+            const uint32_t q2 = as_u32(deq2(nib_pair(w >> 8), hz, hs));    // k2, k6
+            const uint32_t q3 = as_u32(deq2(nib_pair(w >> 12), hz, hs));   // k3, k7
             return u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
                          perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
         }
     };
-    auto dq_store = [&](int buf, const u32x4 (&col)[4]) {
+    auto dq_store = [&](int buf, const u32x4 (&col)[DQC]) {
         half_t* B = Bs + buf * B_ST + kq * 256 * 8;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            *reinterpret_cast<u32x4*>(B + 8 * bpos(8 * bw + 4 * hh + c)) = col[c];
+        for (int c = 0; c < DQC; ++c)
+            *reinterpret_cast<u32x4*>(B + 8 * bpos(8 * bw + DQC * hh + c)) = col[c];
+    };
+    auto dequant_b = [&](int slot, int buf) {
+        const DqRaw d = dq_load(slot);
+        u32x4 col[DQC];
+#pragma unroll
+        for (int c = 0; c < DQC; ++c) col[c] = dq_col(d, c);
+        dq_store(buf, col);
     };
 
     float4_t acc[RB][CB];
@@ -584,7 +545,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         const DqRaw d = dq_load(raw_slot);
         const half_t* A = As + a_slot * A_ST + aoff_l;
         const half_t* B = Bs + buf * B_ST;
-        u32x4 col[4];
+        u32x4 col[DQC];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int kc = 4 * ks + kb;
@@ -600,8 +561,8 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
                 for (int c = 0; c < CB; ++c)
                     acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[r], bf[c], acc[r][c], 0, 0, 0);
-            col[2 * ks] = dq_col(d, 2 * ks);
-            col[2 * ks + 1] = dq_col(d, 2 * ks + 1);
+#pragma unroll
+            for (int c = ks * DQC / 2; c < (ks + 1) * DQC / 2; ++c) col[c] = dq_col(d, c);
             // place the dequantisation arithmetic between the MFMAs: 1 MFMA, 2 VALU
             // (measured 229 -> 216 us at M=2048, K=4096, N=14336 against MFMAs then
             // dequantisation; 1 or 3 VALU per MFMA were slower)
@@ -668,12 +629,13 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
     if (dma_ok(N, K, G, M)) {
         // tile minimising (rounds of tiles over the CUs) x (tile area); ties to larger BM
         long long best = -1;
-        for (int bn : {256, 224}) {
+        for (int bn : {256, 224, 128}) {
             if (N % bn) continue;
             for (int bm : {256, 128}) {
+                if (bn == 128 && bm != 256) continue;   // 128-wide tiles only with 256 rows
                 const long long tiles = (long long)(N / bn) * ((M + bm - 1) / bm);
                 const long long cost = (tiles + num_cus - 1) / num_cus * bm * bn;
-                if (best < 0 || cost < best) {
+                if (best < 0 || cost < best || (cost == best && bm > s.bm)) {
                     best = cost; s.bm = bm; s.bn = bn;
                 }
             }
@@ -724,6 +686,7 @@ static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, si
         else launch_dma_t<FMT, 128, 256, true>(p, grid, lds, st);
     } else {
         if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false>(p, grid, lds, st);
+        else if (bm == 256 && bn == 128) launch_dma_t<FMT, 256, 128, false>(p, grid, lds, st);
         else if (bm == 256) launch_dma_t<FMT, 256, 256, false>(p, grid, lds, st);
         else if (bn == 224) launch_dma_t<FMT, 128, 224, false>(p, grid, lds, st);
         else launch_dma_t<FMT, 128, 256, false>(p, grid, lds, st);
