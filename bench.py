@@ -152,15 +152,25 @@ def cpu_model() -> str:
 
 # ----------------------------------------------------------------------------- traffic
 
+# workloads a counter run (--pmc-child) can drive: the headline, and config 3's two shapes
+PMC_WORKLOADS = {
+    "headline": HEADLINE,
+    "c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128),
+    "c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128),
+}
+
+
 def pmc_child(args) -> int:
-    """Workload profiled by the counter passes: PMC_WARM + PMC_MEASURED headline launches
-    over the rotated weight sets, then three launches of the calibration kernel."""
+    """Workload profiled by the counter passes: PMC_WARM + PMC_MEASURED launches of the chosen
+    workload (--pmc-workload; the headline by default) over rotated weight sets, then three
+    launches of the calibration kernel."""
     import torch
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
-    fmt, M, K, N, G = HEADLINE
-    sets = make_weight_sets(torch, fmt, K, N, G, args.sets, dev, seed=0x5EED0001)
+    fmt, M, K, N, G = PMC_WORKLOADS[args.pmc_workload]
+    n_sets = args.sets if M <= 64 else 2
+    sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=0x5EED0001)
     x = torch.randn((M, K), device=dev).half()
     out = torch.empty((M, N), dtype=torch.float16, device=dev)
     for i in range(PMC_WARM + PMC_MEASURED):
@@ -308,6 +318,8 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=15.0)
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--pmc-workload", default="headline", choices=sorted(PMC_WORKLOADS),
+                    help="workload of a --pmc-child run (for counter profiles)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
