@@ -193,7 +193,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
 
     if (kernel == W4A16_KERNEL_SKINNY) {
-        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr);
+        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd_placement());
         SkinnyParams p{};
         p.g_idx = g_idx;
         p.x = static_cast<const half_t*>(x);
@@ -202,7 +202,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
-        p.splits = s.splits; p.steps_per_wave = s.steps_per_wave;
+        p.splits = s.splits; p.steps_per_wave = s.steps_per_wave; p.col_tiles = s.col_tiles;
         if (s.splits > 1) {
             if ((size_t)s.col_tiles > SPLITK_MAX_TILES)
                 return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");

@@ -34,7 +34,7 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }
 }  // namespace
 
-template <int FMT, int BM, int CPL, int PF, bool GIDX>
+template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD>
 __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     constexpr int RB = BM / 16;
@@ -48,7 +48,9 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kb = lane >> 4;
-    const int ct = blockIdx.x, split = blockIdx.y;
+    int ct, split;
+    tile_of_block<XCD>(p.col_tiles, p.splits, ct, split);
+    constexpr int SC = XCD ? SCOPE_XCD : SCOPE_DEVICE;
     const int n0 = ct * WN;
     const int nl = n0 + CPL * j;              // first output column of this lane
     const int NW = p.N >> 3;
@@ -256,26 +258,27 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         const float v = red[0][m][col] + red[1][m][col] + red[2][m][col] + red[3][m][col];
         const size_t off = (size_t)m * p.N + n0 + col;
         if (p.splits == 1) p.out[off] = (half_t)v;
-        else st_partial<SCOPE_DEVICE>(p.ws + (size_t)split * p.M * p.N + off, v);
+        else st_partial<SC>(p.ws + (size_t)split * p.M * p.N + off, v);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.flags, ct), p.splits, &flag))
-        splitk_finish_rows<SCOPE_DEVICE>(p.ws, p.out, p.splits, p.M, p.N, 0, p.M, n0, WN);
+        splitk_finish_rows<SC>(p.ws, p.out, p.splits, p.M, p.N, 0, p.M, n0, WN);
 }
 
 // ------------------------------------------------------------------ host side
 
-SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx) {
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx,
+                         bool xcd_placement) {
     SkinnyShape s{};
     if (M < 1 || M > 64 || K % 128) return s;
     // without g_idx a k32 step lies in one group; with it the group comes from the table
     if (gidx ? (fmt == FMT_AWQ || G < 1) : (G % 32 || K % G)) return s;
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     const bool awq = fmt == FMT_AWQ;
-    // narrowest strip (most workgroups) the format supports; wide strips at BM=64 would
-    // not fit the cross-wave reduction buffer
+    // 4 columns per lane where N allows (the wider strip re-reads the activations from L2
+    // half as often as 2; 8 would not fit the cross-wave reduction buffer at BM=64)
     int cpl = 0;
-    for (int c : {2, 4, 8}) {
+    for (int c : {4, 2, 8}) {
         if (awq && c < 4) continue;
         if (s.bm == 64 && c > 4) continue;
         if (N % (16 * c) == 0) { cpl = c; break; }
@@ -288,35 +291,42 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     s.cpl = cpl;
     s.col_tiles = N / (16 * cpl);
     // split K across workgroups until ~2 workgroups per CU, keeping the fp32 partials
-    // (splits * M * N * 4 bytes) under a quarter of the packed weights (K * N / 2 bytes)
+    // (splits * M * N * 4 bytes) under a quarter of the packed weights (K * N / 2 bytes) and
+    // workgroups x M near 12K (measured optimum at K=4096, N=6144: 8 splits at M=16, 4 at
+    // M=32, 2 at M=64; more splits cost more in partial traffic than they gain in width)
     int splits = 1;
     while (s.col_tiles * splits < 2 * num_cus && K % (128 * 2 * splits) == 0 &&
-           2 * splits * 32 * M <= K)
+           2 * splits * 32 * M <= K && (long long)s.col_tiles * 2 * splits * M <= 12288)
         splits *= 2;
     s.splits = splits;
     s.steps_per_wave = K / (128 * splits);
+    s.xcd = xcd_placement && splits > 1 && s.col_tiles % 8 == 0;
     s.ok = true;
     return s;
 }
 
-template <int FMT, int BM, int CPL>
-static hipError_t launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+template <int FMT, int BM, int CPL, bool XCD>
+static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     constexpr int PF = (FMT == FMT_AWQ || CPL >= 8) ? 3 : 4;
+    const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     if constexpr (FMT != FMT_AWQ) {
         if (p.g_idx) {
             // static reduction buffer plus the group table may exceed the default 64 KiB
             static const hipError_t attr = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true>),
+                reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true, XCD>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
             if (attr != hipSuccess) return attr;
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true>), dim3(s.col_tiles, s.splits),
-                               dim3(256), s.lds, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(256), s.lds, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false>), dim3(s.col_tiles, s.splits),
-                       dim3(256), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(256), 0, st, p);
     return hipGetLastError();
+}
+
+template <int FMT, int BM, int CPL>
+static hipError_t launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    return s.xcd ? launch_x<FMT, BM, CPL, true>(p, s, st) : launch_x<FMT, BM, CPL, false>(p, s, st);
 }
 
 template <int FMT, int BM>

@@ -95,11 +95,12 @@ struct SkinnyParams {
     float* ws;
     uint32_t* flags;
     const int32_t* g_idx;   // act-order groups [K], or null
-    int M, N, K, G, zero_offset, splits, steps_per_wave;
+    int M, N, K, G, zero_offset, splits, steps_per_wave, col_tiles;
 };
 
 struct SkinnyShape {
     bool ok;
+    bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     int bm, cpl, col_tiles, splits, steps_per_wave;
     size_t lds;             // dynamic LDS bytes (act-order group table)
 };
@@ -107,7 +108,8 @@ struct SkinnyShape {
 // Largest act-order group table a workgroup stages in LDS.
 constexpr size_t SKINNY_GIDX_MAX_LDS = 64 * 1024;
 
-SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx = false);
+SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx = false,
+                         bool xcd_placement = false);
 hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st);
 
 // Generic strided GEMM with the reference kernels' parameter list

@@ -97,7 +97,8 @@ __device__ __forceinline__ void tile_of_block(int tiles, int splits, int& tile, 
 //    scalar loads, FB in flight before the first add (a remainder of fewer than FB splits
 //    in batches of FB/4); spare threads take groups of splits, combined through LDS;
 //  * more entries than threads: float4 column chunks (C % 4 == 0, N % 4 == 0), up to FB4
-//    splits in flight per chunk, groups of splits when threads outnumber chunks.
+//    splits in flight per chunk (two chunks at a time when there are at least two per thread
+//    and at most FB4/2 splits), groups of splits when threads outnumber chunks.
 // Summation order: splits in order within a group, groups in order.
 constexpr int FB = 16;
 constexpr int FB4 = 16;
@@ -154,6 +155,32 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
     const int groups = chunks >= T ? 1 : min(splits, T / chunks);
     const int per = (splits + groups - 1) / groups;
     const int span = groups == 1 ? T : chunks;   // chunks handled per pass
+    if (groups == 1 && chunks >= 2 * T && splits <= FB4 / 2) {
+        // two chunks per thread per batch: the loads of both are in flight together
+        for (int c0 = 0; c0 < chunks; c0 += 2 * T) {
+            const int cha = c0 + (int)threadIdx.x, chb = cha + T;
+            const bool okb = chb < chunks;
+            const size_t offa = (size_t)(m0 + cha / cpr) * N + n0 + 4 * (cha % cpr);
+            const size_t offb = okb ? (size_t)(m0 + chb / cpr) * N + n0 + 4 * (chb % cpr) : offa;
+            float4_t va[FB4 / 2], vb[FB4 / 2];
+#pragma unroll
+            for (int t = 0; t < FB4 / 2; ++t)
+                if (t < splits) {
+                    va[t] = ld_partial4<SC>(ws + (size_t)t * stride + offa);
+                    vb[t] = ld_partial4<SC>(ws + (size_t)t * stride + offb);
+                }
+            float4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < FB4 / 2; ++t)
+                if (t < splits) { a += va[t]; b += vb[t]; }
+            *reinterpret_cast<u32x2*>(out + offa) =
+                u32x2{as_u32(half2_t{(half_t)a[0], (half_t)a[1]}), as_u32(half2_t{(half_t)a[2], (half_t)a[3]})};
+            if (okb)
+                *reinterpret_cast<u32x2*>(out + offb) =
+                    u32x2{as_u32(half2_t{(half_t)b[0], (half_t)b[1]}), as_u32(half2_t{(half_t)b[2], (half_t)b[3]})};
+        }
+        return;
+    }
     for (int c0 = 0; c0 < chunks; c0 += span) {
         const int ch = c0 + (int)threadIdx.x % span;
         const int gi = (int)threadIdx.x / span;
