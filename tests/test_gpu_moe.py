@@ -156,3 +156,64 @@ def test_fused_moe_config4_sampled_tokens(torch_cuda, orc):
     ref = orc.moe_forward(np.ascontiguousarray(x[toks]), np.ascontiguousarray(ids[toks]),
                           np.ascontiguousarray(w[toks]), w13d, w2d, inter=I)
     assert_parity(y[toks], ref.astype(np.float64), what="config 4 sampled tokens")
+
+
+def _layer_by_pieces(P, x, logits, w13, w2, topk, fmt, G, block_m):
+    """The layer composed from the public pieces: route, align, grouped GEMM over block_m
+    blocks, silu*mul, grouped GEMM, weighted sum."""
+    import torch
+    T, K = x.shape
+    E = logits.shape[1]
+    I = w2[1].shape[1] * G
+    ids, w = P.moe_route(logits, topk)
+    sorted_ids, expert_ids, npp = P.moe_align(ids, E, block_m)
+    h = P.moe_gemm(x, topk, *w13, sorted_ids, expert_ids, npp, T * topk, 2 * I, K, fmt=fmt,
+                   group_size=G, block_m=block_m)
+    a = torch.empty((T * topk, I), dtype=torch.float16, device=x.device)
+    P.fused_silu_mul_interleaved_f16(h, a, I, T * topk * I)
+    yp = P.moe_gemm(a, 1, *w2, sorted_ids, expert_ids, npp, T * topk, K, I, fmt=fmt,
+                    group_size=G, block_m=block_m)
+    return P.moe_sum(yp, w, T, topk, K)
+
+
+# The fused layer computes its grouped GEMMs over expert tiles (an expert's rows in one tile
+# of 64/128/192/256 rows, 256/224/128 columns, chosen from the mean rows per expert and the CU
+# count). Every pair row goes through the same arithmetic as in the block_m-block GEMM, so
+# the layer must equal the composition of the public pieces bit for bit. Cases, with the
+# tiles they take on a 256-CU MI355X: (T, E, topk, K, I, skew, fmt, block_m)
+TILE_CASES = [
+    (512, 8, 2, 256, 1792, None, GPTQ, 64),     # 192 x 224 (gate/up), 192 x 128 (down)
+    (512, 8, 2, 256, 4096, None, AWQ, 128),     # 192 x 256, 192 x 128
+    (512, 8, 2, 256, 256, 3, GPTQ, 64),         # expert 3 takes ~512 rows: 3 tiles of it
+    (300, 8, 2, 512, 256, 0, AWQ, 64),          # 128-row tiles, expert 0 in 3 of them
+    (1024, 4, 2, 256, 512, None, SYM, 128),     # 256-row tiles, two per expert
+    (48, 4, 2, 256, 256, None, AWQ, 64),        # 64-row tiles
+    (40, 64, 2, 256, 256, None, GPTQ, 64),      # 64-row tiles, most experts without tokens
+]
+
+
+@pytest.mark.parametrize("case", TILE_CASES, ids=[f"T{c[0]}_E{c[1]}_I{c[4]}_skew{c[5]}"
+                                                  for c in TILE_CASES])
+def test_fused_layer_expert_tiles_equal_block_composition(torch_cuda, case):
+    torch = torch_cuda
+    T, E, topk, K, I, skew, fmt, bm = case
+    P = pkg()
+    g = np.random.default_rng(80 + T + I)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    if skew is not None:
+        logits[:, skew] += 4.0          # nearly every token picks this expert
+    G = 128
+    w13 = tuple(to_dev(a) for a in stacked_weights(fmt, E, K, 2 * I, G, 81))
+    w2 = tuple(to_dev(a) for a in stacked_weights(fmt, E, I, K, G, 82))
+    if fmt == SYM:
+        w13 = (w13[0], w13[1], None)
+        w2 = (w2[0], w2[1], None)
+    xd, ld = to_dev(x), to_dev(logits)
+    y = P.fused_moe(xd, ld, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G, block_m=bm)
+    ref = _layer_by_pieces(P, xd, ld, w13, w2, topk, FMT_NAME[fmt], G, 64)
+    torch.cuda.synchronize()
+    got, want = y.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16)
+    diff = np.argwhere(got != want)
+    assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
+    assert np.all(np.isfinite(y.cpu().numpy()))

@@ -472,8 +472,8 @@ W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk
 
 namespace {
 struct MoeLayout {
-    size_t ids, weights, sorted, experts, npp, h, a, yp, total;
-    int32_t capacity;
+    size_t ids, weights, sorted, experts, npp, tiles, ntiles, h, a, yp, total;
+    int32_t capacity, max_tiles;
 };
 size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, int32_t block_m) {
@@ -487,11 +487,43 @@ MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, i
     L.sorted = off; off = up256(off + cap * 4);
     L.experts = off; off = up256(off + cap / block_m * 4);
     L.npp = off; off = up256(off + 4);
+    L.max_tiles = moe_max_tiles((int)P, E, 64);   // bound for every tile height >= 64
+    L.tiles = off; off = up256(off + (size_t)L.max_tiles * 16);
+    L.ntiles = off; off = up256(off + 4);
     L.h = off; off = up256(off + (size_t)P * 2 * I * 2);
     L.a = off; off = up256(off + (size_t)P * I * 2);
     L.yp = off; off = up256(off + (size_t)P * K * 2);
     L.total = off;
     return L;
+}
+
+// Expert-tile shape of the fused layer's grouped GEMMs. Tile height: the smallest of 64,
+// 128, 192, 256 rows holding 1.25x the mean rows per expert, so that one tile usually covers
+// all of an expert's tokens and its weights are dequantised once per column tile. Tile
+// width: the fewest rounds of workgroups over the CUs times the width (ties to the wider
+// tile), for the tile count a balanced routing gives; 64-row tiles come 256 wide only.
+struct MoeTiles { int bm, bn13, bn2; };
+int moe_tile_bn(int N, int bm, int est_tiles, int cus) {
+    if (bm == 64) return 256;
+    int best = 0;
+    long long best_cost = 0;
+    for (int bn : {256, 224, 128}) {
+        if (N % bn) continue;
+        const long long wgs = (long long)est_tiles * (N / bn);
+        const long long cost = (wgs + cus - 1) / cus * bn;
+        if (!best || cost < best_cost) { best = bn; best_cost = cost; }
+    }
+    return best;
+}
+MoeTiles moe_tiles(int P, int E, int K, int I, int cus) {
+    const double want = 1.25 * P / E;
+    MoeTiles t{};
+    t.bm = want <= 64 ? 64 : want <= 128 ? 128 : want <= 192 ? 192 : 256;
+    const int per_expert = (int)((P / E + t.bm - 1) / t.bm);
+    const int est = E * (per_expert > 0 ? per_expert : 1);
+    t.bn13 = moe_tile_bn(2 * I, t.bm, est, cus);
+    t.bn2 = moe_tile_bn(K, t.bm, est, cus);
+    return t;
 }
 }  // namespace
 
@@ -511,7 +543,8 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
     if (!x || !router_logits || !workspace || !out)
         return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
     if (int rc = check_moe_dims(T, E, topk)) return rc;
-    if (I < 1 || K < 1) return fail(W4A16_ERR_INVALID_ARG, "bad sizes (K=%d I=%d)", K, I);
+    if (I < 1 || K < 1 || block_m < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (K=%d I=%d block_m=%d)", K, I, block_m);
     const MoeLayout L = moe_layout(T, E, topk, I, K, block_m);
     if (workspace_bytes < L.total)
         return fail(W4A16_ERR_INVALID_ARG, "workspace too small (%zu < %zu bytes)", workspace_bytes,
@@ -527,10 +560,61 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
     void* a = ws + L.a;
     void* yp = ws + L.yp;
     const int32_t P = T * topk;
+    hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = w4a16_moe_route(stream, router_logits, T, E, topk, renormalize, ids, wts);
-    if (!rc) rc = w4a16_moe_align(stream, ids, P, E, block_m, L.capacity, sorted, experts, npp);
+    if (rc) return rc;
+    // Expert tiles (one tile per expert's rows, whatever block_m padded them to) when both
+    // GEMMs take the pipelined kernel; else the grouped GEMM over block_m blocks.
+    const MoeTiles mt = moe_tiles(P, E, K, I, device_cus());
+    const int64_t n13 = 2 * (int64_t)I;
+    if (n13 <= INT32_MAX && mt.bn13 && mt.bn2 && moe_tiles_supported((int)n13, K, G, T, mt.bn13) &&
+        moe_tiles_supported(K, I, G, P, mt.bn2)) {
+        if (int e = check_gemm_args(fmt, x, w13_qweight, w13_scales, w13_qzeros, h, 1, (int)n13, K, G))
+            return e;
+        if (int e = check_gemm_args(fmt, a, w2_qweight, w2_scales, w2_qzeros, yp, 1, K, I, G))
+            return e;
+        if (int e = check_zero_offset(fmt, zero_offset)) return e;
+        if (!aligned(x, 16) || !aligned(w13_qweight, 16) || !aligned(w13_scales, 16) ||
+            !aligned(w2_qweight, 16) || !aligned(w2_scales, 16))
+            return fail(W4A16_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
+        auto* tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
+        auto* ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
+        hipError_t e = launch_moe_align(ids, P, E, block_m, L.capacity, sorted, experts, npp, st,
+                                        mt.bm, tiles, ntiles);
+        if (e != hipSuccess) return hip_fail(e, "moe align launch");
+        const int max_tiles = moe_max_tiles(P, E, mt.bm);
+        PrefillParams p{};
+        p.sorted_ids = sorted; p.expert_ids = experts; p.num_post_padded = npp;
+        p.tiles = tiles; p.num_tiles = ntiles;
+        p.num_pairs = P; p.G = G; p.zero_offset = zero_offset; p.M = L.capacity;
+        // gate/up: h[p] = x[p / topk] @ W13[e]
+        p.x = static_cast<const half_t*>(x);
+        p.qweight = static_cast<const uint32_t*>(w13_qweight);
+        p.scales = static_cast<const half_t*>(w13_scales);
+        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(w13_qzeros);
+        p.out = static_cast<half_t*>(h);
+        p.N = (int)n13; p.K = K; p.a_div = topk;
+        p.qweight_stride = (int64_t)K * n13 / 8; p.scales_stride = (int64_t)(K / G) * n13;
+        p.qzeros_stride = (int64_t)(K / G) * n13 / 8;
+        e = launch_moe_gemm_tiles(fmt, p, mt.bm, mt.bn13, max_tiles, st);
+        if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
+        rc = fused_silu_mul_interleaved_f16(stream, h, a, I, P * I);
+        if (rc) return rc;
+        // down: yp[p] = a[p] @ W2[e]
+        p.x = static_cast<const half_t*>(a);
+        p.qweight = static_cast<const uint32_t*>(w2_qweight);
+        p.scales = static_cast<const half_t*>(w2_scales);
+        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(w2_qzeros);
+        p.out = static_cast<half_t*>(yp);
+        p.N = K; p.K = I; p.a_div = 1;
+        p.qweight_stride = (int64_t)I * K / 8; p.scales_stride = (int64_t)(I / G) * K;
+        p.qzeros_stride = (int64_t)(I / G) * K / 8;
+        e = launch_moe_gemm_tiles(fmt, p, mt.bm, mt.bn2, max_tiles, st);
+        if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
+        return w4a16_moe_sum(stream, yp, wts, out, T, topk, K);
+    }
+    rc = w4a16_moe_align(stream, ids, P, E, block_m, L.capacity, sorted, experts, npp);
     if (!rc) {
-        const int64_t n13 = 2 * (int64_t)I;
         rc = w4a16_moe_gemm(stream, fmt, x, topk, w13_qweight, w13_scales, w13_qzeros,
                             (int64_t)K * n13 / 8, (int64_t)(K / G) * n13, (int64_t)(K / G) * n13 / 8,
                             sorted, experts, npp, h, P, (int32_t)n13, K, G, block_m, L.capacity,

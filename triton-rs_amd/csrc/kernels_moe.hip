@@ -63,13 +63,18 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int ren
 // places every pair at start[e] + (number of earlier pairs of the same expert), which keeps
 // the order stable. The rank is built per chunk of 1024 pairs and per expert with wave
 // ballots and a prefix over the 16 waves.
+// With `tiles`, it also lists expert tiles for the grouped GEMM: the cnt[e] rows of expert e
+// split into ceil(cnt[e] / tile_bm) tiles of equal height (rounded up to 16 rows, the last
+// one shorter), each {first sorted row, rows, e, 0}, experts in order, and their number in
+// *num_tiles. A tile never reaches into the padding, so the GEMM computes no padded block.
 constexpr int ALIGN_THREADS = 1024;
 constexpr int ALIGN_MAX_E = 1024;
 
 __global__ void __launch_bounds__(ALIGN_THREADS)
 moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int capacity,
                  int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-                 int32_t* __restrict__ num_post_padded) {
+                 int32_t* __restrict__ num_post_padded, int tile_bm, int32_t* __restrict__ tiles,
+                 int32_t* __restrict__ num_tiles) {
     __shared__ int cnt[ALIGN_MAX_E];
     __shared__ int start[ALIGN_MAX_E];
     __shared__ int wave_tot[ALIGN_THREADS / 64];
@@ -88,6 +93,22 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
         }
         total_sh = acc;
         *num_post_padded = acc;
+        if (tiles) {
+            int n_tiles = 0;
+            for (int e = 0; e < E; ++e) {
+                const int c = cnt[e];
+                const int n = (c + tile_bm - 1) / tile_bm;
+                const int per = ((c + n - 1) / max(n, 1) + 15) / 16 * 16;   // <= tile_bm
+                for (int r0 = 0; r0 < c; r0 += per, ++n_tiles) {
+                    int32_t* td = tiles + 4 * n_tiles;
+                    td[0] = start[e] + r0;
+                    td[1] = min(per, c - r0);
+                    td[2] = e;
+                    td[3] = 0;
+                }
+            }
+            *num_tiles = n_tiles;
+        }
     }
     __syncthreads();
     const int total = total_sh;
@@ -133,11 +154,13 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
 
 hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
-                            hipStream_t st) {
+                            hipStream_t st, int tile_bm, int32_t* tiles, int32_t* num_tiles) {
     (void)hipGetLastError();
     if (E > ALIGN_MAX_E) return hipErrorInvalidValue;
+    if (tiles && (tile_bm < 16 || tile_bm % 16 || !num_tiles)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(ALIGN_THREADS), 0, st, ids, P, E, block_m,
-                       capacity, sorted_ids, expert_ids, num_post_padded);
+                       capacity, sorted_ids, expert_ids, num_post_padded, tile_bm, tiles,
+                       num_tiles);
     return hipGetLastError();
 }
 

@@ -20,6 +20,8 @@
 //
 // k order inside a chunk of 8: GPTQ words are unpacked as (k0,k4)(k1,k5)(k2,k6)(k3,k7) and
 // A is staged in that same order; AWQ keeps natural order (rows paired with v_perm_b32).
+#include <type_traits>
+
 #include "device_common.h"
 #include "launch.h"
 
@@ -363,19 +365,31 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int j = lane & 15, kb = lane >> 4;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    int m0 = blockIdx.y * BM, rows = BM;
+    (void)rows;
+    const int n0 = blockIdx.x * BN;
     const int NW = p.N >> 3;
     const int ns = p.K / BK;
 
     if constexpr (MOE) {
-        if (m0 >= *p.num_post_padded) return;
-        const int e = p.expert_ids[blockIdx.y];
+        int e;
+        if (p.tiles) {   // expert tile: rows past its height are masked like padding
+            if ((int)blockIdx.y >= *p.num_tiles) return;
+            const int32_t* td = p.tiles + 4 * blockIdx.y;
+            m0 = td[0];
+            rows = td[1];
+            e = td[2];
+        } else {
+            if (m0 >= *p.num_post_padded) return;
+            e = p.expert_ids[blockIdx.y];
+        }
         p.qweight += (size_t)e * p.qweight_stride;
         p.scales += (size_t)e * p.scales_stride;
         if (p.qzeros) p.qzeros += (size_t)e * p.qzeros_stride;
     }
     auto src_row = [&](int row) -> int {
         if constexpr (MOE) {
+            if (row >= rows) return -1;
             const int pair = p.sorted_ids[m0 + row];
             return pair < p.num_pairs ? pair / p.a_div : -1;
         } else {
@@ -384,6 +398,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     };
     auto dst_row = [&](int row) -> int {
         if constexpr (MOE) {
+            if (row >= rows) return -1;
             const int pair = p.sorted_ids[m0 + row];
             return pair < p.num_pairs ? pair : -1;
         } else {
@@ -535,13 +550,23 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
         for (int c = 0; c < CB; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // operand offsets (halfs) within a stage: A row block r at +16 r rows; B column block c
+    // Rows of the wave's row blocks: block r covers rows row0 + RSTEP r .. +15. A dense tile
+    // gives each wave WM contiguous rows; an expert tile interleaves the blocks over the four
+    // wave rows (r WGM + wm), so that a tile filled only partly still spreads its real rows,
+    // and the MFMAs they need, evenly over the SIMDs.
+    constexpr int RSTEP = MOE ? 16 * WGM : 16;
+    const int row0 = MOE ? 16 * wm : wm * WM;
+
+    // operand offsets (halfs) within a stage: A row block r at +RSTEP r rows; B column block c
     int boff[CB];
 #pragma unroll
     for (int c = 0; c < CB; ++c) boff[c] = (kb * 256 + bpos(wn * WN + 16 * c + j)) * 8;
-    const int aoff_l = (wm * WM + j) * BK;
+    const int aoff_l = (row0 + j) * BK;
 
-    auto fused = [&](int a_slot, int buf, int raw_slot, int dq_buf) {
+    // One stage with the MFMAs of the first RV row blocks only (an expert tile's blocks past
+    // its rows hold no tokens and are skipped; RV is uniform over the wave).
+    auto fused = [&](auto rv, int a_slot, int buf, int raw_slot, int dq_buf) {
+        constexpr int RV = decltype(rv)::value;
         const DqRaw d = dq_load(raw_slot);
         const half_t* A = As + a_slot * A_ST + aoff_l;
         const half_t* B = Bs + buf * B_ST;
@@ -549,15 +574,15 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int kc = 4 * ks + kb;
-            half8_t af[RB], bf[CB];
+            half8_t af[RV > 0 ? RV : 1], bf[CB];
 #pragma unroll
-            for (int r = 0; r < RB; ++r)
-                af[r] = *reinterpret_cast<const half8_t*>(A + 16 * r * BK + 8 * (kc ^ (j & 7)));
+            for (int r = 0; r < RV; ++r)
+                af[r] = *reinterpret_cast<const half8_t*>(A + RSTEP * r * BK + 8 * (kc ^ (j & 7)));
 #pragma unroll
             for (int c = 0; c < CB; ++c)
-                bf[c] = *reinterpret_cast<const half8_t*>(B + boff[c] + ks * 4 * 256 * 8);
+                if (RV > 0) bf[c] = *reinterpret_cast<const half8_t*>(B + boff[c] + ks * 4 * 256 * 8);
 #pragma unroll
-            for (int r = 0; r < RB; ++r)
+            for (int r = 0; r < RV; ++r)
 #pragma unroll
                 for (int c = 0; c < CB; ++c)
                     acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[r], bf[c], acc[r][c], 0, 0, 0);
@@ -567,7 +592,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
             // (measured 229 -> 216 us at M=2048, K=4096, N=14336 against MFMAs then
             // dequantisation; 1 or 3 VALU per MFMA were slower)
 #pragma unroll
-            for (int i = 0; i < RB * CB; ++i) {
+            for (int i = 0; i < RV * CB; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // 1 MFMA
                 __builtin_amdgcn_sched_group_barrier(0x002, 2, 0); // 2 VALU
             }
@@ -589,13 +614,27 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     // of stage s with the dequantisation of B(s+1) interleaved; wait for all but the raw
     // word load just issued; barrier. Indices past the end are clamped (their loads land in slots nobody
     // reads any more).
-    for (int s = 0; s < ns; ++s) {
-        const int rs = s % 3;
-        dma_a((s + 1) & 1, min(s + 1, ns - 1));
-        dma_b(rs, min(s + 3, ns - 1));
-        fused(s & 1, s & 1, rs == 2 ? 0 : rs + 1, (s + 1) & 1);
-        wait_vmcnt<1>();
-        __syncthreads();
+    auto main_loop = [&](auto rv) {
+        for (int s = 0; s < ns; ++s) {
+            const int rs = s % 3;
+            dma_a((s + 1) & 1, min(s + 1, ns - 1));
+            dma_b(rs, min(s + 3, ns - 1));
+            fused(rv, s & 1, s & 1, rs == 2 ? 0 : rs + 1, (s + 1) & 1);
+            wait_vmcnt<1>();
+            __syncthreads();
+        }
+    };
+    if constexpr (MOE) {
+        // row blocks of this wave that start inside the tile's rows; every variant runs the
+        // same stages and barriers
+        const int rv = rows <= row0 ? 0 : min(RB, (rows - row0 + RSTEP - 1) / RSTEP);
+        if (rv >= RB) main_loop(std::integral_constant<int, RB>{});
+        else if (RB > 1 && rv == RB - 1) main_loop(std::integral_constant<int, (RB > 1 ? RB - 1 : RB)>{});
+        else if (RB > 2 && rv == RB - 2) main_loop(std::integral_constant<int, (RB > 2 ? RB - 2 : RB)>{});
+        else if (RB > 3 && rv == RB - 3) main_loop(std::integral_constant<int, (RB > 3 ? RB - 3 : RB)>{});
+        else main_loop(std::integral_constant<int, 0>{});
+    } else {
+        main_loop(std::integral_constant<int, RB>{});
     }
     wait_vmcnt<0>();   // no LDS write may be in flight when the workgroup ends
 
@@ -604,7 +643,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     for (int r = 0; r < RB; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int m = dst_row(wm * WM + 16 * r + 4 * kb + i);
+            const int m = dst_row(row0 + RSTEP * r + 4 * kb + i);
             if (m < 0) continue;
             half_t* dst = p.out + (size_t)m * p.N + n0 + wn * WN + j;
 #pragma unroll
@@ -683,7 +722,15 @@ static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, si
                            hipStream_t st) {
     if constexpr (MOE) {
         if (bm == 64) launch_dma_t<FMT, 64, 256, true>(p, grid, lds, st);
-        else launch_dma_t<FMT, 128, 256, true>(p, grid, lds, st);
+        else if (bm == 128 && bn == 224) launch_dma_t<FMT, 128, 224, true>(p, grid, lds, st);
+        else if (bm == 128 && bn == 128) launch_dma_t<FMT, 128, 128, true>(p, grid, lds, st);
+        else if (bm == 128) launch_dma_t<FMT, 128, 256, true>(p, grid, lds, st);
+        else if (bm == 192 && bn == 224) launch_dma_t<FMT, 192, 224, true>(p, grid, lds, st);
+        else if (bm == 192 && bn == 128) launch_dma_t<FMT, 192, 128, true>(p, grid, lds, st);
+        else if (bm == 192) launch_dma_t<FMT, 192, 256, true>(p, grid, lds, st);
+        else if (bn == 224) launch_dma_t<FMT, 256, 224, true>(p, grid, lds, st);
+        else if (bn == 128) launch_dma_t<FMT, 256, 128, true>(p, grid, lds, st);
+        else launch_dma_t<FMT, 256, 256, true>(p, grid, lds, st);
     } else {
         if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false>(p, grid, lds, st);
         else if (bm == 256 && bn == 128) launch_dma_t<FMT, 256, 128, false>(p, grid, lds, st);
@@ -747,6 +794,22 @@ hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s
 bool moe_gemm_supported(int N, int K, int G, int block_m) {
     return N % BN == 0 && K % BK == 0 && G % 8 == 0 && K % G == 0 &&
            (block_m == 64 || block_m == 128);
+}
+
+bool moe_tiles_supported(int N, int K, int G, long long a_rows, int bn) {
+    return (bn == 256 || bn == 224 || bn == 128) && N % bn == 0 && K % BK == 0 && G % 8 == 0 &&
+           K % G == 0 && dma_ok(N, K, G, a_rows);
+}
+
+hipError_t launch_moe_gemm_tiles(int fmt, const PrefillParams& p, int tile_bm, int bn,
+                                 int max_tiles, hipStream_t st) {
+    const bool shape_ok = (tile_bm == 64 && bn == 256) || tile_bm == 128 || tile_bm == 192 ||
+                          tile_bm == 256;
+    if (!p.tiles || !p.num_tiles || !shape_ok ||
+        !moe_tiles_supported(p.N, p.K, p.G, (p.num_pairs + p.a_div - 1) / p.a_div, bn))
+        return hipErrorInvalidValue;
+    return launch_dma_any<true>(fmt, p, tile_bm, bn, dim3(p.N / bn, max_tiles),
+                                prefill_dma_lds(tile_bm, bn), st);
 }
 
 hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,

@@ -57,6 +57,11 @@ struct PrefillParams {
     const int32_t* num_post_padded;  // device scalar
     int num_pairs, a_div;            // x row of pair p is p / a_div
     int64_t qweight_stride, scales_stride, qzeros_stride;   // per expert, in elements
+    // expert-tile mode (tiles != nullptr): workgroup row y computes tile y of the list,
+    // {first sorted row, rows, expert, 0}, while y < *num_tiles; expert_ids and
+    // num_post_padded are then unused
+    const int32_t* tiles;
+    const int32_t* num_tiles;
 };
 
 struct PrefillShape {
@@ -73,13 +78,21 @@ hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s
 bool moe_gemm_supported(int N, int K, int G, int block_m);
 hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
                            hipStream_t st);
+// Expert-tile grouped GEMM: tile rows tile_bm (128, 192 or 256 with tile columns bn = 256,
+// 224 or 128 dividing N; 64 with bn = 256); grid rows max_tiles, the bound of moe_max_tiles.
+bool moe_tiles_supported(int N, int K, int G, long long a_rows, int bn);
+hipError_t launch_moe_gemm_tiles(int fmt, const PrefillParams& p, int tile_bm, int bn,
+                                 int max_tiles, hipStream_t st);
 
 // Fused-MoE helpers (kernels_moe.hip).
 hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int renormalize,
                             int32_t* ids, float* weights, hipStream_t st);
 hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
-                            hipStream_t st);
+                            hipStream_t st, int tile_bm = 0, int32_t* tiles = nullptr,
+                            int32_t* num_tiles = nullptr);
+// Upper bound on the expert tiles of tile_bm rows that P pairs over E experts can need.
+inline int moe_max_tiles(int P, int E, int tile_bm) { return (P + tile_bm - 1) / tile_bm + E; }
 hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
                            hipStream_t st);
 hipError_t launch_moe_sum(const half_t* y_pairs, const float* weights, half_t* out, int T,
