@@ -163,6 +163,23 @@ def test_prefill_narrow_tiles(torch_cuda, orc, fmt, M, K, N):
         assert_parity(y[rows], ref.astype(np.float64), what=f"prefill 128-wide fmt={fmt} M={M}")
 
 
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N,G", [(2000, 640, 14336, 128), (512, 64, 128, 64),
+                                     (512, 192, 128, 64), (1000, 128, 14336, 64)])
+def test_prefill_256_row_tiles(torch_cuda, orc, fmt, M, K, N, G):
+    """256-row tiles, 224 and 128 columns wide: every format, a row tail, and pipelines of 1,
+    2 and 3 stages of 64 k."""
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=2400 + M + K + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, G) == "prefill"
+    y = _run_gemm(torch_cuda, p)
+    rows = np.random.default_rng(5).choice(M, 16, replace=False).astype(np.int32)
+    rows[:3] = [0, 255, M - 1]
+    ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, G, rows)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"prefill 256-row tiles fmt={fmt} M={M} K={K}")
+    assert np.all(np.isfinite(y))
+
+
 def test_mfma_split_k_deterministic(torch_cuda, orc):
     P = pkg()
     p = Problem(AWQ, M=8, K=4096, N=1024, G=128, seed=2200)
