@@ -45,6 +45,7 @@ CASES = [
     ("gptq_m128_k256_n256", 0, 128, 256, 256, 128, False),  # prefill
     ("awq_m96_k256_n384", 2, 96, 256, 384, 128, False),     # prefill (128-wide tiles)
     ("awq_m5_k384_n200", 2, 5, 384, 200, 128, False),       # generic strided kernel
+    ("awq_m6_k1024_n256", 2, 6, 1024, 256, 128, False),     # matrix-core GEMV, 1024-row tile
 ]
 
 

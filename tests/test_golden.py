@@ -19,6 +19,7 @@ EXPECT_KERNEL = {
     "awq_m8_k512_n256": "gemv", "gptq_m16_k512_n256": "skinny", "awq_m24_k512_n256": "skinny",
     "gptq_ao_m16_k512_n256": "skinny", "gptq_m128_k256_n256": "prefill",
     "awq_m96_k256_n384": "prefill", "awq_m5_k384_n200": "strided",
+    "awq_m6_k1024_n256": "gemv",
 }
 
 

@@ -329,6 +329,7 @@ gemv_awq_mfma_kernel(GemvParams p) {
     constexpr int WW = 16 * CW;       // words per tile row
     constexpr int C = 8 * WW;         // columns per tile
     static_assert(S % 8 == 0 && PF <= S && (CW == 2 || CW == 4), "tile shape");
+    static_assert(64 * WAVES <= FINISH_MAX_THREADS, "split-K finish buffer");
 
     __shared__ float red[WAVES][M][C];
     __shared__ int flag;
@@ -491,9 +492,17 @@ constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
 constexpr int GQ_CW = 4, GQ_RL = 4, GQ_WAVES = 4, GQ_LPR = 32;
 constexpr int GQ_COLS = GQ_LPR * GQ_CW;
 constexpr int GQ_ROWS = (64 / GQ_LPR) * GQ_WAVES * GQ_RL * 8;
-// AWQ, M = 5..8, matrix-core dot: CW = 2 words per lane (256 columns), R = 64 rows per wave
-constexpr int AM_CW = 2, AM_R = 64, AM_WAVES = 4, AM_PF = 16;
-constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES;
+// AWQ, M = 2..8, matrix-core dot: CW = 2 words per lane (256 columns). Wide tile: R = 128
+// rows per wave, 8 waves (1024 rows per workgroup: a quarter of the split-K partials of the
+// narrow tile, which rereads M x N fp32 per split); narrow tile (R = 64, 4 waves, 256 rows)
+// for K or group sizes the wide one does not divide. At K=4096 -> N=14336 / K=14336 ->
+// N=4096 the wide tile takes M=2: 9.4 / 10.3 us, M=4: 11.4 / 11.9 us, M=8: 14.5 / 15.8 us
+// against 10.6 / 12.1, 11.9 / 15.4, 17.7 / 24.6 us for the narrow one (4 waves x 128 rows:
+// 15.3 / 19.0 us at M=8; 16 waves x 64 rows: 15.7 / 17.0 us).
+constexpr int AM_CW = 2, AM_PF = 16;
+constexpr int AM_R = 64, AM_WAVES = 4;
+constexpr int AMW_R = 128, AMW_WAVES = 8;
+constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R * AMW_WAVES;
 }  // namespace
 
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
@@ -501,9 +510,11 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     // AWQ: matrix-core dot for M = 2..8 (M = 2: 10.3 vs 11.4 us, M = 4: 12.0 vs 14.5 us at
     // K=4096, N=14336), VALU dot2 for M = 1 and for shapes the matrix-core tile rejects
     const bool mfma_fits = N % AM_COLS == 0 && K % AM_ROWS == 0 && G % AM_R == 0 && K % G == 0;
+    const bool wide_fits = mfma_fits && K % AMW_ROWS == 0 && G % AMW_R == 0;
     if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
-        s.ok = true; s.mfma = true; s.col_tiles = N / AM_COLS; s.splits = K / AM_ROWS;
-        s.threads = 64 * AM_WAVES;
+        s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
+        s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
+        s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
     } else if (M >= 1 && M <= GEMV_MAX_M && fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
         s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
@@ -525,8 +536,12 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     const dim3 block(s.threads);
     if (fmt == FMT_AWQ && s.mfma) {
-        if constexpr (M <= GEMV_MFMA_MAX_M)
-            hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+        if constexpr (M <= GEMV_MFMA_MAX_M) {
+            if (s.mfma_wide)
+                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AMW_R, AMW_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+            else
+                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+        }
     } else if constexpr (M <= GEMV_MAX_M) {
         if (fmt == FMT_AWQ)
             hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD>), grid, block, 0, st, p);

@@ -32,6 +32,7 @@ struct GemvParams {
 struct GemvShape {
     bool ok;
     bool mfma;              // AWQ matrix-core kernel (else VALU dot products)
+    bool mfma_wide;         // its 8-wave, 1024-row tile (else 4 waves, 256 rows)
     bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     int col_tiles, splits, threads;
 };
