@@ -37,6 +37,7 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD>
 __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
+    static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ), "columns per lane");
     constexpr int RB = BM / 16;
     constexpr int WN = 16 * CPL;
     constexpr int WPS = (FMT == FMT_AWQ) ? 8 : CPL;   // packed words per lane per k32 step
@@ -67,7 +68,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         const int kg = 32 * step;
         // packed weights
         if constexpr (FMT == FMT_AWQ) {
-            const int wcol = (CPL == 8) ? (n0 >> 3) + j : (nl >> 3);
+            const int wcol = nl >> 3;
             const uint32_t off0 = (uint32_t)(kg + 8 * kb) * (uint32_t)NW + (uint32_t)wcol;
 #pragma unroll
             for (int r = 0; r < 8; ++r)
@@ -104,10 +105,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         // scales and zero word of the lane's columns for this step's group
         const int g = kg / p.G;
         const uint32_t* sp = reinterpret_cast<const uint32_t*>(p.scales + (size_t)g * p.N + nl);
-        if constexpr (CPL == 8) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(sp);
-            sreg[u][0] = v.x; sreg[u][1] = v.y; sreg[u][2] = v.z; sreg[u][3] = v.w;
-        } else if constexpr (CPL == 4) {
+        if constexpr (CPL == 4) {
             const u32x2 v = *reinterpret_cast<const u32x2*>(sp);
             sreg[u][0] = v.x; sreg[u][1] = v.y;
         } else {
@@ -168,22 +166,13 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
                     const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
                     const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
                     const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
-                    if constexpr (CPL == 8) {
-#pragma unroll
-                        for (int sl = 0; sl < 8; ++sl) {
-                            const uint32_t src = sl < 4 ? p0 : p1;
-                            const int col = awq_col_of_slot(sl);
-                            pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
-                        }
-                    } else {
-                        // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
-                        const int sh = 8 * (j & 1);
-                        const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
-                        pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
-                        pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
-                        pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
-                        pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
-                    }
+                    // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
+                    const int sh = 8 * (j & 1);
+                    const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
+                    pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
+                    pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
+                    pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
+                    pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
                 }
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
@@ -276,11 +265,10 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     const bool awq = fmt == FMT_AWQ;
     // 4 columns per lane where N allows (the wider strip re-reads the activations from L2
-    // half as often as 2; 8 would not fit the cross-wave reduction buffer at BM=64)
+    // half as often as 2); AWQ needs 4 (half an AWQ word per lane)
     int cpl = 0;
-    for (int c : {4, 2, 8}) {
+    for (int c : {4, 2}) {
         if (awq && c < 4) continue;
-        if (s.bm == 64 && c > 4) continue;
         if (N % (16 * c) == 0) { cpl = c; break; }
     }
     if (!cpl) return s;
@@ -307,7 +295,7 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
 
 template <int FMT, int BM, int CPL, bool XCD>
 static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
-    constexpr int PF = (FMT == FMT_AWQ || CPL >= 8) ? 3 : 4;
+    constexpr int PF = FMT == FMT_AWQ ? 3 : 4;
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     if constexpr (FMT != FMT_AWQ) {
         if (p.g_idx) {
@@ -333,9 +321,6 @@ template <int FMT, int BM>
 static hipError_t launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (FMT != FMT_AWQ) {
         if (s.cpl == 2) return launch_t<FMT, BM, 2>(p, s, st);
-    }
-    if constexpr (BM < 64) {
-        if (s.cpl == 8) return launch_t<FMT, BM, 8>(p, s, st);
     }
     return launch_t<FMT, BM, 4>(p, s, st);
 }
