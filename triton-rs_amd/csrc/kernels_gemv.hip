@@ -489,9 +489,13 @@ namespace {
 constexpr int AWQ_CW = 1, AWQ_RL = 32, AWQ_WAVES = 4;
 constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
 // GPTQ: CW = 4 columns per lane, 4 packed rows per lane, LPR = 32 -> 128 columns x 256 k.
-constexpr int GQ_CW = 4, GQ_RL = 4, GQ_WAVES = 4, GQ_LPR = 32;
+// At M = 1, 8 packed rows per lane (128 columns x 512 k, half the splits) where the group
+// size allows: 4.84 -> 4.55 us for config 0 (GPTQ sym 4096 x 4096) and 9.67 -> 8.87 us for
+// GPTQ 4096 -> 14336 (graph replays); at M = 4 the deeper tile was slower (16.2 -> 17.0 us).
+constexpr int GQ_CW = 4, GQ_RL = 4, GQ_RL1 = 8, GQ_WAVES = 4, GQ_LPR = 32;
 constexpr int GQ_COLS = GQ_LPR * GQ_CW;
 constexpr int GQ_ROWS = (64 / GQ_LPR) * GQ_WAVES * GQ_RL * 8;
+constexpr int GQ_ROWS1 = (64 / GQ_LPR) * GQ_WAVES * GQ_RL1 * 8;
 // AWQ, M = 2..8, matrix-core dot: CW = 2 words per lane (256 columns). Wide tile: R = 128
 // rows per wave, 8 waves (1024 rows per workgroup: a quarter of the split-K partials of the
 // narrow tile, which rereads M x N fp32 per split); narrow tile (R = 64, 4 waves, 256 rows)
@@ -520,7 +524,9 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
     } else if (M >= 1 && M <= GEMV_MAX_M) {
         if (N % GQ_COLS || K % GQ_ROWS || G % (GQ_RL * 8) || K % G) return s;
-        s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / GQ_ROWS; s.threads = 64 * GQ_WAVES;
+        s.gptq_deep = M == 1 && K % GQ_ROWS1 == 0 && G % (GQ_RL1 * 8) == 0;
+        s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / (s.gptq_deep ? GQ_ROWS1 : GQ_ROWS);
+        s.threads = 64 * GQ_WAVES;
     } else {
         return s;
     }
@@ -543,6 +549,15 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
                 hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
         }
     } else if constexpr (M <= GEMV_MAX_M) {
+        if constexpr (M == 1) {
+            if (fmt != FMT_AWQ && s.gptq_deep) {
+                if (fmt == FMT_GPTQ)
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+                else
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+                return;
+            }
+        }
         if (fmt == FMT_AWQ)
             hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD>), grid, block, 0, st, p);
         else if (fmt == FMT_GPTQ)
