@@ -109,4 +109,19 @@ __device__ __forceinline__ u32x4 ld_stream4(const uint32_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// f16(silu(g) * u) with g, u fp16 and silu(g) = g / (1 + exp(-g)) in f32
+// (crates/triton-kernels/src/elementwise.rs:188-212): the product is rounded to f32, then to
+// f16, as in the reference and the oracle. Contraction is off and the product passes through
+// an empty asm: otherwise the compiler may fold multiply and conversion into one
+// mixed-precision FMA (v_fma_mixlo_f16), which rounds once and differs from the two
+// roundings in about 1 case in 15000 (seen where the code was inlined into a GEMM epilogue).
+__device__ __forceinline__ half_t silu_mul_f16(half_t g, half_t u) {
+#pragma clang fp contract(off)
+    const float gf = (float)g;
+    const float s = gf / (1.0f + expf(-gf));
+    float prod = s * (float)u;
+    asm volatile("" : "+v"(prod));
+    return (half_t)prod;
+}
+
 }  // namespace w4a16

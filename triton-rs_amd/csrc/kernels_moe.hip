@@ -179,11 +179,7 @@ silu_mul_kernel(const half_t* __restrict__ gate_up, half_t* __restrict__ out, in
     const half8_t uv = *reinterpret_cast<const half8_t*>(g + inter);
     half8_t o;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float gf = (float)gv[k];
-        const float s = gf / (1.0f + expf(-gf));
-        o[k] = (half_t)(s * (float)uv[k]);
-    }
+    for (int k = 0; k < 8; ++k) o[k] = silu_mul_f16(gv[k], uv[k]);
     *reinterpret_cast<half8_t*>(out + i8) = o;
 }
 
