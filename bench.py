@@ -272,7 +272,7 @@ def extras(torch, pkg, dev, stream, args):
     gemm_case("c1_awq_m8_k14336_n4096", "awq", 8, 14336, 4096, 128, 20, 1000)
     perm = torch.randperm(4096, generator=torch.Generator().manual_seed(2))
     g_idx = (torch.arange(4096) // 128)[perm].to(torch.int32).to(dev)
-    for M in (16, 64):
+    for M in (16, 32, 64):
         gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 20, 500,
                   g_idx=g_idx)
         gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 20, 500)

@@ -2,13 +2,14 @@
 // so the kernel is built to keep loads in flight and to need few workgroup-to-workgroup
 // reductions.
 //
-// A workgroup owns a strip of WN = 16*CPL columns; its 4 waves split the strip's K range
-// four ways and stream independently (no LDS staging, no barrier in the main loop). Each
+// A workgroup owns a strip of WN = 16*CPL columns; its waves (4, or 8 for 32-row tiles)
+// split the strip's K range and stream independently (no LDS staging, no barrier in the main
+// loop). Each
 // lane keeps a ring of PF k32 steps of loads in flight: its packed words, the activation
 // fragments and the group's scales/zeros. Words are dequantised bit-exactly
 // (W16 = RNE_f16((q - z) * s), crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:246-260,
 // awq_gemm_int4_typed.rs:213-228) straight into MFMA B-operand registers and multiplied
-// with v_mfma_f32_16x16x32_f16 (fp32 accumulation, the reference's tt.dot). The four waves'
+// with v_mfma_f32_16x16x32_f16 (fp32 accumulation, the reference's tt.dot). The waves'
 // accumulators are summed in LDS; when the strip count alone cannot fill the GPU the K
 // range is also split across workgroups, joined by the counter hand-off of splitk.h.
 //
@@ -28,6 +29,11 @@
 namespace w4a16 {
 
 namespace {
+// waves per workgroup: 8 for 32-row tiles (the same wave count with half the workgroup
+// splits, so half the split-K partials: config 2 M=32 12.3 -> 11.9 us plain, 15.3 -> 14.1 us
+// act-order; at M=16 the 4-wave tile was faster, 9.7 vs 10.9 us; 64-row tiles keep 4 for
+// the reduction buffer)
+constexpr int skinny_waves(int bm) { return bm == 32 ? 8 : 4; }
 __device__ __forceinline__ half2_t deq2(half2_t h, half2_t hz, half2_t hs) { return (h - hz) * hs; }
 __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
     return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
@@ -35,15 +41,17 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }  // namespace
 
 template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD>
-__global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
+__global__ void __launch_bounds__(64 * skinny_waves(BM)) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ), "columns per lane");
+    constexpr int W = skinny_waves(BM), NT = 64 * W;
+    static_assert(NT <= FINISH_MAX_THREADS, "split-K finish buffer");
     constexpr int RB = BM / 16;
     constexpr int WN = 16 * CPL;
     constexpr int WPS = (FMT == FMT_AWQ) ? 8 : CPL;   // packed words per lane per k32 step
     constexpr int SW = (CPL + 1) / 2;                  // scale words (2 halfs each) per lane
 
-    __shared__ float red[4][BM][WN + 1];
+    __shared__ float red[W][BM][WN + 1];
     __shared__ int flag;
     extern __shared__ uint32_t gtab[];   // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16)
 
@@ -56,7 +64,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
     const int nl = n0 + CPL * j;              // first output column of this lane
     const int NW = p.N >> 3;
     const int spw = p.steps_per_wave;
-    const int step0 = (split * 4 + wave) * spw;  // first k32 step of this wave
+    const int step0 = (split * W + wave) * spw;  // first k32 step of this wave
 
     // ------------------------------------------------ per-step loads into ring slot u
     uint32_t bw[PF][WPS];
@@ -126,7 +134,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
 
     const int ngroups = (p.K + p.G - 1) / p.G;
     if constexpr (GIDX) {
-        for (int o = threadIdx.x; o < ngroups * WN; o += 256) {
+        for (int o = threadIdx.x; o < ngroups * WN; o += NT) {
             const int g = o / WN, n = n0 + (o - g * WN);
             const uint32_t sc = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
             const int z = (FMT == FMT_GPTQ_SYM)
@@ -233,7 +241,7 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
         }
     }
 
-    // ------------------------------------------------ reduce the 4 waves' K ranges
+    // ------------------------------------------------ reduce the W waves' K ranges
 #pragma unroll
     for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -241,10 +249,12 @@ __global__ void __launch_bounds__(256) skinny_kernel(SkinnyParams p) {
 #pragma unroll
             for (int c = 0; c < CPL; ++c) red[wave][16 * r + 4 * kb + i][CPL * j + c] = acc[r][c][i];
     __syncthreads();
-    for (int o = threadIdx.x; o < BM * WN; o += 256) {
+    for (int o = threadIdx.x; o < BM * WN; o += NT) {
         const int m = o / WN, col = o - m * WN;
         if (m >= p.M) continue;
-        const float v = red[0][m][col] + red[1][m][col] + red[2][m][col] + red[3][m][col];
+        float v = red[0][m][col];
+#pragma unroll
+        for (int w = 1; w < W; ++w) v += red[w][m][col];
         const size_t off = (size_t)m * p.N + n0 + col;
         if (p.splits == 1) p.out[off] = (half_t)v;
         else st_partial<SC>(p.ws + (size_t)split * p.M * p.N + off, v);
@@ -263,6 +273,8 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     // without g_idx a k32 step lies in one group; with it the group comes from the table
     if (gidx ? (fmt == FMT_AWQ || G < 1) : (G % 32 || K % G)) return s;
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
+    // the 8-wave tile consumes K in steps of 256 rows; other K take the 64-row tile
+    if (skinny_waves(s.bm) == 8 && K % 256) s.bm = 64;
     const bool awq = fmt == FMT_AWQ;
     // 4 columns per lane where N allows (the wider strip re-reads the activations from L2
     // half as often as 2); AWQ needs 4 (half an AWQ word per lane)
@@ -282,12 +294,15 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     // (splits * M * N * 4 bytes) under a quarter of the packed weights (K * N / 2 bytes) and
     // workgroups x M near 12K (measured optimum at K=4096, N=6144: 8 splits at M=16, 4 at
     // M=32, 2 at M=64; more splits cost more in partial traffic than they gain in width)
-    int splits = 1;
-    while (s.col_tiles * splits < 2 * num_cus && K % (128 * 2 * splits) == 0 &&
-           2 * splits * 32 * M <= K && (long long)s.col_tiles * 2 * splits * M <= 12288)
-        splits *= 2;
+    // (counted in units of 4 waves: quads = splits x waves / 4)
+    int quads = 1;
+    while (s.col_tiles * quads < 2 * num_cus && K % (128 * 2 * quads) == 0 &&
+           2 * quads * 32 * M <= K && (long long)s.col_tiles * 2 * quads * M <= 12288)
+        quads *= 2;
+    const int wq = skinny_waves(s.bm) / 4;
+    const int splits = quads >= wq ? quads / wq : 1;
     s.splits = splits;
-    s.steps_per_wave = K / (128 * splits);
+    s.steps_per_wave = K / (32 * skinny_waves(s.bm) * splits);
     s.xcd = xcd_placement && splits > 1 && s.col_tiles % 8 == 0;
     s.ok = true;
     return s;
@@ -304,11 +319,11 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
                 reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true, XCD>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
             if (attr != hipSuccess) return attr;
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(256), s.lds, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(64 * skinny_waves(BM)), s.lds, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(256), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(64 * skinny_waves(BM)), 0, st, p);
     return hipGetLastError();
 }
 
