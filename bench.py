@@ -268,8 +268,8 @@ def extras(torch, pkg, dev, stream, args):
     gemm_case("c0_gptq_sym_m1_k4096_n4096", "gptq_sym", 1, 4096, 4096, 128, 60, 1000)
     for M in (4, 8):
         gemm_case(f"c1_awq_m{M}_k4096_n14336", "awq", M, 4096, 14336, 128, 20, 1000)
-    gemm_case("c1_awq_m1_k14336_n4096", "awq", 1, 14336, 4096, 128, 20, 1000)
-    gemm_case("c1_awq_m8_k14336_n4096", "awq", 8, 14336, 4096, 128, 20, 1000)
+    for M in (1, 4, 8):
+        gemm_case(f"c1_awq_m{M}_k14336_n4096", "awq", M, 14336, 4096, 128, 20, 1000)
     perm = torch.randperm(4096, generator=torch.Generator().manual_seed(2))
     g_idx = (torch.arange(4096) // 128)[perm].to(torch.int32).to(dev)
     for M in (16, 32, 64):
