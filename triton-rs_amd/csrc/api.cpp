@@ -223,6 +223,13 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
+        p.ksplit = s.ksplit;
+        if (s.ksplit > 1) {
+            if ((size_t)s.col_tiles * s.row_tiles > SPLITK_MAX_TILES)
+                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
+            rc = get_workspace(st, (size_t)s.ksplit * M * N * sizeof(float), &p.counters, &p.ws);
+            if (rc) return rc;
+        }
         hipError_t e = launch_prefill(fmt, p, s, st);
         if (e != hipSuccess) return hip_fail(e, "prefill launch");
         return W4A16_OK;

@@ -24,6 +24,7 @@
 
 #include "device_common.h"
 #include "launch.h"
+#include "splitk.h"
 
 namespace w4a16 {
 
@@ -369,7 +370,10 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     (void)rows;
     const int n0 = blockIdx.x * BN;
     const int NW = p.N >> 3;
-    const int ns = p.K / BK;
+    // split-K (dense only): this workgroup's K stages are [s0, s0 + ns)
+    const int ksp = MOE ? 1 : max(p.ksplit, 1);
+    const int ns = p.K / BK / ksp;
+    const int s0 = MOE ? 0 : (int)blockIdx.z * ns;
 
     if constexpr (MOE) {
         int e;
@@ -422,7 +426,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         half_t* dst = As + slot * A_ST;
 #pragma unroll
         for (int q = 0; q < ADMA; ++q)
-            dma16(ars, dst + (q * NWV + wave) * 64 * 8, aoff[q] + (uint32_t)s * (BK * 2));
+            dma16(ars, dst + (q * NWV + wave) * 64 * 8, aoff[q] + (uint32_t)(s0 + s) * (BK * 2));
     };
 
     // ---- B raw: words of a stage as [64 rows][32 words] (AWQ) or [8 packed rows][256
@@ -451,7 +455,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     const int szdst = RAW_W + (zw_wave ? RAW_S : 0);
     auto dma_b = [&](int slot, int s) {
         char* dst = Raw + slot * RAW_ST;
-        const int k0 = s * BK, g = k0 / p.G;
+        const int k0 = (s0 + s) * BK, g = k0 / p.G;
         const uint32_t wstep = (FMT == FMT_AWQ) ? (uint32_t)k0 * (uint32_t)NW * 4u
                                                 : (uint32_t)(k0 >> 3) * (uint32_t)p.N * 4u;
         dma16(szrs, dst + szdst, szoff + (uint32_t)g * szrow);
@@ -639,6 +643,38 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     wait_vmcnt<0>();   // no LDS write may be in flight when the workgroup ends
 
     // ---- epilogue: lane holds D[4 kb + i][j] of each 16 x 16 block
+    if constexpr (!MOE) {
+        if (ksp > 1) {
+            // partials of this split, then the last split of the tile sums all of them in
+            // split order (deterministic) and writes the fp16 tile
+            __shared__ int last_flag;
+            const size_t MN = (size_t)p.M * p.N;
+            float* mine = p.ws + (size_t)blockIdx.z * MN;
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = m0 + row0 + RSTEP * r + 4 * kb + i;
+                    if (m >= p.M) continue;
+                    float* dst = mine + (size_t)m * p.N + n0 + wn * WN + j;
+#pragma unroll
+                    for (int c = 0; c < CB; ++c) st_partial<SCOPE_DEVICE>(dst + 16 * c, acc[r][c][i]);
+                }
+            const int tile = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
+            if (!splitk_arrive(splitk_counter(p.counters, tile), ksp, &last_flag)) return;
+            constexpr int C4 = BN / 4;
+            const int rows = min(BM, p.M - m0);
+            for (int idx = t; idx < rows * C4; idx += PF_THREADS) {
+                const int r = idx / C4, c = 4 * (idx - r * C4);
+                const size_t off = (size_t)(m0 + r) * p.N + n0 + c;
+                float4_t v = ld_partial4<SCOPE_DEVICE>(p.ws + off);
+                for (int sp = 1; sp < ksp; ++sp) v += ld_partial4<SCOPE_DEVICE>(p.ws + sp * MN + off);
+                const half2_t lo = {(half_t)v.x, (half_t)v.y}, hi = {(half_t)v.z, (half_t)v.w};
+                *reinterpret_cast<u32x2*>(p.out + off) = u32x2{as_u32(lo), as_u32(hi)};
+            }
+            return;
+        }
+    }
 #pragma unroll
     for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -681,6 +717,26 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
         }
         if (best >= 0) {
             s.dma = true;
+            s.ksplit = 1;
+            // 256 x 256 tiles with K split across workgroups, where the chosen tiles leave
+            // CUs idle or K is long: a 256 x 256 stage does twice the work of a 256 x 128
+            // one in ~1.4x the time, while the fp32 partials cost a fixed write and reread.
+            // Measured (graph replays): config 3 down (M=2048, 14336 -> 4096) 258 -> 231
+            // us with 2 splits; M=1024 on the same shape 235 -> 140 us with 4; M=512,
+            // 4096 -> 4096 68 -> 64 us; but M=2048, 4096 -> 4096 (256 tiles of 256 x 128
+            // already fill the CUs, 32 stages per split) 76 -> 85 us, so a full grid is
+            // split only from 64 stages (8192 rows of K) per split. Each split keeps at
+            // least 8 stages.
+            const long long wgs = (long long)(N / s.bn) * ((M + s.bm - 1) / s.bm);
+            if (s.bm == 256 && (s.bn == 128 || s.bn == 256) && N % 256 == 0 &&
+                (wgs < num_cus || K / BK / 2 >= 64)) {
+                const int tiles = (N / 256) * ((M + 255) / 256);
+                int ks = 1;
+                while (ks < 4 && tiles * ks * 2 <= num_cus && (K / BK) % (ks * 2) == 0 &&
+                       K / BK / (ks * 2) >= 8)
+                    ks *= 2;
+                if (ks > 1) { s.bn = 256; s.ksplit = ks; }
+            }
             s.col_tiles = N / s.bn;
             s.row_tiles = (M + s.bm - 1) / s.bm;
             s.lds = prefill_dma_lds(s.bm, s.bn);
@@ -693,6 +749,7 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
     // 256-row tiles when they still give every CU a workgroup, else 128
     s.bm = ((M + 255) / 256) * col_tiles >= num_cus ? 256 : 128;
     s.bn = BN;
+    s.ksplit = 1;
     s.col_tiles = col_tiles;
     s.row_tiles = (M + s.bm - 1) / s.bm;
     s.lds = (size_t)2 * (s.bm + BN) * LD * sizeof(half_t);
@@ -787,7 +844,8 @@ static hipError_t launch_any(int fmt, const PrefillParams& p, int bm, dim3 grid,
 
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
     if (s.dma)
-        return launch_dma_any<false>(fmt, p, s.bm, s.bn, dim3(s.col_tiles, s.row_tiles), s.lds, st);
+        return launch_dma_any<false>(fmt, p, s.bm, s.bn, dim3(s.col_tiles, s.row_tiles, s.ksplit),
+                                     s.lds, st);
     return launch_any<false>(fmt, p, s.bm, dim3(s.col_tiles, s.row_tiles), s.lds, st);
 }
 

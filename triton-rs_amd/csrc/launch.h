@@ -64,12 +64,18 @@ struct PrefillParams {
     // num_post_padded are then unused
     const int32_t* tiles;
     const int32_t* num_tiles;
+    // dense split-K (ksplit > 1): workgroup z computes K stages [z ns, (z+1) ns) into
+    // ws[z][M][N] (fp32); the last of a tile's splits sums them in split order
+    float* ws;
+    uint32_t* counters;       // one per tile (FLAG_STRIDE apart), zero between calls
+    int ksplit;
 };
 
 struct PrefillShape {
     bool ok;
     bool dma;               // pipelined kernel (LDS-DMA); else the register-staged one
     int bm, bn, col_tiles, row_tiles;
+    int ksplit;             // K splits across workgroups (1: none)
     size_t lds;
 };
 
