@@ -217,3 +217,25 @@ def test_fused_layer_expert_tiles_equal_block_composition(torch_cuda, case):
     diff = np.argwhere(got != want)
     assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
     assert np.all(np.isfinite(y.cpu().numpy()))
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, AWQ])
+def test_fused_layer_down_projection_split_k(torch_cuda, fmt):
+    """A long down projection (I = 8192) splits its K over two workgroups per tile (fp32
+    partials summed in split order): the layer stays within the GEMM tolerance of the
+    block_m composition, and repeated calls are bit-identical."""
+    T, E, topk, K, I, G = 512, 4, 2, 256, 8192, 128
+    P = pkg()
+    g = np.random.default_rng(90 + fmt)
+    x = to_dev(synth.rand_x(g, T, K))
+    logits = to_dev(g.standard_normal((T, E)).astype(np.float32))
+    w13 = tuple(to_dev(a) for a in stacked_weights(fmt, E, K, 2 * I, G, 91))
+    w2 = tuple(to_dev(a) for a in stacked_weights(fmt, E, I, K, G, 92))
+    y1 = P.fused_moe(x, logits, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G)
+    y2 = P.fused_moe(x, logits, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G)
+    ref = _layer_by_pieces(P, x, logits, w13, w2, topk, FMT_NAME[fmt], G, 64)
+    torch_cuda.cuda.synchronize()
+    a, b = y1.cpu().numpy(), y2.cpu().numpy()
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+    assert np.all(np.isfinite(a))
+    assert_parity(a, ref.cpu().numpy().astype(np.float64), what="split-K down projection")

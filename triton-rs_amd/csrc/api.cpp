@@ -479,9 +479,12 @@ W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk
 
 namespace {
 struct MoeLayout {
-    size_t ids, weights, sorted, experts, npp, tiles, ntiles, h, a, yp, total;
-    int32_t capacity, max_tiles;
+    size_t ids, weights, sorted, experts, npp, tiles, ntiles, h, a, yp, part, ctr, total;
+    int32_t capacity, max_tiles, n_ctr;
 };
+// The down projection may split its K (= I) in two (moe_tiles): fp32 partials for every
+// pair and a counter per tile. Reserved whenever the shape allows the split.
+bool moe_down_may_split(int32_t K, int32_t I) { return K % 256 == 0 && I % 128 == 0 && I / 128 >= 64; }
 size_t up256(size_t v) { return (v + 255) / 256 * 256; }
 MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, int32_t block_m) {
     MoeLayout L{};
@@ -500,6 +503,13 @@ MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, i
     L.h = off; off = up256(off + (size_t)P * 2 * I * 2);
     L.a = off; off = up256(off + (size_t)P * I * 2);
     L.yp = off; off = up256(off + (size_t)P * K * 2);
+    L.n_ctr = 0;
+    L.part = L.ctr = off;
+    if (moe_down_may_split(K, I)) {
+        L.part = off; off = up256(off + (size_t)2 * P * K * 4);
+        L.n_ctr = L.max_tiles * (K / 256);
+        L.ctr = off; off = up256(off + (size_t)L.n_ctr * FLAG_STRIDE * 4);
+    }
     L.total = off;
     return L;
 }
@@ -509,7 +519,7 @@ MoeLayout moe_layout(int32_t T, int32_t E, int32_t topk, int32_t I, int32_t K, i
 // all of an expert's tokens and its weights are dequantised once per column tile. Tile
 // width: the fewest rounds of workgroups over the CUs times the width (ties to the wider
 // tile), for the tile count a balanced routing gives; 64-row tiles come 256 wide only.
-struct MoeTiles { int bm, bn13, bn2; };
+struct MoeTiles { int bm, bn13, bn2, ks2; };
 int moe_tile_bn(int N, int bm, int est_tiles, int cus) {
     if (bm == 64) return 256;
     int best = 0;
@@ -530,6 +540,14 @@ MoeTiles moe_tiles(int P, int E, int K, int I, int cus) {
     const int est = E * (per_expert > 0 ? per_expert : 1);
     t.bn13 = moe_tile_bn(2 * I, t.bm, est, cus);
     t.bn2 = moe_tile_bn(K, t.bm, est, cus);
+    // down projection with 128-wide tiles and a long K: 256-wide tiles with K split in two
+    // (as the dense prefill does; config 4: 16 x 8 x 2 = 256 workgroups)
+    t.ks2 = 1;
+    if (t.bn2 == 128 && t.bm > 64 && moe_down_may_split(K, I) &&
+        (long long)est * (K / 256) * 2 <= cus) {
+        t.bn2 = 256;
+        t.ks2 = 2;
+    }
     return t;
 }
 }  // namespace
@@ -586,8 +604,9 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
             return fail(W4A16_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
         auto* tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
         auto* ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
+        auto* ctr = reinterpret_cast<uint32_t*>(ws + L.ctr);
         hipError_t e = launch_moe_align(ids, P, E, block_m, L.capacity, sorted, experts, npp, st,
-                                        mt.bm, tiles, ntiles);
+                                        mt.bm, tiles, ntiles, ctr, mt.ks2 > 1 ? L.n_ctr : 0);
         if (e != hipSuccess) return hip_fail(e, "moe align launch");
         const int max_tiles = moe_max_tiles(P, E, mt.bm);
         PrefillParams p{};
@@ -616,6 +635,11 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
         p.N = K; p.K = I; p.a_div = 1;
         p.qweight_stride = (int64_t)I * K / 8; p.scales_stride = (int64_t)(I / G) * K;
         p.qzeros_stride = (int64_t)(I / G) * K / 8;
+        if (mt.ks2 > 1) {
+            p.ksplit = mt.ks2;
+            p.ws = reinterpret_cast<float*>(ws + L.part);
+            p.counters = ctr;
+        }
         e = launch_moe_gemm_tiles(fmt, p, mt.bm, mt.bn2, max_tiles, st);
         if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
         return w4a16_moe_sum(stream, yp, wts, out, T, topk, K);

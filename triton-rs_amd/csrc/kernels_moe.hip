@@ -74,7 +74,7 @@ __global__ void __launch_bounds__(ALIGN_THREADS)
 moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int capacity,
                  int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
                  int32_t* __restrict__ num_post_padded, int tile_bm, int32_t* __restrict__ tiles,
-                 int32_t* __restrict__ num_tiles) {
+                 int32_t* __restrict__ num_tiles, uint32_t* __restrict__ counters, int n_counters) {
     __shared__ int cnt[ALIGN_MAX_E];
     __shared__ int start[ALIGN_MAX_E];
     __shared__ int wave_tot[ALIGN_THREADS / 64];
@@ -82,6 +82,8 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
     for (int e = tid; e < E; e += ALIGN_THREADS) cnt[e] = 0;
+    // split-K counters of the grouped GEMMs that follow start at zero on every call
+    for (int i = tid; i < n_counters; i += ALIGN_THREADS) counters[(size_t)i * FLAG_STRIDE] = 0u;
     __syncthreads();
     for (int p = tid; p < P; p += ALIGN_THREADS) atomicAdd(&cnt[ids[p]], 1);
     __syncthreads();
@@ -154,13 +156,15 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
 
 hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
-                            hipStream_t st, int tile_bm, int32_t* tiles, int32_t* num_tiles) {
+                            hipStream_t st, int tile_bm, int32_t* tiles, int32_t* num_tiles,
+                            uint32_t* counters, int n_counters) {
     (void)hipGetLastError();
     if (E > ALIGN_MAX_E) return hipErrorInvalidValue;
     if (tiles && (tile_bm < 16 || tile_bm % 16 || !num_tiles)) return hipErrorInvalidValue;
+    if (n_counters && !counters) return hipErrorInvalidValue;
     hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(ALIGN_THREADS), 0, st, ids, P, E, block_m,
                        capacity, sorted_ids, expert_ids, num_post_padded, tile_bm, tiles,
-                       num_tiles);
+                       num_tiles, counters, n_counters);
     return hipGetLastError();
 }
 

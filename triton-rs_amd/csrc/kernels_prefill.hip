@@ -370,10 +370,10 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     (void)rows;
     const int n0 = blockIdx.x * BN;
     const int NW = p.N >> 3;
-    // split-K (dense only): this workgroup's K stages are [s0, s0 + ns)
-    const int ksp = MOE ? 1 : max(p.ksplit, 1);
+    // split K: this workgroup's K stages are [s0, s0 + ns)
+    const int ksp = max(p.ksplit, 1);
     const int ns = p.K / BK / ksp;
-    const int s0 = MOE ? 0 : (int)blockIdx.z * ns;
+    const int s0 = (int)blockIdx.z * ns;
 
     if constexpr (MOE) {
         int e;
@@ -643,37 +643,38 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     wait_vmcnt<0>();   // no LDS write may be in flight when the workgroup ends
 
     // ---- epilogue: lane holds D[4 kb + i][j] of each 16 x 16 block
-    if constexpr (!MOE) {
-        if (ksp > 1) {
-            // partials of this split, then the last split of the tile sums all of them in
-            // split order (deterministic) and writes the fp16 tile
-            __shared__ int last_flag;
-            const size_t MN = (size_t)p.M * p.N;
-            float* mine = p.ws + (size_t)blockIdx.z * MN;
+    if (ksp > 1) {
+        // partials of this split (rows of the output: M rows, or pairs in MoE mode), then
+        // the last split of the tile sums all of them in split order (deterministic) and
+        // writes the fp16 tile
+        __shared__ int last_flag;
+        const size_t MN = (size_t)(MOE ? p.num_pairs : p.M) * p.N;
+        float* mine = p.ws + (size_t)blockIdx.z * MN;
 #pragma unroll
-            for (int r = 0; r < RB; ++r)
+        for (int r = 0; r < RB; ++r)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = m0 + row0 + RSTEP * r + 4 * kb + i;
-                    if (m >= p.M) continue;
-                    float* dst = mine + (size_t)m * p.N + n0 + wn * WN + j;
+            for (int i = 0; i < 4; ++i) {
+                const int m = dst_row(row0 + RSTEP * r + 4 * kb + i);
+                if (m < 0) continue;
+                float* dst = mine + (size_t)m * p.N + n0 + wn * WN + j;
 #pragma unroll
-                    for (int c = 0; c < CB; ++c) st_partial<SCOPE_DEVICE>(dst + 16 * c, acc[r][c][i]);
-                }
-            const int tile = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
-            if (!splitk_arrive(splitk_counter(p.counters, tile), ksp, &last_flag)) return;
-            constexpr int C4 = BN / 4;
-            const int rows = min(BM, p.M - m0);
-            for (int idx = t; idx < rows * C4; idx += PF_THREADS) {
-                const int r = idx / C4, c = 4 * (idx - r * C4);
-                const size_t off = (size_t)(m0 + r) * p.N + n0 + c;
-                float4_t v = ld_partial4<SCOPE_DEVICE>(p.ws + off);
-                for (int sp = 1; sp < ksp; ++sp) v += ld_partial4<SCOPE_DEVICE>(p.ws + sp * MN + off);
-                const half2_t lo = {(half_t)v.x, (half_t)v.y}, hi = {(half_t)v.z, (half_t)v.w};
-                *reinterpret_cast<u32x2*>(p.out + off) = u32x2{as_u32(lo), as_u32(hi)};
+                for (int c = 0; c < CB; ++c) st_partial<SCOPE_DEVICE>(dst + 16 * c, acc[r][c][i]);
             }
-            return;
+        const int tile = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
+        if (!splitk_arrive(splitk_counter(p.counters, tile), ksp, &last_flag)) return;
+        constexpr int C4 = BN / 4;
+        const int nrows = MOE ? rows : min(BM, p.M - m0);
+        for (int idx = t; idx < nrows * C4; idx += PF_THREADS) {
+            const int lr = idx / C4, c = 4 * (idx - lr * C4);
+            const int m = dst_row(lr);
+            if (m < 0) continue;
+            const size_t off = (size_t)m * p.N + n0 + c;
+            float4_t v = ld_partial4<SCOPE_DEVICE>(p.ws + off);
+            for (int sp = 1; sp < ksp; ++sp) v += ld_partial4<SCOPE_DEVICE>(p.ws + sp * MN + off);
+            const half2_t lo = {(half_t)v.x, (half_t)v.y}, hi = {(half_t)v.z, (half_t)v.w};
+            *reinterpret_cast<u32x2*>(p.out + off) = u32x2{as_u32(lo), as_u32(hi)};
         }
+        return;
     }
 #pragma unroll
     for (int r = 0; r < RB; ++r)
@@ -866,7 +867,10 @@ hipError_t launch_moe_gemm_tiles(int fmt, const PrefillParams& p, int tile_bm, i
     if (!p.tiles || !p.num_tiles || !shape_ok ||
         !moe_tiles_supported(p.N, p.K, p.G, (p.num_pairs + p.a_div - 1) / p.a_div, bn))
         return hipErrorInvalidValue;
-    return launch_dma_any<true>(fmt, p, tile_bm, bn, dim3(p.N / bn, max_tiles),
+    if (p.ksplit > 1 && (!p.ws || !p.counters || (p.K / BK) % p.ksplit ||
+                         (size_t)(p.N / bn) * max_tiles > SPLITK_MAX_TILES))
+        return hipErrorInvalidValue;
+    return launch_dma_any<true>(fmt, p, tile_bm, bn, dim3(p.N / bn, max_tiles, max(p.ksplit, 1)),
                                 prefill_dma_lds(tile_bm, bn), st);
 }
 

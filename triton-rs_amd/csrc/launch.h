@@ -98,7 +98,8 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int ren
 hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int capacity,
                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_post_padded,
                             hipStream_t st, int tile_bm = 0, int32_t* tiles = nullptr,
-                            int32_t* num_tiles = nullptr);
+                            int32_t* num_tiles = nullptr, uint32_t* counters = nullptr,
+                            int n_counters = 0);
 // Upper bound on the expert tiles of tile_bm rows that P pairs over E experts can need.
 inline int moe_max_tiles(int P, int E, int tile_bm) { return (P + tile_bm - 1) / tile_bm + E; }
 hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
