@@ -175,8 +175,8 @@ W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, 
 W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk_weights,
                             void* out, int32_t T, int32_t topk, int32_t K);
 
-/* Bytes of workspace w4a16_fused_moe needs (routing tables, expert tile list and fp16
- * intermediates). */
+/* Bytes of workspace w4a16_fused_moe needs (routing tables, expert tile list, fp16
+ * intermediates and, when I >= 8192, the down projection's fp32 split-K partials). */
 W4A16_API size_t w4a16_fused_moe_workspace_size(int32_t T, int32_t E, int32_t topk, int32_t I,
                                                 int32_t K, int32_t block_m);
 
