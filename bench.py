@@ -298,7 +298,7 @@ def extras(torch, pkg, dev, stream, args):
         ws = torch.empty(pkg.lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, bm),
                          dtype=torch.uint8, device=dev)
         ms = time_direct(torch, lambda i: pkg.fused_moe(x, logits, w13, w2, topk=topk, block_m=bm,
-                                                        out=out, workspace=ws), 50, stream, warm=5)
+                                                        out=out, workspace=ws), 50, stream, warm=20)
         res[f"c4_fused_moe_block_m{bm}"] = {
             "ms_per_layer": round(ms, 3), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
             "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
