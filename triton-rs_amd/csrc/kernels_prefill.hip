@@ -286,6 +286,10 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
 //  B [8 chunks][256 columns] of 8 k each: column n at position n ^ ((n >> 3) & 7).
 // A is staged in natural k order (GPTQ's unpack order is undone on the B side with
 // v_perm_b32).
+//
+// Variants of the same kernel: dense (rows m0 + r of x); grouped MoE (rows gathered
+// through sorted pair ids), over block_m blocks or over expert tiles from a list; and split
+// K (grid z = K splits, fp32 partials, the last split of a tile sums them in split order).
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
 
 namespace {
