@@ -239,3 +239,39 @@ def test_fused_layer_down_projection_split_k(torch_cuda, fmt):
     assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
     assert np.all(np.isfinite(a))
     assert_parity(a, ref.cpu().numpy().astype(np.float64), what="split-K down projection")
+
+
+def _moe_cases(n=10, seed=77):
+    g = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        E = int(g.choice([2, 4, 8, 16, 32]))
+        topk = int(g.integers(1, min(E, 4) + 1))
+        T = int(g.integers(1, 700))
+        K = 256 * int(g.integers(1, 5))
+        I = 128 * int(g.integers(1, 9))
+        out.append((T, E, topk, K, I, int(g.choice([GPTQ, SYM, AWQ]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _moe_cases(), ids=lambda c: "T{}_E{}_k{}_K{}_I{}_f{}".format(*c))
+def test_fused_layer_random_shapes_equal_block_composition(torch_cuda, case):
+    """Seeded random layers (token counts 1..700, 2..32 experts, top-1..4): the expert-tile
+    layer equals the block_m composition of the pieces bit for bit."""
+    torch = torch_cuda
+    T, E, topk, K, I, fmt = case
+    P = pkg()
+    g = np.random.default_rng(T * 31 + E * 7 + I)
+    x = to_dev(synth.rand_x(g, T, K))
+    logits = to_dev(g.standard_normal((T, E)).astype(np.float32))
+    G = 128
+    w13 = tuple(to_dev(a) for a in stacked_weights(fmt, E, K, 2 * I, G, 93))
+    w2 = tuple(to_dev(a) for a in stacked_weights(fmt, E, I, K, G, 94))
+    if fmt == SYM:
+        w13, w2 = (w13[0], w13[1], None), (w2[0], w2[1], None)
+    y = P.fused_moe(x, logits, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G)
+    ref = _layer_by_pieces(P, x, logits, w13, w2, topk, FMT_NAME[fmt], G, 64)
+    torch.cuda.synchronize()
+    got, want = y.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16)
+    diff = np.argwhere(got != want)
+    assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
