@@ -29,11 +29,14 @@
 namespace w4a16 {
 
 namespace {
-// waves per workgroup: 8 for 32-row tiles (the same wave count with half the workgroup
+// waves per workgroup: 8 for GPTQ 32-row tiles (the same wave count with half the workgroup
 // splits, so half the split-K partials: config 2 M=32 12.3 -> 11.9 us plain, 15.3 -> 14.1 us
-// act-order; at M=16 the 4-wave tile was faster, 9.7 vs 10.9 us; 64-row tiles keep 4 for
-// the reduction buffer)
-constexpr int skinny_waves(int bm) { return bm == 32 ? 8 : 4; }
+// act-order; at M=16 the 4-wave tile was faster, 9.7 vs 10.9 us); 4 otherwise (64-row tiles
+// and AWQ, whose 8-column strips would not fit the reduction buffer twice: AWQ M=32
+// 4096 -> 14336 22.2 us with 4 waves against 30.9 us with 8)
+constexpr int skinny_waves(int fmt, int bm, int cpl) {
+    return fmt != FMT_AWQ && bm == 32 && cpl < 8 ? 8 : 4;
+}
 __device__ __forceinline__ half2_t deq2(half2_t h, half2_t hz, half2_t hs) { return (h - hz) * hs; }
 __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t d) {
     return half8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
@@ -41,10 +44,11 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }  // namespace
 
 template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD>
-__global__ void __launch_bounds__(64 * skinny_waves(BM)) skinny_kernel(SkinnyParams p) {
+__global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
-    static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ), "columns per lane");
-    constexpr int W = skinny_waves(BM), NT = 64 * W;
+    static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
+                  "columns per lane");
+    constexpr int W = skinny_waves(FMT, BM, CPL), NT = 64 * W;
     static_assert(NT <= FINISH_MAX_THREADS, "split-K finish buffer");
     constexpr int RB = BM / 16;
     constexpr int WN = 16 * CPL;
@@ -76,7 +80,7 @@ __global__ void __launch_bounds__(64 * skinny_waves(BM)) skinny_kernel(SkinnyPar
         const int kg = 32 * step;
         // packed weights
         if constexpr (FMT == FMT_AWQ) {
-            const int wcol = nl >> 3;
+            const int wcol = (CPL == 8) ? (n0 >> 3) + j : (nl >> 3);
             const uint32_t off0 = (uint32_t)(kg + 8 * kb) * (uint32_t)NW + (uint32_t)wcol;
 #pragma unroll
             for (int r = 0; r < 8; ++r)
@@ -113,7 +117,10 @@ __global__ void __launch_bounds__(64 * skinny_waves(BM)) skinny_kernel(SkinnyPar
         // scales and zero word of the lane's columns for this step's group
         const int g = kg / p.G;
         const uint32_t* sp = reinterpret_cast<const uint32_t*>(p.scales + (size_t)g * p.N + nl);
-        if constexpr (CPL == 4) {
+        if constexpr (CPL == 8) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(sp);
+            sreg[u][0] = v.x; sreg[u][1] = v.y; sreg[u][2] = v.z; sreg[u][3] = v.w;
+        } else if constexpr (CPL == 4) {
             const u32x2 v = *reinterpret_cast<const u32x2*>(sp);
             sreg[u][0] = v.x; sreg[u][1] = v.y;
         } else {
@@ -174,13 +181,23 @@ __global__ void __launch_bounds__(64 * skinny_waves(BM)) skinny_kernel(SkinnyPar
                     const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
                     const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
                     const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
-                    // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
-                    const int sh = 8 * (j & 1);
-                    const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
-                    pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
-                    pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
-                    pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
-                    pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
+                    if constexpr (CPL == 8) {
+                        // the whole word: slot sl holds column awq_col_of_slot(sl)
+#pragma unroll
+                        for (int sl = 0; sl < 8; ++sl) {
+                            const uint32_t src = sl < 4 ? p0 : p1;
+                            const int col = awq_col_of_slot(sl);
+                            pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
+                        }
+                    } else {
+                        // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
+                        const int sh = 8 * (j & 1);
+                        const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
+                        pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
+                        pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
+                        pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
+                        pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
+                    }
                 }
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
@@ -273,15 +290,25 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     // without g_idx a k32 step lies in one group; with it the group comes from the table
     if (gidx ? (fmt == FMT_AWQ || G < 1) : (G % 32 || K % G)) return s;
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
-    // the 8-wave tile consumes K in steps of 256 rows; other K take the 64-row tile
-    if (skinny_waves(s.bm) == 8 && K % 256) s.bm = 64;
     const bool awq = fmt == FMT_AWQ;
-    // 4 columns per lane where N allows (the wider strip re-reads the activations from L2
-    // half as often as 2); AWQ needs 4 (half an AWQ word per lane)
-    int cpl = 0;
-    for (int c : {4, 2}) {
-        if (awq && c < 4) continue;
-        if (N % (16 * c) == 0) { cpl = c; break; }
+    // GPTQ: 4 columns per lane where N allows (the wider strip re-reads the activations from
+    // L2 half as often as 2). AWQ: a whole AWQ word (8 columns) per lane for tiles of up to
+    // 32 rows and N >= 4096 (with 4, two lanes load each word: M=16, 4096 -> 14336: 21.4 ->
+    // 15.5 us; at N=2048 the halved strip count cost more than it saved, 10.8 -> 12.4 us),
+    // else half a word (the 64-row reduction buffer does not fit 8)
+    auto pick_cpl = [&](int bm) {
+        for (int c : {8, 4, 2}) {
+            if (awq ? c < 4 : c > 4) continue;
+            if (c == 8 && (bm > 32 || N < 4096)) continue;   // small N: keep the strips
+            if (N % (16 * c) == 0) return c;
+        }
+        return 0;
+    };
+    int cpl = pick_cpl(s.bm);
+    // the 8-wave tile consumes K in steps of 256 rows; other K take the 64-row tile
+    if (cpl && skinny_waves(fmt, s.bm, cpl) == 8 && K % 256) {
+        s.bm = 64;
+        cpl = pick_cpl(s.bm);
     }
     if (!cpl) return s;
     if (gidx) {
@@ -295,14 +322,22 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     // workgroups x M near 12K (measured optimum at K=4096, N=6144: 8 splits at M=16, 4 at
     // M=32, 2 at M=64; more splits cost more in partial traffic than they gain in width)
     // (counted in units of 4 waves: quads = splits x waves / 4)
+    // AWQ with 8-column strips: up to 2 workgroups per CU at M <= 16, 1 above (measured at
+    // M = 9..32 on both config-1 shapes: e.g. M=24, 4096 -> 14336 21.1 us with 224
+    // workgroups against 26.6 with 448; M=32, 14336 -> 4096 21.5 with 256 against 32.3 with
+    // 128)
+    auto more = [&](int q) {
+        if (cpl == 8) return (long long)s.col_tiles * 2 * q <= (M <= 16 ? 2 : 1) * num_cus;
+        return (long long)s.col_tiles * 2 * q * M <= 12288;
+    };
     int quads = 1;
     while (s.col_tiles * quads < 2 * num_cus && K % (128 * 2 * quads) == 0 &&
-           2 * quads * 32 * M <= K && (long long)s.col_tiles * 2 * quads * M <= 12288)
+           2 * quads * 32 * M <= K && more(quads))
         quads *= 2;
-    const int wq = skinny_waves(s.bm) / 4;
+    const int wq = skinny_waves(fmt, s.bm, cpl) / 4;
     const int splits = quads >= wq ? quads / wq : 1;
     s.splits = splits;
-    s.steps_per_wave = K / (32 * skinny_waves(s.bm) * splits);
+    s.steps_per_wave = K / (32 * skinny_waves(fmt, s.bm, cpl) * splits);
     s.xcd = xcd_placement && splits > 1 && s.col_tiles % 8 == 0;
     s.ok = true;
     return s;
@@ -319,11 +354,11 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
                 reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true, XCD>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
             if (attr != hipSuccess) return attr;
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(64 * skinny_waves(BM)), s.lds, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), s.lds, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(64 * skinny_waves(BM)), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
     return hipGetLastError();
 }
 
@@ -336,6 +371,8 @@ template <int FMT, int BM>
 static hipError_t launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (FMT != FMT_AWQ) {
         if (s.cpl == 2) return launch_t<FMT, BM, 2>(p, s, st);
+    } else if constexpr (BM <= 32) {
+        if (s.cpl == 8) return launch_t<FMT, BM, 8>(p, s, st);
     }
     return launch_t<FMT, BM, 4>(p, s, st);
 }
