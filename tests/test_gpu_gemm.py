@@ -102,7 +102,7 @@ def test_gemv_deterministic_and_reusable(torch_cuda, orc):
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
 @pytest.mark.parametrize("M,K,N", [(5, 1024, 512), (8, 4096, 1024), (16, 512, 256),
                                    (20, 384, 256), (12, 1024, 4096), (32, 512, 4096),
-                                   (33, 1024, 512), (64, 2048, 768), (128, 1024, 512),
+                                   (48, 512, 4096), (33, 1024, 512), (64, 2048, 768), (128, 1024, 512),
                                    (200, 512, 1024)])
 def test_mfma_shapes(torch_cuda, orc, fmt, M, K, N):
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2000 + M + 7 * fmt)

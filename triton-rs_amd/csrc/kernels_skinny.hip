@@ -292,14 +292,15 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     s.bm = M <= 16 ? 16 : M <= 32 ? 32 : 64;
     const bool awq = fmt == FMT_AWQ;
     // GPTQ: 4 columns per lane where N allows (the wider strip re-reads the activations from
-    // L2 half as often as 2). AWQ: a whole AWQ word (8 columns) per lane for tiles of up to
-    // 32 rows and N >= 4096 (with 4, two lanes load each word: M=16, 4096 -> 14336: 21.4 ->
-    // 15.5 us; at N=2048 the halved strip count cost more than it saved, 10.8 -> 12.4 us),
-    // else half a word (the 64-row reduction buffer does not fit 8)
+    // L2 half as often as 2). AWQ: a whole AWQ word (8 columns) per lane where N >= 4096 (with
+    // 4, two lanes load each word: 4096 -> 14336 at M=16 21.4 -> 15.5 us, M=64 43.8 -> 32.0
+    // us; at N=2048 the halved strip count cost more than it saved, 10.8 -> 12.4 us), else
+    // half a word. (The 64-row, 8-column reduction buffer takes 132 KB of LDS: no room for
+    // an act-order table, which AWQ never has.)
     auto pick_cpl = [&](int bm) {
         for (int c : {8, 4, 2}) {
             if (awq ? c < 4 : c > 4) continue;
-            if (c == 8 && (bm > 32 || N < 4096)) continue;   // small N: keep the strips
+            if (c == 8 && N < 4096) continue;   // small N: keep the strips
             if (N % (16 * c) == 0) return c;
         }
         return 0;
@@ -371,7 +372,7 @@ template <int FMT, int BM>
 static hipError_t launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (FMT != FMT_AWQ) {
         if (s.cpl == 2) return launch_t<FMT, BM, 2>(p, s, st);
-    } else if constexpr (BM <= 32) {
+    } else {
         if (s.cpl == 8) return launch_t<FMT, BM, 8>(p, s, st);
     }
     return launch_t<FMT, BM, 4>(p, s, st);
