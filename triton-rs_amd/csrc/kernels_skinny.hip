@@ -4,9 +4,10 @@
 //
 // A workgroup owns a strip of WN = 16*CPL columns; its waves (4, or 8 for 32-row tiles)
 // split the strip's K range and stream independently (no LDS staging, no barrier in the main
-// loop). Each
-// lane keeps a ring of PF k32 steps of loads in flight: its packed words, the activation
-// fragments and the group's scales/zeros. Words are dequantised bit-exactly
+// loop). Each lane keeps a ring of PF k32 steps of loads in flight: its packed words, the
+// activation fragments and the group's scales/zeros. Every load of the steady state is
+// unconditional (rows past M are loaded clamped and zeroed at use), so the compiler's
+// wait counts let each step wait for its own slot only. Words are dequantised bit-exactly
 // (W16 = RNE_f16((q - z) * s), crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:246-260,
 // awq_gemm_int4_typed.rs:213-228) straight into MFMA B-operand registers and multiplied
 // with v_mfma_f32_16x16x32_f16 (fp32 accumulation, the reference's tt.dot). The waves'
@@ -43,7 +44,9 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }
 }  // namespace
 
-template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD>
+// SPW: k32 steps per wave when known at compile time (SPW = PF: the prologue issues every
+// step and no loop is emitted), 0 for the runtime count p.steps_per_wave
+template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD, int SPW>
 __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
@@ -67,7 +70,7 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
     const int n0 = ct * WN;
     const int nl = n0 + CPL * j;              // first output column of this lane
     const int NW = p.N >> 3;
-    const int spw = p.steps_per_wave;
+    const int spw = SPW ? SPW : p.steps_per_wave;
     const int step0 = (split * W + wave) * spw;  // first k32 step of this wave
 
     // ------------------------------------------------ per-step loads into ring slot u
@@ -99,12 +102,12 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
                 }
             }
         }
-        // activation fragments: row 16 r + j, k = kg + 8 kb .. + 7 (rows >= M read as 0)
+        // activation fragments: row 16 r + j, k = kg + 8 kb .. + 7; rows >= M load row M - 1
+        // and are zeroed where they are used, so that every lane issues every load
 #pragma unroll
         for (int r = 0; r < RB; ++r) {
-            const int m = 16 * r + j;
-            areg[u][r] = (m < p.M) ? *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + kg + 8 * kb)
-                                   : u32x4{0u, 0u, 0u, 0u};
+            const int m = min(16 * r + j, p.M - 1);
+            areg[u][r] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + kg + 8 * kb);
         }
         if constexpr (GIDX) {
             // groups of the lane's 8 k rows
@@ -135,128 +138,180 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
 #pragma unroll
         for (int c = 0; c < CPL; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-#pragma unroll
-    for (int u = 0; u < PF; ++u)
-        if (u < spw) issue(u, step0 + u);
-
+    // Act-order table: entry o = (group o / WN, strip column o % WN). Loads of one wave
+    // complete in issue order, so where the table fits TE entries per thread its scales and
+    // zeros are loaded into registers before the weight stream and written to LDS after it
+    // has been issued; the table is then ready about when the first weights arrive (loaded
+    // after the stream, its build waited for all of it: config 2 M=16 12.5 -> 10.9 us).
     const int ngroups = (p.K + p.G - 1) / p.G;
+    constexpr int TE = GIDX ? 8 : 1;
+    const int tab_n = GIDX ? ngroups * WN : 0;
+    const bool tab_early = GIDX && tab_n <= TE * NT;
+    uint32_t tsc[TE], tzw[TE];
+    auto tab_entry = [&](uint32_t sc, uint32_t zw, int o) -> uint32_t {
+        const int g = o / WN, n = n0 + (o - g * WN);
+        const int z = (FMT == FMT_GPTQ_SYM) ? 8 : nib(zw, n & 7) + p.zero_offset;
+        const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
+        return sc | (zf << 16);
+    };
     if constexpr (GIDX) {
-        for (int o = threadIdx.x; o < ngroups * WN; o += NT) {
-            const int g = o / WN, n = n0 + (o - g * WN);
-            const uint32_t sc = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
-            const int z = (FMT == FMT_GPTQ_SYM)
-                              ? 8 : nib(p.qzeros[(size_t)g * NW + (n >> 3)], n & 7) + p.zero_offset;
-            const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
-            gtab[o] = sc | (zf << 16);
+        if (tab_early) {
+#pragma unroll
+            for (int e = 0; e < TE; ++e) {
+                const int o = min((int)threadIdx.x + e * NT, tab_n - 1);   // in range: loads unconditional
+                const int g = o / WN, n = n0 + (o - g * WN);
+                tsc[e] = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
+                tzw[e] = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (n >> 3)];
+            }
+        }
+    }
+
+    // prologue: PF steps in flight (a wave with fewer steps re-reads its last one, so the
+    // number of loads in flight is known at compile time)
+#pragma unroll
+    for (int u = 0; u < PF; ++u) issue(u, step0 + min(u, spw - 1));
+
+    if constexpr (GIDX) {
+        if (tab_early) {
+#pragma unroll
+            for (int e = 0; e < TE; ++e) {
+                const int o = (int)threadIdx.x + e * NT;
+                if (o < tab_n) gtab[o] = tab_entry(tsc[e], tzw[e], o);
+            }
+        } else {
+            for (int o = threadIdx.x; o < tab_n; o += NT) {
+                const int g = o / WN, n = n0 + (o - g * WN);
+                const uint32_t sc = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
+                const uint32_t zw = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (n >> 3)];
+                gtab[o] = tab_entry(sc, zw, o);
+            }
         }
         __syncthreads();
     }
 
-    for (int s0 = 0; s0 < spw; s0 += PF) {
+    // one k32 step from ring slot u
+    auto compute = [&](int u) __attribute__((always_inline)) {
+        // zero point (as fp16 1024 + z) and scale per column, splatted
+        half2_t hz[CPL], hs[CPL];
+#pragma unroll
+        for (int c = 0; c < (GIDX ? 0 : CPL); ++c) {
+            const int cw = (nl & 7) + c;   // column within its qzeros word
+            int z;
+            if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
+            else if constexpr (FMT == FMT_AWQ) z = nib(zreg[u], awq_slot(cw));
+            else z = nib(zreg[u], cw) + p.zero_offset;
+            const half_t zh = (half_t)(1024 + z);
+            hz[c] = half2_t{zh, zh};
+            const half2_t sv = as_h2(sreg[u][c >> 1]);
+            const half_t sc = (c & 1) ? sv.y : sv.x;
+            hs[c] = half2_t{sc, sc};
+        }
+        // dequantise B fragments
+        half8_t bf[CPL];
+        if constexpr (FMT == FMT_AWQ) {
+            half2_t pr[4][CPL];
+#pragma unroll
+            for (int rp = 0; rp < 4; ++rp) {
+                const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
+                const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
+                const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
+                if constexpr (CPL == 8) {
+                    // the whole word: slot sl holds column awq_col_of_slot(sl)
+#pragma unroll
+                    for (int sl = 0; sl < 8; ++sl) {
+                        const uint32_t src = sl < 4 ? p0 : p1;
+                        const int col = awq_col_of_slot(sl);
+                        pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
+                    }
+                } else {
+                    // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
+                    const int sh = 8 * (j & 1);
+                    const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
+                    pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
+                    pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
+                    pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
+                    pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+        } else if constexpr (GIDX) {
+            // entries of rows k0..k7 for the lane's columns; a g_idx outside the table
+            // is clamped into [0, groups - 1], as in the generic kernel
+            uint32_t t[8][CPL];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t g = (uint32_t)min(max(greg[u][i], 0), ngroups - 1);
+                const uint32_t* row = gtab + g * WN + CPL * j;
+                if constexpr (CPL == 2) {
+                    const u32x2 v = *reinterpret_cast<const u32x2*>(row);
+                    t[i][0] = v.x; t[i][1] = v.y;
+                } else {
+#pragma unroll
+                    for (int h = 0; h < CPL / 4; ++h) {
+                        const u32x4 v = *reinterpret_cast<const u32x4*>(row + 4 * h);
+                        t[i][4 * h + 0] = v.x; t[i][4 * h + 1] = v.y;
+                        t[i][4 * h + 2] = v.z; t[i][4 * h + 3] = v.w;
+                    }
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t w = bw[u][c];
+                half2_t pr[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    // the pair holds rows k_q (low half) and k_{q+4} (high half)
+                    const half2_t s2 = as_h2(perm(t[q + 4][c], t[q][c], 0x05040100u));
+                    const half2_t z2 = as_h2(perm(t[q + 4][c], t[q][c], 0x07060302u));
+                    pr[q] = deq2(nib_pair(w >> (4 * q)), z2, s2);
+                }
+                bf[c] = cat8(pr[0], pr[1], pr[2], pr[3]);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const uint32_t w = bw[u][c];
+                bf[c] = cat8(deq2(nib_pair(w), hz[c], hs[c]), deq2(nib_pair(w >> 4), hz[c], hs[c]),
+                             deq2(nib_pair(w >> 8), hz[c], hs[c]), deq2(nib_pair(w >> 12), hz[c], hs[c]));
+            }
+        }
+        // MFMAs
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            u32x4 a = areg[u][r];
+            if (16 * r + j >= p.M) a = u32x4{0u, 0u, 0u, 0u};
+            if constexpr (FMT != FMT_AWQ)   // k order (0,4)(1,5)(2,6)(3,7) as in the GPTQ unpack
+                a = u32x4{perm(a.z, a.x, 0x05040100u), perm(a.z, a.x, 0x07060302u),
+                          perm(a.w, a.y, 0x05040100u), perm(a.w, a.y, 0x07060302u)};
+            const half8_t af = __builtin_bit_cast(half8_t, a);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c)
+                acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c], acc[r][c], 0, 0, 0);
+        }
+    };
+
+    // Steady state: every step issues the step PF ahead, unconditionally, so the number of
+    // loads in flight is the same on every iteration and each step waits only for its own
+    // slot. The last 2 PF - 1 or fewer steps run in the tail.
+    int s0 = 0;
+    for (; s0 + 2 * PF <= spw; s0 += PF) {
 #pragma unroll
         for (int u = 0; u < PF; ++u) {
-            const int s = s0 + u;
-            if (s >= spw) break;
-            // zero point (as fp16 1024 + z) and scale per column, splatted
-            half2_t hz[CPL], hs[CPL];
-#pragma unroll
-            for (int c = 0; c < (GIDX ? 0 : CPL); ++c) {
-                const int cw = (nl & 7) + c;   // column within its qzeros word
-                int z;
-                if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
-                else if constexpr (FMT == FMT_AWQ) z = nib(zreg[u], awq_slot(cw));
-                else z = nib(zreg[u], cw) + p.zero_offset;
-                const half_t zh = (half_t)(1024 + z);
-                hz[c] = half2_t{zh, zh};
-                const half2_t sv = as_h2(sreg[u][c >> 1]);
-                const half_t sc = (c & 1) ? sv.y : sv.x;
-                hs[c] = half2_t{sc, sc};
-            }
-            // dequantise B fragments
-            half8_t bf[CPL];
-            if constexpr (FMT == FMT_AWQ) {
-                half2_t pr[4][CPL];
-#pragma unroll
-                for (int rp = 0; rp < 4; ++rp) {
-                    const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
-                    const uint32_t p0 = perm(b, a, 0x05040100u);   // slots 0-3 of both rows
-                    const uint32_t p1 = perm(b, a, 0x07060302u);   // slots 4-7
-                    if constexpr (CPL == 8) {
-                        // the whole word: slot sl holds column awq_col_of_slot(sl)
-#pragma unroll
-                        for (int sl = 0; sl < 8; ++sl) {
-                            const uint32_t src = sl < 4 ? p0 : p1;
-                            const int col = awq_col_of_slot(sl);
-                            pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
-                        }
-                    } else {
-                        // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
-                        const int sh = 8 * (j & 1);
-                        const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
-                        pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
-                        pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
-                        pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
-                        pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
-            } else if constexpr (GIDX) {
-                // entries of rows k0..k7 for the lane's columns; a g_idx outside the table
-                // is clamped into [0, groups - 1], as in the generic kernel
-                uint32_t t[8][CPL];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) {
-                    const uint32_t g = (uint32_t)min(max(greg[u][i], 0), ngroups - 1);
-                    const uint32_t* row = gtab + g * WN + CPL * j;
-                    if constexpr (CPL == 2) {
-                        const u32x2 v = *reinterpret_cast<const u32x2*>(row);
-                        t[i][0] = v.x; t[i][1] = v.y;
-                    } else {
-#pragma unroll
-                        for (int h = 0; h < CPL / 4; ++h) {
-                            const u32x4 v = *reinterpret_cast<const u32x4*>(row + 4 * h);
-                            t[i][4 * h + 0] = v.x; t[i][4 * h + 1] = v.y;
-                            t[i][4 * h + 2] = v.z; t[i][4 * h + 3] = v.w;
-                        }
-                    }
-                }
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    const uint32_t w = bw[u][c];
-                    half2_t pr[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        // the pair holds rows k_q (low half) and k_{q+4} (high half)
-                        const half2_t s2 = as_h2(perm(t[q + 4][c], t[q][c], 0x05040100u));
-                        const half2_t z2 = as_h2(perm(t[q + 4][c], t[q][c], 0x07060302u));
-                        pr[q] = deq2(nib_pair(w >> (4 * q)), z2, s2);
-                    }
-                    bf[c] = cat8(pr[0], pr[1], pr[2], pr[3]);
-                }
-            } else {
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    const uint32_t w = bw[u][c];
-                    bf[c] = cat8(deq2(nib_pair(w), hz[c], hs[c]), deq2(nib_pair(w >> 4), hz[c], hs[c]),
-                                 deq2(nib_pair(w >> 8), hz[c], hs[c]), deq2(nib_pair(w >> 12), hz[c], hs[c]));
-                }
-            }
-            // MFMAs
-#pragma unroll
-            for (int r = 0; r < RB; ++r) {
-                u32x4 a = areg[u][r];
-                if constexpr (FMT != FMT_AWQ)   // k order (0,4)(1,5)(2,6)(3,7) as in the GPTQ unpack
-                    a = u32x4{perm(a.z, a.x, 0x05040100u), perm(a.z, a.x, 0x07060302u),
-                              perm(a.w, a.y, 0x05040100u), perm(a.w, a.y, 0x07060302u)};
-                const half8_t af = __builtin_bit_cast(half8_t, a);
-#pragma unroll
-                for (int c = 0; c < CPL; ++c)
-                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c], acc[r][c], 0, 0, 0);
-            }
-            if (s + PF < spw) issue(u, step0 + s + PF);
+            compute(u);
+            issue(u, step0 + s0 + PF + u);
         }
     }
+    const int rest = spw - s0 - PF;   // steps not yet issued (< PF; negative if spw < PF)
+#pragma unroll
+    for (int u = 0; u < PF; ++u) {
+        if (s0 + u >= spw) break;
+        compute(u);
+        if (u < rest) issue(u, step0 + s0 + PF + u);
+    }
+#pragma unroll
+    for (int u = 0; u < PF - 1; ++u)
+        if (u < rest) compute(u);
 
     // ------------------------------------------------ reduce the W waves' K ranges
 #pragma unroll
@@ -350,16 +405,22 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     if constexpr (FMT != FMT_AWQ) {
         if (p.g_idx) {
-            // static reduction buffer plus the group table may exceed the default 64 KiB
-            static const hipError_t attr = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&skinny_kernel<FMT, BM, CPL, PF, true, XCD>),
-                hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
-            if (attr != hipSuccess) return attr;
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, true, XCD>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), s.lds, st, p);
-            return hipGetLastError();
+            // act-order waves with exactly one ring of steps run without a loop: the loop's
+            // ring copies raise the kernel to 186 VGPRs, two waves per SIMD instead of three
+            // (config 2 M=16: 14.3 -> 10.5 us)
+            auto go = [&](auto kern) -> hipError_t {
+                // static reduction buffer plus the group table may exceed the default 64 KiB
+                const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
+                if (attr != hipSuccess) return attr;
+                hipLaunchKernelGGL(kern, grid, dim3(64 * skinny_waves(FMT, BM, CPL)), s.lds, st, p);
+                return hipGetLastError();
+            };
+            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, true, XCD, PF>);
+            return go(&skinny_kernel<FMT, BM, CPL, PF, true, XCD, 0>);
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD, 0>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
     return hipGetLastError();
 }
 
