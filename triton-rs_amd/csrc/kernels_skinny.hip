@@ -420,6 +420,12 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
             return go(&skinny_kernel<FMT, BM, CPL, PF, true, XCD, 0>);
         }
     }
+    if constexpr (FMT != FMT_AWQ) {
+        if (s.steps_per_wave == PF) {   // as above: M=16, 4096 -> 6144 9.4 -> 8.6 us
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            return hipGetLastError();
+        }
+    }
     hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD, 0>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
     return hipGetLastError();
 }
