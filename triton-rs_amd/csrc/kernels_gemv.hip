@@ -492,10 +492,13 @@ constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
 // At M = 1, 8 packed rows per lane (128 columns x 512 k, half the splits) where the group
 // size allows: 4.84 -> 4.55 us for config 0 (GPTQ sym 4096 x 4096) and 9.67 -> 8.87 us for
 // GPTQ 4096 -> 14336 (graph replays); at M = 4 the deeper tile was slower (16.2 -> 17.0 us).
-constexpr int GQ_CW = 4, GQ_RL = 4, GQ_RL1 = 8, GQ_WAVES = 4, GQ_LPR = 32;
-constexpr int GQ_COLS = GQ_LPR * GQ_CW;
-constexpr int GQ_ROWS = (64 / GQ_LPR) * GQ_WAVES * GQ_RL * 8;
-constexpr int GQ_ROWS1 = (64 / GQ_LPR) * GQ_WAVES * GQ_RL1 * 8;
+// At M = 2..4, 16 lanes per row where N and K allow (64 columns x 512 k, half the splits
+// of the 128-column tile at the same workgroup count): M=4, 4096 -> 6144 9.1 -> 8.5 us; at
+// M = 1 the 128-column tile is faster (4.56 vs 4.64 us for config 0).
+constexpr int GQ_CW = 4, GQ_RL = 4, GQ_RL1 = 8, GQ_WAVES = 4, GQ_LPR = 32, GQ_LPRN = 16;
+constexpr int gq_cols(int lpr) { return lpr * GQ_CW; }
+constexpr int gq_rows(int lpr, int rl) { return (64 / lpr) * GQ_WAVES * rl * 8; }
+constexpr int GQ_ROWS1 = gq_rows(GQ_LPR, GQ_RL1);
 // AWQ, M = 2..8, matrix-core dot: CW = 2 words per lane (256 columns). Wide tile: R = 128
 // rows per wave, 8 waves (1024 rows per workgroup: a quarter of the split-K partials of the
 // narrow tile, which rereads M x N fp32 per split); narrow tile (R = 64, 4 waves, 256 rows)
@@ -525,9 +528,12 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
         s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
     } else if (M >= 1 && M <= GEMV_MAX_M) {
-        if (N % GQ_COLS || K % GQ_ROWS || G % (GQ_RL * 8) || K % G) return s;
+        if (G % (GQ_RL * 8) || K % G) return s;
+        s.gptq_narrow = M > 1 && N % gq_cols(GQ_LPRN) == 0 && K % gq_rows(GQ_LPRN, GQ_RL) == 0;
+        const int lpr = s.gptq_narrow ? GQ_LPRN : GQ_LPR, rows = gq_rows(lpr, GQ_RL);
+        if (N % gq_cols(lpr) || K % rows) return s;
         s.gptq_deep = M == 1 && K % GQ_ROWS1 == 0 && G % (GQ_RL1 * 8) == 0;
-        s.ok = true; s.col_tiles = N / GQ_COLS; s.splits = K / (s.gptq_deep ? GQ_ROWS1 : GQ_ROWS);
+        s.ok = true; s.col_tiles = N / gq_cols(lpr); s.splits = K / (s.gptq_deep ? GQ_ROWS1 : rows);
         s.threads = 64 * GQ_WAVES;
     } else {
         return s;
@@ -557,6 +563,15 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
                     hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
                 else
                     hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+                return;
+            }
+        }
+        if constexpr (M > 1) {
+            if (fmt != FMT_AWQ && s.gptq_narrow) {
+                if (fmt == FMT_GPTQ)
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
+                else
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
                 return;
             }
         }

@@ -34,6 +34,7 @@ struct GemvShape {
     bool mfma;              // AWQ matrix-core kernel (else VALU dot products)
     bool mfma_wide;         // its 8-wave, 1024-row tile (else 4 waves, 256 rows)
     bool gptq_deep;         // GPTQ at M = 1: 8 packed rows per lane (512 k per workgroup)
+    bool gptq_narrow;       // GPTQ at M >= 2: 64-column tile (16 lanes per packed row)
     bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     int col_tiles, splits, threads;
 };
