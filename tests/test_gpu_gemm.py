@@ -53,6 +53,17 @@ def test_gemv_small(torch_cuda, orc, fmt, M):
     assert_parity(y, _oracle(orc, p), what=f"gemv fmt={fmt} M={M}")
 
 
+@pytest.mark.parametrize("fmt", [GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N", [(2, 1024, 192), (4, 2048, 320), (3, 768, 256), (2, 256, 128)])
+def test_gemv_gptq_tile_widths(torch_cuda, orc, fmt, M, K, N):
+    """GPTQ decode at M = 2..4: the 64-column tile where N % 64 == 0 and K % 512 == 0 (N=192,
+    320 only fit it), the 128-column, 256-row tile otherwise (K=768, K=256)."""
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=1200 + 10 * fmt + M + K // 64)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, 128) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"gptq gemv fmt={fmt} M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("M", [5, 6, 7, 8])
 @pytest.mark.parametrize("K,N,G", [(1024, 512, 128), (2048, 768, 64), (512, 256, 256)])
 def test_gemv_awq_matrix_core(torch_cuda, orc, M, K, N, G):
