@@ -108,6 +108,57 @@ def test_gemv_deterministic_and_reusable(torch_cuda, orc):
     assert_parity(ys[0], _oracle(orc, p))
 
 
+@pytest.mark.parametrize("fmt,M", [(AWQ, 1), (GPTQ, 1), (SYM, 1), (GPTQ, 3), (SYM, 4),
+                                   (AWQ, 4), (AWQ, 8)])
+def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
+    """Split-K partials of magnitude >= 2^15 leave the fixed-point hand-off for its fp32
+    path (partial stored, split bit set, added in split order by the last arrival).
+
+    Exact arithmetic, so the output must equal the oracle bit for bit: x[m, k] is 16 * 2^-m
+    on the first half of K and -8 * 2^-m on the second, every scale is 0.5 and q and the
+    zero point are constant down each column, so every product, partial sum and output is
+    a small multiple of a power of two. Each split covers 512 rows (VALU kernels: partial
+    4096 c for row 0 in the first half, c = q - z, so >= 2^15 exactly when |c| >= 8; two such
+    splits per entry) or 1024 rows (AWQ matrix-core kernel at M >= 2: 8192 c, |c| >= 4):
+    entries of both kinds in every call."""
+    K, N = 2048, 2048
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=4242 + 10 * fmt + M)
+    g = np.random.default_rng(4243 + 10 * fmt + M)
+    col_q = g.integers(0, 16, size=N)
+    col_z = g.integers(0, 15, size=N)              # GPTQ zero = nibble + 1 stays <= 15
+    p.q = np.broadcast_to(col_q, (K, N)).astype(np.int32)
+    p.zq = np.broadcast_to(col_z, (K // 128, N)).astype(np.int32)
+    if fmt == AWQ:
+        p.qweight = synth.pack_along_n(p.q, awq=True)
+        p.qzeros = synth.pack_along_n(p.zq, awq=True)
+    else:
+        p.qweight = synth.pack_gptq_qweight(p.q)
+        p.qzeros = synth.pack_along_n(p.zq, awq=False) if fmt == GPTQ else None
+    p.scales = np.full((K // 128, N), 0.5, dtype=np.float16)
+    half = np.where(np.arange(K) < K // 2, 16.0, -8.0)
+    p.x = (half[None, :] * (2.0 ** -np.arange(M))[:, None]).astype(np.float16)
+    c = col_q - p.zero_int()[0]
+    assert np.any(np.abs(c) >= 8) and np.any(np.abs(c) < 4)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, 128) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    ref = _oracle(orc, p)
+    assert np.array_equal(y.astype(np.float64), ref.astype(np.float64)), \
+        f"max abs diff {np.max(np.abs(y.astype(np.float64) - ref))}"
+    # and again: the hand-off left its slots and masks at zero
+    assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [(SYM, 1, 16384, 256), (AWQ, 8, 1024, 8448), (AWQ, 8, 4096, 14336)])
+def test_gemv_split_k_counter_protocol(torch_cuda, orc, fmt, M, K, N):
+    """Shapes past the fixed-point hand-off's limits (32 splits; M * N > 65536 entries)
+    keep the per-tile counter protocol: parity and repeatability."""
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=555 + M)
+    assert pkg().plan(FMT_NAME[fmt], M, N, K, 128) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"gemv counter protocol fmt={fmt} M={M}")
+    assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
+
+
 # ------------------------------------------------------------------ MFMA (small batch / prefill)
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])

@@ -43,7 +43,8 @@ struct Workspace {
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
 
-constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES;  // room for SPLITK_MAX_TILES counters
+// room for SPLITK_MAX_TILES counters, then the fixed-point hand-off's slots and masks
+constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES + FIX_SLOT_BYTES;
 
 static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
     int dev = 0;
@@ -250,6 +251,10 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
                 return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K counter area");
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;
+            // every GEMV kernel takes the fixed-point hand-off where its limits allow
+            p.fixed = s.splits <= FIX_MAX_SPLITS && (size_t)M * N <= FIX_MAX_ENTRIES;
+            p.slots = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(p.counters) + SPLITK_FLAG_BYTES);
+            p.masks = reinterpret_cast<uint32_t*>(p.slots + FIX_MAX_ENTRIES);
         }
         hipError_t e = launch_gemv(fmt, p, s, st);
         if (e != hipSuccess) return hip_fail(e, "gemv launch");

@@ -155,6 +155,26 @@ gemv_awq_kernel(GemvParams p) {
 
     // ---- reduce over row blocks; write partial (or the output when there is one split)
     const int n0 = ct * C;
+    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+        constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
+        size_t off[E];
+        float v[E];
+        int n = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = (int)threadIdx.x + e * T;
+            if (i >= M * C) break;
+            const int m = i / C, cidx = i - m * C;
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
+            off[e] = (size_t)m * p.N + n0 + cidx;
+            v[e] = s;
+            n = e + 1;
+        }
+        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        return;
+    }
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float s = 0.f;
@@ -286,6 +306,26 @@ gemv_gptq_kernel(GemvParams p) {
     }
     __syncthreads();
 
+    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+        constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
+        size_t off[E];
+        float v[E];
+        int n = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = (int)threadIdx.x + e * T;
+            if (i >= M * C) break;
+            const int m = i / C, cidx = i - m * C;
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
+            off[e] = (size_t)m * p.N + n0 + cidx;
+            v[e] = s;
+            n = e + 1;
+        }
+        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        return;
+    }
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float s = 0.f;
@@ -468,6 +508,26 @@ gemv_awq_mfma_kernel(GemvParams p) {
 
     // ---- reduce over waves; write partial (or the output when there is one split)
     const int n0 = ct * C;
+    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+        constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
+        size_t off[E];
+        float v[E];
+        int n = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = (int)threadIdx.x + e * T;
+            if (i >= M * C) break;
+            const int m = i / C, cidx = i - m * C;
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) s += red[w][m][cidx];
+            off[e] = (size_t)m * p.N + n0 + cidx;
+            v[e] = s;
+            n = e + 1;
+        }
+        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        return;
+    }
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float sum = 0.f;
@@ -488,6 +548,10 @@ namespace {
 // AWQ: CW = 1 word per lane per row, 32 rows per lane, 4 waves -> 256 columns x 256 rows.
 constexpr int AWQ_CW = 1, AWQ_RL = 32, AWQ_WAVES = 4;
 constexpr int AWQ_ROWS = (64 / (32 / AWQ_CW)) * AWQ_WAVES * AWQ_RL;
+// At M = 1, 8 waves (512 rows, half the splits) where K allows: 8.51 -> 8.41 us at
+// K=4096, N=14336 with the fixed-point hand-off.
+constexpr int AWQ_WAVES_DEEP = 8;
+constexpr int AWQ_ROWS_DEEP = (64 / (32 / AWQ_CW)) * AWQ_WAVES_DEEP * AWQ_RL;
 // GPTQ: CW = 4 columns per lane, 4 packed rows per lane, LPR = 32 -> 128 columns x 256 k.
 // At M = 1, 8 packed rows per lane (128 columns x 512 k, half the splits) where the group
 // size allows: 4.84 -> 4.55 us for config 0 (GPTQ sym 4096 x 4096) and 9.67 -> 8.87 us for
@@ -526,7 +590,9 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
     } else if (M >= 1 && M <= GEMV_MAX_M && fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
-        s.ok = true; s.col_tiles = N / 256; s.splits = K / AWQ_ROWS; s.threads = 64 * AWQ_WAVES;
+        s.awq_deep = M == 1 && K % AWQ_ROWS_DEEP == 0;
+        s.ok = true; s.col_tiles = N / 256; s.splits = K / (s.awq_deep ? AWQ_ROWS_DEEP : AWQ_ROWS);
+        s.threads = 64 * (s.awq_deep ? AWQ_WAVES_DEEP : AWQ_WAVES);
     } else if (M >= 1 && M <= GEMV_MAX_M) {
         if (G % (GQ_RL * 8) || K % G) return s;
         s.gptq_narrow = M > 1 && N % gq_cols(GQ_LPRN) == 0 && K % gq_rows(GQ_LPRN, GQ_RL) == 0;
@@ -572,6 +638,12 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
                     hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
                 else
                     hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
+                return;
+            }
+        }
+        if constexpr (M == 1) {
+            if (fmt == FMT_AWQ && s.awq_deep) {
+                hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES_DEEP, XCD>), grid, block, 0, st, p);
                 return;
             }
         }

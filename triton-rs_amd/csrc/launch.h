@@ -17,6 +17,15 @@ constexpr int GEMV_MFMA_MAX_M = 8;   // AWQ with matrix-core dot products
 constexpr int FLAG_STRIDE = 64;
 constexpr size_t SPLITK_FLAG_BYTES = 2u << 20;
 constexpr size_t SPLITK_MAX_TILES = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
+// Fixed-point split-K hand-off (splitk.h, splitk_fixed_commit): after the counters, one
+// 64-bit slot word per output entry, then one 32-bit split mask per entry, all zero between
+// calls. Used when splits <= FIX_MAX_SPLITS and M * N <= FIX_MAX_ENTRIES: with more entries
+// the atomics cost more than the counter protocol's reload (AWQ M = 8, 4096 -> 14336, four
+// splits: 14.5 us with the counter, 15.3 us fixed-point; every measured shape with at most
+// 65536 entries was faster fixed-point).
+constexpr int FIX_MAX_SPLITS = 31;
+constexpr size_t FIX_MAX_ENTRIES = 65536;
+constexpr size_t FIX_SLOT_BYTES = FIX_MAX_ENTRIES * (sizeof(uint64_t) + sizeof(uint32_t));
 
 struct GemvParams {
     const half_t* x;          // [M, K] contiguous
@@ -26,7 +35,10 @@ struct GemvParams {
     half_t* out;              // [M, N]
     float* ws;                // split-K partials [splits, M, N]
     uint32_t* counters;       // one per column tile (FLAG_STRIDE apart), zero between calls
+    uint64_t* slots;          // fixed-point hand-off: one word per output entry, zero between calls
+    uint32_t* masks;          // its out-of-range split masks, one per output entry, zero between calls
     int M, N, K, G, zero_offset, splits, col_tiles;
+    int fixed;                // 1: fixed-point hand-off (splitk_fixed_commit), 0: counter per tile
 };
 
 struct GemvShape {
@@ -35,6 +47,7 @@ struct GemvShape {
     bool mfma_wide;         // its 8-wave, 1024-row tile (else 4 waves, 256 rows)
     bool gptq_deep;         // GPTQ at M = 1: 8 packed rows per lane (512 k per workgroup)
     bool gptq_narrow;       // GPTQ at M >= 2: 64-column tile (16 lanes per packed row)
+    bool awq_deep;          // AWQ VALU kernel at M = 1: 8 waves, 512 rows per workgroup
     bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     int col_tiles, splits, threads;
 };
