@@ -252,7 +252,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
             rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
             if (rc) return rc;
             // every GEMV kernel takes the fixed-point hand-off where its limits allow
-            p.fixed = s.splits <= FIX_MAX_SPLITS && (size_t)M * N <= FIX_MAX_ENTRIES;
+            p.fixed = s.splits <= FIX_MAX_SPLITS && M <= FIX_MAX_M && (size_t)M * N <= FIX_MAX_ENTRIES;
             p.slots = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(p.counters) + SPLITK_FLAG_BYTES);
             p.masks = reinterpret_cast<uint32_t*>(p.slots + FIX_MAX_ENTRIES);
         }

@@ -19,11 +19,13 @@ constexpr size_t SPLITK_FLAG_BYTES = 2u << 20;
 constexpr size_t SPLITK_MAX_TILES = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
 // Fixed-point split-K hand-off (splitk.h, splitk_fixed_commit): after the counters, one
 // 64-bit slot word per output entry, then one 32-bit split mask per entry, all zero between
-// calls. Used when splits <= FIX_MAX_SPLITS and M * N <= FIX_MAX_ENTRIES: with more entries
-// the atomics cost more than the counter protocol's reload (AWQ M = 8, 4096 -> 14336, four
-// splits: 14.5 us with the counter, 15.3 us fixed-point; every measured shape with at most
-// 65536 entries was faster fixed-point).
+// calls. Used when splits <= FIX_MAX_SPLITS, M <= FIX_MAX_M and M * N <= FIX_MAX_ENTRIES:
+// with more entries the atomics cost more than the counter protocol's reload (AWQ M = 8,
+// 4096 -> 14336, four splits: 14.5 us with the counter, 15.3 us fixed-point), and at M = 8
+// the fixed-point time varied with the weight data (14336 -> 4096: 15.3 to 18.2 us across
+// seeds, no partial near the fp32 path's range; the counter protocol 15.8 us for both).
 constexpr int FIX_MAX_SPLITS = 31;
+constexpr int FIX_MAX_M = 4;
 constexpr size_t FIX_MAX_ENTRIES = 65536;
 constexpr size_t FIX_SLOT_BYTES = FIX_MAX_ENTRIES * (sizeof(uint64_t) + sizeof(uint32_t));
 
