@@ -62,6 +62,7 @@ def make_weight_sets(torch, fmt, K, N, G, count, dev, seed):
                            generator=gen)
         sc = (torch.rand((K // G, N), device=dev, generator=gen) * 0.018 + 0.002).half()
         sets.append((qw, sc, qz))
+    torch.cuda.synchronize()   # generated on the default stream; the calls run on another
     return sets
 
 

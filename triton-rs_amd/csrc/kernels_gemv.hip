@@ -579,12 +579,13 @@ constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     GemvShape s{};
     // AWQ: matrix-core dot for M = 2..8 (M = 2: 10.3 vs 11.4 us, M = 4: 12.0 vs 14.5 us at
-    // K=4096, N=14336) and for M = 1 when K > N (14336 -> 4096: 9.87 -> 9.45 us; at
-    // 4096 -> 14336 the VALU kernel is as fast), VALU dot2 otherwise and for shapes the
-    // matrix-core tile rejects
+    // K=4096, N=14336), VALU dot2 at M = 1 (with the 512-row tile and the fixed-point
+    // hand-off: 14336 -> 4096 8.40 vs 8.65 us, 8192 -> 4096 6.25 vs 7.70 us, 4096 -> 14336
+    // 8.47 vs 9.20 us against the matrix-core kernel) and for shapes the matrix-core tile
+    // rejects
     const bool mfma_fits = N % AM_COLS == 0 && K % AM_ROWS == 0 && G % AM_R == 0 && K % G == 0;
     const bool wide_fits = mfma_fits && K % AMW_ROWS == 0 && G % AMW_R == 0;
-    if (fmt == FMT_AWQ && M >= 1 && M <= GEMV_MFMA_MAX_M && mfma_fits && (M > 1 || K > N)) {
+    if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
         s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
         s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
