@@ -148,7 +148,19 @@ def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
     assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
 
 
-@pytest.mark.parametrize("fmt,M,K,N", [(SYM, 1, 16384, 256), (AWQ, 8, 1024, 8448), (AWQ, 8, 4096, 14336)])
+@pytest.mark.parametrize("K,N", [(768, 512), (1280, 256), (6144, 1024), (4608, 768)])
+def test_gemv_awq_m1_tiles(torch_cuda, orc, K, N):
+    """AWQ at M = 1 always takes the VALU kernel: the 512-row tile where K % 512 == 0 (K > N
+    included: 12 and 9 splits), the 256-row tile otherwise (K=768, K=1280)."""
+    p = Problem(AWQ, M=1, K=K, N=N, G=128, seed=1300 + K // 128 + N)
+    assert pkg().plan("awq", 1, N, K, 128) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"awq gemv M=1 K={K} N={N}")
+    assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [(SYM, 1, 16384, 256), (AWQ, 1, 16384, 512),
+                                       (AWQ, 8, 1024, 8448), (AWQ, 8, 4096, 14336)])
 def test_gemv_split_k_counter_protocol(torch_cuda, orc, fmt, M, K, N):
     """Shapes past the fixed-point hand-off's limits (32 splits; M > 4; M * N > 65536 entries)
     keep the per-tile counter protocol: parity and repeatability."""
