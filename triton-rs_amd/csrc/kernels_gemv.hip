@@ -600,6 +600,11 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         const int lpr = s.gptq_narrow ? GQ_LPRN : GQ_LPR, rows = gq_rows(lpr, GQ_RL);
         if (N % gq_cols(lpr) || K % rows) return s;
         s.gptq_deep = M == 1 && K % GQ_ROWS1 == 0 && G % (GQ_RL1 * 8) == 0;
+        // With the fixed-point hand-off the 256-row tile wins where the 512-row one leaves
+        // fewer than 512 workgroups (4096 -> 6144: 5.13 -> 4.70 us, 4096 -> 4096: 4.06 ->
+        // 4.02 us) and loses above (4096 -> 14336, 896 workgroups: 8.45 -> 9.11 us).
+        if (s.gptq_deep && (N / gq_cols(lpr)) * (K / GQ_ROWS1) < 512 && K / rows <= FIX_MAX_SPLITS)
+            s.gptq_deep = false;
         s.ok = true; s.col_tiles = N / gq_cols(lpr); s.splits = K / (s.gptq_deep ? GQ_ROWS1 : rows);
         s.threads = 64 * GQ_WAVES;
     } else {
