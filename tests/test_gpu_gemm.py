@@ -120,8 +120,9 @@ def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
     a small multiple of a power of two. Each split covers 512 rows (VALU kernels: partial
     4096 c for row 0 in the first half, c = q - z, so >= 2^15 exactly when |c| >= 8; two such
     splits per entry) or 1024 rows (AWQ matrix-core kernel at M >= 2: 8192 c, |c| >= 4):
-    entries of both kinds in every call."""
-    K, N = 2048, 2048
+    entries of both kinds in every call. At M = 1, N = 16384 keeps the 512-row tiles (the
+    GEMVs take 256-row tiles for grids this K leaves small)."""
+    K, N = 2048, (16384 if M == 1 else 2048)
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=4242 + 10 * fmt + M)
     g = np.random.default_rng(4243 + 10 * fmt + M)
     col_q = g.integers(0, 16, size=N)
@@ -148,10 +149,12 @@ def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
     assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
 
 
-@pytest.mark.parametrize("K,N", [(768, 512), (1280, 256), (6144, 1024), (4608, 768)])
+@pytest.mark.parametrize("K,N", [(768, 512), (1280, 256), (6144, 1024), (4608, 768),
+                                 (4096, 4096), (8192, 1024)])
 def test_gemv_awq_m1_tiles(torch_cuda, orc, K, N):
-    """AWQ at M = 1 always takes the VALU kernel: the 512-row tile where K % 512 == 0 (K > N
-    included: 12 and 9 splits), the 256-row tile otherwise (K=768, K=1280)."""
+    """AWQ at M = 1 always takes the VALU kernel: the 256-row tile where K % 512 != 0
+    (K=768, 1280) or the 512-row tile would leave under 192 workgroups (6144 x 1024, 4608 x
+    768, 4096 x 4096), the 512-row tile otherwise (8192 x 1024 would need 32 splits)."""
     p = Problem(AWQ, M=1, K=K, N=N, G=128, seed=1300 + K // 128 + N)
     assert pkg().plan("awq", 1, N, K, 128) == "gemv"
     y = _run_gemm(torch_cuda, p)

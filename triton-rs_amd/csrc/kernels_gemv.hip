@@ -592,6 +592,11 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     } else if (M >= 1 && M <= GEMV_MAX_M && fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
         s.awq_deep = M == 1 && K % AWQ_ROWS_DEEP == 0;
+        // the 256-row tile where the 512-row one leaves fewer than 192 workgroups (4096 ->
+        // 4096, 128 workgroups: 5.02 -> 4.33 us; 2048 -> 4096: 4.73 -> 3.74 us), the 512-row
+        // tile from 192 up (4096 -> 6144: 5.44 vs 5.57 us; 4096 -> 8192: 6.01 vs 6.07 us)
+        if (s.awq_deep && (N / 256) * (K / AWQ_ROWS_DEEP) < 192 && K / AWQ_ROWS <= FIX_MAX_SPLITS)
+            s.awq_deep = false;
         s.ok = true; s.col_tiles = N / 256; s.splits = K / (s.awq_deep ? AWQ_ROWS_DEEP : AWQ_ROWS);
         s.threads = 64 * (s.awq_deep ? AWQ_WAVES_DEEP : AWQ_WAVES);
     } else if (M >= 1 && M <= GEMV_MAX_M) {
