@@ -69,6 +69,13 @@ typedef enum {
 W4A16_API const char* w4a16_last_error(void);
 W4A16_API const char* w4a16_version(void);
 
+/* Optional set-up for `device` (it is current again on return): caches the device's CU
+ * count and runs the workgroup-placement probe the decode kernels' L2-local split-K hand-off
+ * depends on. Without it both happen on the first call; a first call made while its stream
+ * is being captured into a HIP graph cannot probe (probing synchronises) and uses the
+ * device-scope hand-off instead. No reference counterpart. */
+W4A16_API int w4a16_init(int32_t device);
+
 /* ------------------------------------------------------------------ op level */
 
 /* out[M, N] = x[M, K] @ W16[K, N], W16 = RNE_f16((q - z) * scale[g, n]) with
@@ -77,9 +84,13 @@ W4A16_API const char* w4a16_version(void);
  * (int32 [K], values in [0, K/group_size); values outside are clamped into it) is optional
  * and, in the reference, absent: it adds GPTQ act-order. Requirements: M, N, K, group_size >= 1; K % group_size == 0;
  * N % 8 == 0; K % 8 == 0 for GPTQ formats. The kernel is chosen by shape (see
- * w4a16_gemm_plan). The decode kernels use a per-(device, stream) split-K workspace
- * that the library allocates on first use of a size and keeps; concurrent calls on
- * different streams are safe. */
+ * w4a16_gemm_plan). The split-K kernels use a per-(device, stream) workspace that the
+ * library allocates on first use of a size; a larger size later allocates a new one and
+ * retires the old one without freeing it (HIP graphs captured earlier keep using it), so a
+ * captured call stays valid for the life of the process. Growing the workspace is not
+ * possible under stream capture: make one call of the largest size before capturing, or
+ * the call fails with W4A16_ERR_UNSUPPORTED. Concurrent calls on different streams are
+ * safe. */
 W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
                          const void* scales, const void* qzeros, const int32_t* g_idx,
                          void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
@@ -93,6 +104,15 @@ W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t 
  * The reference kernels' exact parameter lists (a_ptr, qweight_ptr, scales_ptr, qzeros_ptr,
  * c_ptr, m, n, k, group_size, 10 strides), prefixed by the stream. Any strides (in
  * elements of the tensor's own type), any M/N/K; masked tails read as zero. */
+
+/* Dense row-major operands (stride_ak = stride_qwn = stride_sn = stride_qzn = stride_cn = 1,
+ * stride_am = k, stride_qwk = n (GPTQ) or n / 8 (AWQ), stride_sk = n, stride_qzk = n / 8,
+ * stride_cm = n; 16-byte aligned pointers; k % group_size == 0, n % 8 == 0) go to the
+ * kernels w4a16_gemm plans; other layouts run the generic strided kernel.
+ * w4a16_typed_plan reports which, without touching the GPU (aligned16: whether every
+ * pointer will be 16-byte aligned). */
+W4A16_API int w4a16_typed_plan(int fmt, int32_t m, int32_t n, int32_t k, int32_t group_size,
+                               const int32_t* strides10, int aligned16, int* kernel);
 
 /* replaces w4a16_gptq_gemm_typed (w4a16_gptq_gemm_typed.rs:103-129), zero = nibble + 1 */
 W4A16_API int w4a16_gptq_gemm_typed(void* stream, const void* a_ptr, const void* qweight_ptr,
@@ -146,28 +166,33 @@ W4A16_API int w4a16_moe_route(void* stream, const float* logits, int32_t T, int3
 /* Sort pairs by expert (stable in p), padding each expert to a multiple of block_m with the
  * sentinel num_pairs. sorted_ids int32 [capacity], expert_ids int32 [capacity / block_m],
  * *num_tokens_post_padded = padded length (device). capacity must be a multiple of block_m
- * and >= num_pairs + E * (block_m - 1). */
+ * and >= num_pairs + E * (block_m - 1). topk_ids are read on the device: a pair whose id is
+ * outside [0, E) is dropped (it appears in no block, so a grouped GEMM leaves its output row
+ * unwritten). */
 W4A16_API int w4a16_moe_align(void* stream, const int32_t* topk_ids, int32_t num_pairs, int32_t E,
                               int32_t block_m, int32_t capacity, int32_t* sorted_ids,
                               int32_t* expert_ids, int32_t* num_tokens_post_padded);
 
 /* Grouped W4A16 GEMM over expert-sorted blocks: for every block of block_m sorted pairs with
  * expert e, out[p, :] = a[p / a_div, :] @ W16_e, W16_e from the e-th slice of the stacked
- * qweight / scales / qzeros (expert strides in elements). out is [num_pairs, N]; padding rows
- * are skipped. N % 256 == 0, K % 64 == 0, block_m in {64, 128}. */
+ * qweight / scales / qzeros (expert strides in elements; num_experts slices). out is
+ * [num_pairs, N]; padding rows are skipped. N % 256 == 0, K % 64 == 0, block_m in {64, 128}.
+ * The routing tables are read on the device: a block whose expert id is outside
+ * [0, num_experts) is skipped, and a sorted id outside [0, num_pairs) is padding. */
 W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div,
                              const void* qweight, const void* scales, const void* qzeros,
                              int64_t qweight_expert_stride, int64_t scales_expert_stride,
-                             int64_t qzeros_expert_stride, const int32_t* sorted_ids,
+                             int64_t qzeros_expert_stride, int32_t num_experts,
+                             const int32_t* sorted_ids,
                              const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
                              void* out, int32_t num_pairs, int32_t N, int32_t K,
                              int32_t group_size, int32_t block_m, int32_t capacity,
                              int32_t gptq_zero_offset);
 
 /* replaces fused_silu_mul_interleaved_f16 (crates/triton-kernels/src/elementwise.rs:188-212):
- * out[b * inter + i] = f16(silu(g) * u), g = gate_up[b * 2 * inter + i],
- * u = gate_up[b * 2 * inter + inter + i], silu(g) = g / (1 + exp(-g)) in f32.
- * total = batch * inter; inter % 8 == 0. */
+ * out[idx] = f16(silu(g) * u) for idx < total, b = idx / inter, i = idx % inter,
+ * g = gate_up[b * 2 * inter + i], u = gate_up[b * 2 * inter + inter + i],
+ * silu(g) = g / (1 + exp(-g)) in f32. Any inter >= 1 and total >= 0 (normally batch * inter). */
 W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, void* out,
                                              int32_t inter, int32_t total);
 

@@ -181,15 +181,54 @@ def test_moe_argument_errors():
     assert L.w4a16_moe_align(None, v, 1024, 8, 64, 1024, v, v, v) == P.ERR_INVALID_ARG
     assert "capacity" in L.w4a16_last_error().decode()
     # grouped GEMM shape limits
-    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, v, v, v, v, 1024, 1004, 4096, 128, 64,
-                          1536, 1)
+    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, 8, v, v, v, v, 1024, 1004, 4096, 128,
+                          64, 1536, 1)
     assert rc == P.ERR_INVALID_ARG        # N % 8
-    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, v, v, v, v, 1024, 1032, 4096, 128, 64,
-                          1536, 1)
+    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, 8, v, v, v, v, 1024, 1032, 4096, 128,
+                          64, 1536, 1)
     assert rc == P.ERR_UNSUPPORTED        # N % 256
-    assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, 250) == P.ERR_INVALID_ARG
+    rc = L.w4a16_moe_gemm(None, 0, v, 2, v, v, v, 0, 0, 0, 0, v, v, v, v, 1024, 1024, 4096, 128,
+                          64, 1536, 1)
+    assert rc == P.ERR_INVALID_ARG        # num_experts < 1
+    assert L.fused_silu_mul_interleaved_f16(None, v, v, 0, 250) == P.ERR_INVALID_ARG
+    assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, -1) == P.ERR_INVALID_ARG
+    # any inter and a total that is not a multiple of it are the reference's domain
+    assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, 0) == P.OK
     assert L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64) > 512 * 2 * 14336 * 2
     ws = L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64)
     rc = L.w4a16_fused_moe(None, 0, v, v, 512, 4096, 14336, 8, 2, 1, v, v, v, v, v, v, 128, 64, 1,
                            v, ws - 1, v)
     assert rc == P.ERR_INVALID_ARG and "workspace" in L.w4a16_last_error().decode()
+
+
+def _dense_strides(fmt, m, n, k):
+    return [k, 1, n // 8 if fmt == "awq" else n, 1, n, 1, n // 8, 1, n, 1]
+
+
+@pytest.mark.parametrize("fmt,m,n,k,expect", [
+    ("awq", 1, 14336, 4096, "gemv"), ("awq", 4, 4096, 14336, "gemv"),
+    ("gptq", 16, 6144, 4096, "skinny"), ("awq", 2048, 14336, 4096, "prefill"),
+    ("gptq", 1, 4096, 4096, "gemv"),
+])
+def test_typed_entry_points_route_dense_layouts_to_the_planner(fmt, m, n, k, expect):
+    """The reference-named typed entry points take w4a16_gemm's kernels for dense row-major
+    operands, and the generic strided kernel otherwise."""
+    P = pkg()
+    st = _dense_strides(fmt, m, n, k)
+    assert P.typed_plan(fmt, m, n, k, 128, st) == expect == P.plan(fmt, m, n, k, 128)
+    assert P.typed_plan(fmt, m, n, k, 128, st, aligned16=False) == "strided"
+    for i, bad in ((0, k + 8), (1, 2), (2, st[2] + 1), (5, 2), (6, st[6] + 3), (8, n + 8)):
+        if i in (0, 8) and m == 1:
+            continue                    # a single row's stride is never used
+        s2 = list(st)
+        s2[i] = bad
+        assert P.typed_plan(fmt, m, n, k, 128, s2) == "strided", (i, bad)
+    assert P.typed_plan(fmt, m, n, k + 64, 128, _dense_strides(fmt, m, n, k + 64)) == "strided"
+
+
+def test_init_without_device_reports_backend_disabled():
+    import torch
+    P = pkg()
+    if torch.cuda.is_available():
+        pytest.skip("a device is present")
+    assert P.lib().w4a16_init(0) == P.ERR_BACKEND_DISABLED

@@ -67,7 +67,8 @@ _ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, Module
                                InvalidLaunchConfig, BackendDisabled, NotFound)}
 
 EXPORTED = (
-    "w4a16_last_error", "w4a16_version", "w4a16_gemm", "w4a16_gemm_plan",
+    "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_plan",
+    "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
     "w4a16_moe_gemm", "fused_silu_mul_interleaved_f16", "w4a16_moe_sum",
@@ -95,6 +96,9 @@ def lib() -> ctypes.CDLL:
         L.w4a16_version.restype = ctypes.c_char_p
         L.w4a16_gemm.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_plan.argtypes = [_I, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]
+        L.w4a16_init.argtypes = [_I]
+        L.w4a16_typed_plan.argtypes = [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I,
+                                       ctypes.POINTER(ctypes.c_int)]
         L.w4a16_gptq_gemm_typed.argtypes = [_P] * 6 + [_I] * 14
         L.awq_gemm_int4_typed.argtypes = [_P] * 6 + [_I] * 14
         L.dequant_int4_to_fp16.argtypes = [_P] * 5 + [_I] * 4
@@ -103,7 +107,7 @@ def lib() -> ctypes.CDLL:
         L.w4a16_moe_route.argtypes = [_P, _P, _I, _I, _I, _I, _P, _P]
         L.w4a16_moe_align.argtypes = [_P, _P, _I, _I, _I, _I, _P, _P, _P]
         _L = ctypes.c_int64
-        L.w4a16_moe_gemm.argtypes = [_P, _I, _P, _I, _P, _P, _P, _L, _L, _L, _P, _P, _P, _P,
+        L.w4a16_moe_gemm.argtypes = [_P, _I, _P, _I, _P, _P, _P, _L, _L, _L, _I, _P, _P, _P, _P,
                                      _I, _I, _I, _I, _I, _I, _I]
         L.fused_silu_mul_interleaved_f16.argtypes = [_P, _P, _P, _I, _I]
         L.w4a16_moe_sum.argtypes = [_P, _P, _P, _P, _I, _I, _I]
@@ -177,6 +181,20 @@ _HALF = (torch.float16,)
 
 
 # ------------------------------------------------------------------ op level
+
+def init(device: int = 0) -> None:
+    """Optional per-device set-up (CU count, workgroup-placement probe) ahead of graph capture."""
+    check(lib().w4a16_init(device))
+
+
+def typed_plan(fmt, m: int, n: int, k: int, group_size: int, strides, aligned16: bool = True) -> str:
+    """Kernel regime the reference-named typed entry points would run for these strides."""
+    k_ = ctypes.c_int(0)
+    arr = (ctypes.c_int32 * 10)(*strides)
+    check(lib().w4a16_typed_plan(_fmt(fmt), m, n, k, group_size, arr, int(aligned16),
+                                 ctypes.byref(k_)))
+    return KERNELS[k_.value]
+
 
 def plan(fmt, M: int, N: int, K: int, group_size: int, has_g_idx: bool = False) -> str:
     """Name of the kernel regime w4a16_gemm would choose (no GPU access)."""
@@ -280,7 +298,8 @@ def moe_gemm(a, a_div, qweight, scales, qzeros, sorted_ids, expert_ids, npp, num
     ss = scales[0].numel()
     zs = 0 if qzeros is None else qzeros[0].numel()
     check(lib().w4a16_moe_gemm(_stream(a), f, _ptr(a), a_div, _ptr(qweight), _ptr(scales),
-                               _ptr(qzeros), qs, ss, zs, _ptr(sorted_ids), _ptr(expert_ids),
+                               _ptr(qzeros), qs, ss, zs, qweight.shape[0], _ptr(sorted_ids),
+                               _ptr(expert_ids),
                                _ptr(npp), _ptr(out), num_pairs, N, K, group_size, block_m,
                                sorted_ids.numel(), zero_offset))
     return out

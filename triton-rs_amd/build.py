@@ -48,7 +48,8 @@ def _run(cmd):
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    lang = ["-x", "hip", f"--offload-arch={ARCH}"] if src.endswith(".hip") else []
+    # .cpp sources are host code only (no device pass for a default target)
+    lang = ["-x", "hip", f"--offload-arch={ARCH}"] if src.endswith(".hip") else ["--cuda-host-only"]
     _run([HIPCC, *lang, *COMMON, "-c", os.path.join(CSRC, src), "-o", obj])
     return obj
 

@@ -8,6 +8,7 @@
 #include <mutex>
 #include <string>
 #include <utility>
+#include <vector>
 
 #include "../../include/w4a16.h"
 #include "launch.h"
@@ -35,16 +36,28 @@ static inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) 
 // ------------------------------------------------------------------ workspace
 
 // One split-K workspace per (device, stream): per-tile counters (zeroed at allocation,
-// returned to zero by the kernels themselves) followed by fp32 partials.
+// returned to zero by the kernels themselves) followed by fp32 partials. A workspace is
+// never freed: HIP graphs captured on the stream keep its address in their kernel nodes,
+// so when a larger request arrives a new buffer takes its place and the old one is retired
+// (kept allocated until the process ends). Growth allocates memory, which graph capture
+// forbids; under capture a call that would need a larger workspace fails with an error
+// asking for one call of that size outside capture first.
 struct Workspace {
     void* base = nullptr;
     size_t bytes = 0;
 };
 static std::mutex g_ws_mu;
 static std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+static std::vector<void*> g_ws_retired;   // superseded workspaces, alive until exit
 
 // room for SPLITK_MAX_TILES counters, then the fixed-point hand-off's slots and masks
 constexpr size_t COUNTER_BYTES = SPLITK_FLAG_BYTES + FIX_SLOT_BYTES;
+
+static bool stream_capturing(hipStream_t st) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess) { (void)hipGetLastError(); return false; }
+    return cs != hipStreamCaptureStatusNone;
+}
 
 static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
     int dev = 0;
@@ -54,19 +67,19 @@ static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float
     Workspace& w = g_ws[{dev, st}];
     const size_t total = COUNTER_BYTES + need;
     if (w.bytes < total) {
-        if (w.base) {
-            // the old buffer may still be read by queued work on this stream
-            e = hipStreamSynchronize(st);
-            if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
-            (void)hipFree(w.base);
-            w.base = nullptr;
-            w.bytes = 0;
-        }
-        size_t grow = total < (size_t)(8 << 20) ? (size_t)(8 << 20) : total;
-        e = hipMalloc(&w.base, grow);
+        if (stream_capturing(st))
+            return fail(W4A16_ERR_UNSUPPORTED,
+                        "split-K workspace of %zu bytes needed while the stream is being captured: "
+                        "make one call of this size on the stream before capturing", total);
+        const size_t grow = total < (size_t)(8 << 20) ? (size_t)(8 << 20) : total;
+        void* fresh = nullptr;
+        e = hipMalloc(&fresh, grow);
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-        e = hipMemset(w.base, 0, COUNTER_BYTES);
-        if (e != hipSuccess) return hip_fail(e, "hipMemset(workspace counters)");
+        // ordered after everything queued on the stream, before this call's kernels
+        e = hipMemsetAsync(fresh, 0, COUNTER_BYTES, st);
+        if (e != hipSuccess) { (void)hipFree(fresh); return hip_fail(e, "hipMemsetAsync(workspace counters)"); }
+        if (w.base) g_ws_retired.push_back(w.base);
+        w.base = fresh;
         w.bytes = grow;
     }
     *counters = static_cast<uint32_t*>(w.base);
@@ -128,10 +141,13 @@ static int device_cus() {
 }
 
 // Whether workgroup b of a launch runs on XCD b mod 8 on the current device (the GEMV's
-// L2-local split-K hand-off relies on it). Probed once per device with a small kernel;
-// false when the probe fails or placement differs, and the kernels then use the
-// device-scope hand-off.
-static bool xcd_placement() {
+// L2-local split-K hand-off relies on it). Probed once per device with a small synchronous
+// kernel; false when the probe fails or placement differs, and the kernels then use the
+// device-scope hand-off. The probe allocates and synchronises, which graph capture forbids:
+// a call made while its stream is being captured, before the device was probed, takes the
+// device-scope variant (correct everywhere) and leaves the probe for a later call.
+// w4a16_init() runs the probe up front.
+static bool xcd_placement(hipStream_t st, bool probe = true) {
     static std::mutex mu;
     static std::map<int, bool> cache;
     int dev = 0;
@@ -139,10 +155,16 @@ static bool xcd_placement() {
     std::lock_guard<std::mutex> lk(mu);
     auto it = cache.find(dev);
     if (it != cache.end()) return it->second;
+    if (!probe || stream_capturing(st)) return false;
     bool ok = false;
     if (check_xcd_placement(&ok) != hipSuccess) { (void)hipGetLastError(); ok = false; }
     cache[dev] = ok;
     return ok;
+}
+
+// The placement result if this device has been probed, else false (no probe).
+static bool xcd_placement_cached() {
+    return xcd_placement(nullptr, /*probe=*/false);
 }
 
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
@@ -168,7 +190,26 @@ extern "C" {
 
 W4A16_API const char* w4a16_last_error(void) { return g_last_error.c_str(); }
 
-W4A16_API const char* w4a16_version(void) { return "w4a16-mi355x 0.1 (gfx950)"; }
+W4A16_API const char* w4a16_version(void) { return "w4a16-mi355x 0.2 (gfx950)"; }
+
+W4A16_API int w4a16_init(int32_t device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n < 1) {
+        (void)hipGetLastError();
+        return fail(W4A16_ERR_BACKEND_DISABLED, "no HIP device available");
+    }
+    if (device < 0 || device >= n)
+        return fail(W4A16_ERR_INVALID_ARG, "device %d outside [0, %d)", device, n);
+    int prev = 0;
+    e = hipGetDevice(&prev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (prev != device && (e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    (void)device_cus();
+    (void)xcd_placement(nullptr);
+    if (prev != device && (e = hipSetDevice(prev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    return W4A16_OK;
+}
 
 W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t G, int has_g_idx,
                               int* kernel) {
@@ -179,9 +220,27 @@ W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t 
     return W4A16_OK;
 }
 
-W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
-                         const void* scales, const void* qzeros, const int32_t* g_idx, void* out,
-                         int32_t M, int32_t N, int32_t K, int32_t G, int32_t zero_offset) {
+}  // extern "C"
+
+namespace w4a16 {
+
+// Scratch of the per-stream allocated workspace (get_workspace), sized on demand.
+static int alloc_scratch(hipStream_t st, size_t partial_bytes, Scratch* out) {
+    uint32_t* counters = nullptr;
+    float* partials = nullptr;
+    if (int rc = get_workspace(st, partial_bytes, &counters, &partials)) return rc;
+    out->counters = counters;
+    out->slots = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(counters) + SPLITK_FLAG_BYTES);
+    out->masks = reinterpret_cast<uint32_t*>(out->slots + FIX_MAX_ENTRIES);
+    out->partials = partials;
+    return W4A16_OK;
+}
+
+ScratchSource alloc_scratch_source() { return ScratchSource{SIZE_MAX, SPLITK_MAX_TILES, true, alloc_scratch}; }
+
+int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const void* scales,
+              const void* qzeros, const int32_t* g_idx, void* out, int32_t M, int32_t N,
+              int32_t K, int32_t G, int32_t zero_offset, const ScratchSource& src) {
     int rc = check_gemm_args(fmt, x, qweight, scales, qzeros, out, M, N, K, G);
     if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
@@ -192,9 +251,21 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     const int cus = device_cus();
     int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
+    // the placement probe allocates: sources that must not allocate use what is cached
+    const bool xcd = src.may_probe ? xcd_placement(st) : xcd_placement_cached();
+    auto scratch_for = [&](size_t tiles, size_t partial_bytes, Scratch* sc) -> int {
+        if (tiles > src.max_tiles)
+            return fail(W4A16_ERR_UNSUPPORTED, "%zu split-K tiles exceed the counter area (%zu)",
+                        tiles, src.max_tiles);
+        if (partial_bytes > src.max_partial_bytes)
+            return fail(W4A16_ERR_UNSUPPORTED,
+                        "split-K partials of %zu bytes exceed the scratch limit of %zu bytes "
+                        "(M=%d N=%d K=%d)", partial_bytes, src.max_partial_bytes, M, N, K);
+        return src.get(st, partial_bytes, sc);
+    };
 
     if (kernel == W4A16_KERNEL_SKINNY) {
-        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd_placement());
+        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd);
         SkinnyParams p{};
         p.g_idx = g_idx;
         p.x = static_cast<const half_t*>(x);
@@ -205,10 +276,11 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.splits = s.splits; p.steps_per_wave = s.steps_per_wave; p.col_tiles = s.col_tiles;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles > SPLITK_MAX_TILES)
-                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
-            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.flags, &p.ws);
+            Scratch sc{};
+            rc = scratch_for((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float), &sc);
             if (rc) return rc;
+            p.flags = sc.counters;
+            p.ws = sc.partials;
         }
         hipError_t e = launch_skinny(fmt, p, s, st);
         if (e != hipSuccess) return hip_fail(e, "skinny launch");
@@ -216,7 +288,10 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     }
 
     if (kernel == W4A16_KERNEL_PREFILL) {
-        const PrefillShape s = prefill_shape(fmt, M, N, K, G, cus);
+        PrefillShape s = prefill_shape(fmt, M, N, K, G, cus);
+        if (s.ksplit > 1 && ((size_t)s.ksplit * M * N * sizeof(float) > src.max_partial_bytes ||
+                             (size_t)s.col_tiles * s.row_tiles > src.max_tiles))
+            s = prefill_shape(fmt, M, N, K, G, cus, 1);   // no K split: no scratch at all
         PrefillParams p{};
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
@@ -226,10 +301,12 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.ksplit = s.ksplit;
         if (s.ksplit > 1) {
-            if ((size_t)s.col_tiles * s.row_tiles > SPLITK_MAX_TILES)
-                return fail(W4A16_ERR_UNSUPPORTED, "too many tiles for the split-K counter area");
-            rc = get_workspace(st, (size_t)s.ksplit * M * N * sizeof(float), &p.counters, &p.ws);
+            Scratch sc{};
+            rc = scratch_for((size_t)s.col_tiles * s.row_tiles,
+                             (size_t)s.ksplit * M * N * sizeof(float), &sc);
             if (rc) return rc;
+            p.counters = sc.counters;
+            p.ws = sc.partials;
         }
         hipError_t e = launch_prefill(fmt, p, s, st);
         if (e != hipSuccess) return hip_fail(e, "prefill launch");
@@ -237,7 +314,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     }
 
     if (kernel == W4A16_KERNEL_GEMV) {
-        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd_placement());
+        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd);
         GemvParams p{};
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
@@ -247,14 +324,15 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset; p.splits = s.splits;
         p.col_tiles = s.col_tiles;
         if (s.splits > 1) {
-            if ((size_t)s.col_tiles > SPLITK_MAX_TILES)
-                return fail(W4A16_ERR_UNSUPPORTED, "N too large for the split-K counter area");
-            rc = get_workspace(st, (size_t)s.splits * M * N * sizeof(float), &p.counters, &p.ws);
+            Scratch sc{};
+            rc = scratch_for((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float), &sc);
             if (rc) return rc;
+            p.counters = sc.counters;
+            p.ws = sc.partials;
             // every GEMV kernel takes the fixed-point hand-off where its limits allow
             p.fixed = s.splits <= FIX_MAX_SPLITS && M <= FIX_MAX_M && (size_t)M * N <= FIX_MAX_ENTRIES;
-            p.slots = reinterpret_cast<uint64_t*>(reinterpret_cast<char*>(p.counters) + SPLITK_FLAG_BYTES);
-            p.masks = reinterpret_cast<uint32_t*>(p.slots + FIX_MAX_ENTRIES);
+            p.slots = sc.slots;
+            p.masks = sc.masks;
         }
         hipError_t e = launch_gemv(fmt, p, s, st);
         if (e != hipSuccess) return hip_fail(e, "gemv launch");
@@ -280,6 +358,38 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
     return W4A16_OK;
 }
 
+}  // namespace w4a16
+
+extern "C" {
+
+W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
+                         const void* scales, const void* qzeros, const int32_t* g_idx, void* out,
+                         int32_t M, int32_t N, int32_t K, int32_t G, int32_t zero_offset) {
+    return gemm_impl(stream, fmt, x, qweight, scales, qzeros, g_idx, out, M, N, K, G, zero_offset,
+                     alloc_scratch_source());
+}
+
+// The reference kernels' parameter lists with arbitrary strides. A call whose tensors are
+// the dense row-major layouts of the checkpoint formats (the usual case: a linear layer's
+// weights and activations) is the same problem w4a16_gemm solves, and goes through its
+// planner to the GEMV / small-batch / prefill kernels; anything else (transposed or padded
+// operands, shapes those kernels reject) runs the generic strided kernel. Both give the
+// reference's result: W16 = RNE_f16((q - z) s) with z = nibble + 1 (GPTQ) or the nibble
+// (AWQ), fp32 accumulation, fp16 output.
+static bool typed_dense(int fmt, const void* a, const void* qw, const void* sc, const void* qz,
+                        const void* c, int32_t m, int32_t n, int32_t k, int32_t G,
+                        const int32_t* st) {
+    if (n % 8 || k % G || (fmt == W4A16_FMT_GPTQ && k % 8)) return false;
+    const int32_t qw_k = fmt == W4A16_FMT_AWQ ? n / 8 : n;
+    const bool rows_ok = (st[0] == k || m == 1) && st[1] == 1 &&      // a [m, k]
+                         st[2] == qw_k && st[3] == 1 &&                // qweight
+                         st[4] == n && st[5] == 1 &&                   // scales [k/G, n]
+                         st[6] == n / 8 && st[7] == 1 &&               // qzeros [k/G, n/8]
+                         (st[8] == n || m == 1) && st[9] == 1;         // c [m, n]
+    return rows_ok && aligned(a, 16) && aligned(qw, 16) && aligned(sc, 16) && aligned(qz, 16) &&
+           aligned(c, 16);
+}
+
 static int typed_common(int fmt, void* stream, const void* a, const void* qw, const void* sc,
                         const void* qz, void* c, int32_t m, int32_t n, int32_t k, int32_t G,
                         const int32_t* strides) {
@@ -288,6 +398,9 @@ static int typed_common(int fmt, void* stream, const void* a, const void* qw, co
     if (m < 0 || n < 0 || k < 0 || G < 1)
         return fail(W4A16_ERR_INVALID_ARG, "negative size or group_size < 1");
     if (m == 0 || n == 0) return W4A16_OK;
+    if (k > 0 && typed_dense(fmt, a, qw, sc, qz, c, m, n, k, G, strides))
+        return w4a16_gemm(stream, fmt, a, qw, sc, qz, nullptr, c, m, n, k, G,
+                          fmt == W4A16_FMT_GPTQ ? 1 : 0);
     StridedParams p{};
     p.a = static_cast<const half_t*>(a);
     p.qweight = static_cast<const uint32_t*>(qw);
@@ -304,6 +417,20 @@ static int typed_common(int fmt, void* stream, const void* a, const void* qw, co
     p.zero_offset = (fmt == W4A16_FMT_GPTQ) ? 1 : 0;
     hipError_t e = launch_strided_gemm(fmt, p, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "typed gemm launch");
+    return W4A16_OK;
+}
+
+W4A16_API int w4a16_typed_plan(int fmt, int32_t m, int32_t n, int32_t k, int32_t group_size,
+                               const int32_t* strides, int aligned16, int* kernel) {
+    if (fmt != W4A16_FMT_GPTQ && fmt != W4A16_FMT_AWQ)
+        return fail(W4A16_ERR_INVALID_ARG, "typed entry points take GPTQ or AWQ (fmt %d)", fmt);
+    if (!strides || !kernel) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (m < 1 || n < 1 || k < 1 || group_size < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "sizes must be positive");
+    const void* p = aligned16 ? (const void*)(uintptr_t)256 : (const void*)(uintptr_t)2;
+    *kernel = typed_dense(fmt, p, p, p, p, p, m, n, k, group_size, strides)
+                  ? plan(fmt, m, n, k, group_size, false)
+                  : W4A16_KERNEL_STRIDED;
     return W4A16_OK;
 }
 
@@ -423,7 +550,8 @@ W4A16_API int w4a16_moe_align(void* stream, const int32_t* topk_ids, int32_t num
 W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div,
                              const void* qweight, const void* scales, const void* qzeros,
                              int64_t qweight_expert_stride, int64_t scales_expert_stride,
-                             int64_t qzeros_expert_stride, const int32_t* sorted_ids,
+                             int64_t qzeros_expert_stride, int32_t num_experts,
+                             const int32_t* sorted_ids,
                              const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
                              void* out, int32_t num_pairs, int32_t N, int32_t K, int32_t G,
                              int32_t block_m, int32_t capacity, int32_t zero_offset) {
@@ -432,7 +560,8 @@ W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div
     if (rc) return rc;
     if (!sorted_ids || !expert_ids || !num_tokens_post_padded)
         return fail(W4A16_ERR_INVALID_ARG, "null routing pointer");
-    if (a_div < 1 || num_pairs < 1 || capacity < 1 || capacity % block_m)
+    if (a_div < 1 || num_pairs < 1 || capacity < 1 || block_m < 1 || capacity % block_m ||
+        num_experts < 1)
         return fail(W4A16_ERR_INVALID_ARG, "bad grouped-GEMM sizes");
     if (!moe_gemm_supported(N, K, G, block_m))
         return fail(W4A16_ERR_UNSUPPORTED,
@@ -449,7 +578,7 @@ W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div
     p.M = capacity; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
     p.sorted_ids = sorted_ids; p.expert_ids = expert_ids;
     p.num_post_padded = num_tokens_post_padded;
-    p.num_pairs = num_pairs; p.a_div = a_div;
+    p.num_pairs = num_pairs; p.a_div = a_div; p.num_experts = num_experts;
     p.qweight_stride = qweight_expert_stride; p.scales_stride = scales_expert_stride;
     p.qzeros_stride = qzeros_expert_stride;
     hipError_t e = launch_moe_gemm(fmt, p, block_m, capacity / block_m,
@@ -460,11 +589,8 @@ W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div
 W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, void* out,
                                              int32_t inter, int32_t total) {
     if (!gate_up || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
-    if (inter < 1 || total < 0 || total % inter)
-        return fail(W4A16_ERR_INVALID_ARG, "total (%d) must be a multiple of inter (%d)", total,
-                    inter);
-    if (inter % 8 || !aligned(gate_up, 16) || !aligned(out, 16))
-        return fail(W4A16_ERR_UNSUPPORTED, "inter must be a multiple of 8 and pointers 16-byte aligned");
+    if (inter < 1 || total < 0)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (inter=%d total=%d)", inter, total);
     if (total == 0) return W4A16_OK;
     hipError_t e = launch_silu_mul(static_cast<const half_t*>(gate_up), static_cast<half_t*>(out),
                                    inter, total, static_cast<hipStream_t>(stream));
@@ -617,7 +743,7 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
         PrefillParams p{};
         p.sorted_ids = sorted; p.expert_ids = experts; p.num_post_padded = npp;
         p.tiles = tiles; p.num_tiles = ntiles;
-        p.num_pairs = P; p.G = G; p.zero_offset = zero_offset; p.M = L.capacity;
+        p.num_pairs = P; p.G = G; p.zero_offset = zero_offset; p.M = L.capacity; p.num_experts = E;
         // gate/up: h[p] = x[p / topk] @ W13[e]
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(w13_qweight);
@@ -652,14 +778,14 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
     rc = w4a16_moe_align(stream, ids, P, E, block_m, L.capacity, sorted, experts, npp);
     if (!rc) {
         rc = w4a16_moe_gemm(stream, fmt, x, topk, w13_qweight, w13_scales, w13_qzeros,
-                            (int64_t)K * n13 / 8, (int64_t)(K / G) * n13, (int64_t)(K / G) * n13 / 8,
+                            (int64_t)K * n13 / 8, (int64_t)(K / G) * n13, (int64_t)(K / G) * n13 / 8, E,
                             sorted, experts, npp, h, P, (int32_t)n13, K, G, block_m, L.capacity,
                             zero_offset);
     }
     if (!rc) rc = fused_silu_mul_interleaved_f16(stream, h, a, I, P * I);
     if (!rc)
         rc = w4a16_moe_gemm(stream, fmt, a, 1, w2_qweight, w2_scales, w2_qzeros,
-                            (int64_t)I * K / 8, (int64_t)(I / G) * K, (int64_t)(I / G) * K / 8,
+                            (int64_t)I * K / 8, (int64_t)(I / G) * K, (int64_t)(I / G) * K / 8, E,
                             sorted, experts, npp, yp, P, K, I, G, block_m, L.capacity, zero_offset);
     if (!rc) rc = w4a16_moe_sum(stream, yp, wts, out, T, topk, K);
     return rc;

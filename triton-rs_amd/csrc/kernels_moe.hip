@@ -85,7 +85,11 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
     // split-K counters of the grouped GEMMs that follow start at zero on every call
     for (int i = tid; i < n_counters; i += ALIGN_THREADS) counters[(size_t)i * FLAG_STRIDE] = 0u;
     __syncthreads();
-    for (int p = tid; p < P; p += ALIGN_THREADS) atomicAdd(&cnt[ids[p]], 1);
+    // ids outside [0, E) (caller data) are dropped: such a pair is listed in no block
+    for (int p = tid; p < P; p += ALIGN_THREADS) {
+        const int e = ids[p];
+        if ((unsigned)e < (unsigned)E) atomicAdd(&cnt[e], 1);
+    }
     __syncthreads();
     if (tid == 0) {
         int acc = 0;
@@ -130,7 +134,8 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
 
     for (int c0 = 0; c0 < P; c0 += ALIGN_THREADS) {
         const int p = c0 + tid;
-        const int mine = p < P ? ids[p] : -1;
+        int mine = p < P ? ids[p] : -1;
+        if ((unsigned)mine >= (unsigned)E) mine = -1;
         int rank = 0;
         for (int e = 0; e < E; ++e) {
             const uint64_t bal = __ballot(mine == e);
@@ -150,7 +155,7 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
             }
             __syncthreads();
         }
-        if (p < P) sorted_ids[start[mine] + rank] = p;
+        if (mine >= 0) sorted_ids[start[mine] + rank] = p;
     }
 }
 
@@ -171,7 +176,10 @@ hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int c
 // ------------------------------------------------------------------ activation
 
 // out[b, i] = f16(silu(g) * u), g = gate_up[b, i], u = gate_up[b, inter + i], silu computed
-// in f32 as g / (1 + exp(-g)) (elementwise.rs:188-212). Eight outputs per thread.
+// in f32 as g / (1 + exp(-g)) (elementwise.rs:188-212). Eight outputs per thread where inter
+// and total are multiples of 8 and both buffers 16-byte aligned; one per thread otherwise
+// (any inter, and a last row cut short when total is not a multiple of inter, as the
+// reference's masked kernel allows).
 __global__ void __launch_bounds__(256)
 silu_mul_kernel(const half_t* __restrict__ gate_up, half_t* __restrict__ out, int inter,
                 int64_t total) {
@@ -187,12 +195,30 @@ silu_mul_kernel(const half_t* __restrict__ gate_up, half_t* __restrict__ out, in
     *reinterpret_cast<half8_t*>(out + i8) = o;
 }
 
+// Any inter and any alignment: one output per thread.
+__global__ void __launch_bounds__(256)
+silu_mul_scalar_kernel(const half_t* __restrict__ gate_up, half_t* __restrict__ out, int inter,
+                       int64_t total) {
+    const int64_t i1 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i1 >= total) return;
+    const int64_t b = i1 / inter, i = i1 - b * inter;
+    const half_t* g = gate_up + b * 2 * inter + i;
+    out[i1] = silu_mul_f16(g[0], g[inter]);
+}
+
 hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
                            hipStream_t st) {
     (void)hipGetLastError();
-    const int64_t threads = total / 8;
-    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                       gate_up, out, inter, total);
+    const bool vec = inter % 8 == 0 && total % 8 == 0 && (reinterpret_cast<uintptr_t>(gate_up) % 16) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    if (vec) {
+        const int64_t threads = total / 8;
+        hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, gate_up, out, inter, total);
+    } else {
+        hipLaunchKernelGGL(silu_mul_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                           0, st, gate_up, out, inter, total);
+    }
     return hipGetLastError();
 }
 

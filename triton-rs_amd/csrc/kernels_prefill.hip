@@ -64,6 +64,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     if constexpr (MOE) {
         if (m0 >= *p.num_post_padded) return;      // uniform: past the padded pair count
         const int e = p.expert_ids[blockIdx.y];
+        if ((unsigned)e >= (unsigned)p.num_experts) return;   // caller data out of range
         p.qweight += (size_t)e * p.qweight_stride;
         p.scales += (size_t)e * p.scales_stride;
         if (p.qzeros) p.qzeros += (size_t)e * p.qzeros_stride;
@@ -72,7 +73,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     auto src_row = [&](int row) -> int {
         if constexpr (MOE) {
             const int pair = p.sorted_ids[m0 + row];
-            return pair < p.num_pairs ? pair / p.a_div : -1;
+            return (unsigned)pair < (unsigned)p.num_pairs ? pair / p.a_div : -1;
         } else {
             return m0 + row < p.M ? m0 + row : -1;
         }
@@ -80,7 +81,7 @@ __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
     auto dst_row = [&](int row) -> int {
         if constexpr (MOE) {
             const int pair = p.sorted_ids[m0 + row];
-            return pair < p.num_pairs ? pair : -1;
+            return (unsigned)pair < (unsigned)p.num_pairs ? pair : -1;
         } else {
             return m0 + row < p.M ? m0 + row : -1;
         }
@@ -390,6 +391,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         } else {
             if (m0 >= *p.num_post_padded) return;
             e = p.expert_ids[blockIdx.y];
+            if ((unsigned)e >= (unsigned)p.num_experts) return;   // caller data out of range
         }
         p.qweight += (size_t)e * p.qweight_stride;
         p.scales += (size_t)e * p.scales_stride;
@@ -399,7 +401,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         if constexpr (MOE) {
             if (row >= rows) return -1;
             const int pair = p.sorted_ids[m0 + row];
-            return pair < p.num_pairs ? pair / p.a_div : -1;
+            return (unsigned)pair < (unsigned)p.num_pairs ? pair / p.a_div : -1;
         } else {
             return m0 + row < p.M ? m0 + row : -1;
         }
@@ -408,7 +410,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         if constexpr (MOE) {
             if (row >= rows) return -1;
             const int pair = p.sorted_ids[m0 + row];
-            return pair < p.num_pairs ? pair : -1;
+            return (unsigned)pair < (unsigned)p.num_pairs ? pair : -1;
         } else {
             return m0 + row < p.M ? m0 + row : -1;
         }
@@ -702,7 +704,7 @@ static bool dma_ok(int N, int K, int G, long long a_rows) {
            (long long)(K / G) * N * 2 < lim;
 }
 
-PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
+PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int max_ksplit) {
     PrefillShape s{};
     (void)fmt;
     if (M < 1 || N % 8 || K % BK || G % 8 || K % G) return s;
@@ -737,7 +739,7 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus) {
                 (wgs < num_cus || K / BK / 2 >= 64)) {
                 const int tiles = (N / 256) * ((M + 255) / 256);
                 int ks = 1;
-                while (ks < 4 && tiles * ks * 2 <= num_cus && (K / BK) % (ks * 2) == 0 &&
+                while (ks < 4 && ks * 2 <= max_ksplit && tiles * ks * 2 <= num_cus && (K / BK) % (ks * 2) == 0 &&
                        K / BK / (ks * 2) >= 8)
                     ks *= 2;
                 if (ks > 1) { s.bn = 256; s.ksplit = ks; }

@@ -74,6 +74,7 @@ struct PrefillParams {
     const int32_t* expert_ids;       // [capacity / block_m]
     const int32_t* num_post_padded;  // device scalar
     int num_pairs, a_div;            // x row of pair p is p / a_div
+    int num_experts;                 // expert ids outside [0, num_experts): block skipped
     int64_t qweight_stride, scales_stride, qzeros_stride;   // per expert, in elements
     // expert-tile mode (tiles != nullptr): workgroup row y computes tile y of the list,
     // {first sorted row, rows, expert, 0}, while y < *num_tiles; expert_ids and
@@ -97,7 +98,8 @@ struct PrefillShape {
 
 size_t prefill_dma_lds(int bm, int bn);
 
-PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus);
+// max_ksplit caps the K split (1: never split, so no scratch is needed).
+PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int max_ksplit = 4);
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st);
 bool moe_gemm_supported(int N, int K, int G, int block_m);
 hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
@@ -179,5 +181,33 @@ struct DequantParams {
     int transposed;
 };
 hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st);
+
+// ------------------------------------------------------------------ op layer (api.cpp)
+
+// Split-K scratch of one call: tile counters (FLAG_STRIDE apart), the fixed-point hand-off's
+// slot words and split masks (FIX_MAX_ENTRIES each), fp32 partials. Counters, slots and masks
+// are zero between calls.
+struct Scratch {
+    uint32_t* counters;
+    uint64_t* slots;
+    uint32_t* masks;
+    float* partials;
+};
+// Where a call's scratch comes from: the per-stream workspace the library allocates (grows on
+// demand), or a fixed area (limits below; get() never allocates).
+struct ScratchSource {
+    size_t max_partial_bytes;
+    size_t max_tiles;
+    bool may_probe;   // may run the XCD placement probe (it allocates)
+    int (*get)(hipStream_t st, size_t partial_bytes, Scratch* out);
+};
+ScratchSource alloc_scratch_source();
+
+// w4a16_gemm with the scratch taken from `src`.
+int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const void* scales,
+              const void* qzeros, const int32_t* g_idx, void* out, int32_t M, int32_t N,
+              int32_t K, int32_t G, int32_t zero_offset, const ScratchSource& src);
+int fail(int code, const char* fmt, ...);
+int hip_fail(hipError_t e, const char* what);
 
 }  // namespace w4a16
