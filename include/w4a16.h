@@ -96,6 +96,22 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
                          void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
                          int32_t gptq_zero_offset);
 
+/* No counterpart in the reference: for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and
+ * results as w4a16_gemm, but the split-K scratch (counters, fixed-point hand-off slots,
+ * fp32 partials) lives in a fixed device array of w4a16_gemm_noalloc_scratch_bytes() bytes
+ * (8 MiB: at most 1024 split-K tiles and 7 MiB of partials), one per device, held until the
+ * process ends; the call itself allocates nothing. Requests beyond those limits fail with
+ * W4A16_ERR_UNSUPPORTED (a prefill whose K split would exceed them runs unsplit instead).
+ * All calls on one device share its array: calls that overlap in time on one device (other
+ * streams or threads) race and must be serialised by the caller. The device's array is set
+ * up by w4a16_init (recommended before capture) or by the first call on the device. */
+W4A16_API int w4a16_gemm_noalloc(void* stream, int fmt, const void* x, const void* qweight,
+                                 const void* scales, const void* qzeros, const int32_t* g_idx,
+                                 void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                                 int32_t gptq_zero_offset);
+W4A16_API size_t w4a16_gemm_noalloc_scratch_bytes(void);
+
 /* Which kernel w4a16_gemm would run for this problem (no GPU access). */
 W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t group_size,
                               int has_g_idx, int* kernel);

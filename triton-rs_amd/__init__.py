@@ -67,7 +67,8 @@ _ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, Module
                                InvalidLaunchConfig, BackendDisabled, NotFound)}
 
 EXPORTED = (
-    "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_plan",
+    "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_noalloc",
+    "w4a16_gemm_noalloc_scratch_bytes", "w4a16_gemm_plan",
     "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
@@ -97,6 +98,9 @@ def lib() -> ctypes.CDLL:
         L.w4a16_gemm.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_plan.argtypes = [_I, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]
         L.w4a16_init.argtypes = [_I]
+        L.w4a16_gemm_noalloc.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.w4a16_gemm_noalloc_scratch_bytes.restype = ctypes.c_size_t
+        L.w4a16_gemm_noalloc_scratch_bytes.argtypes = []
         L.w4a16_typed_plan.argtypes = [_I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int32), _I,
                                        ctypes.POINTER(ctypes.c_int)]
         L.w4a16_gptq_gemm_typed.argtypes = [_P] * 6 + [_I] * 14
@@ -237,6 +241,22 @@ def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
             raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
     check(lib().w4a16_gemm(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
                            _ptr(g_idx), _ptr(out), M, N, K, group_size, zero_offset))
+    return out
+
+
+def gemm_noalloc(x, qweight, scales, qzeros, out, fmt="awq", group_size: int = 128, g_idx=None,
+                 zero_offset: int = 1) -> torch.Tensor:
+    """w4a16_gemm_noalloc: as gemm(), but the library allocates nothing during the call (its
+    split-K scratch is a fixed per-device array); `out` must be given."""
+    f = _fmt(fmt)
+    M, K = x.shape
+    N = qweight.shape[1] * 8 if f == FMT_AWQ else qweight.shape[1]
+    _require(out, "out", _HALF, x.device)
+    if tuple(out.shape) != (M, N) or not out.is_contiguous():
+        raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
+    check(lib().w4a16_gemm_noalloc(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales),
+                                   _ptr(qzeros), _ptr(g_idx), _ptr(out), M, N, K, group_size,
+                                   zero_offset))
     return out
 
 

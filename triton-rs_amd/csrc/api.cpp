@@ -207,6 +207,10 @@ W4A16_API int w4a16_init(int32_t device) {
     if (prev != device && (e = hipSetDevice(device)) != hipSuccess) return hip_fail(e, "hipSetDevice");
     (void)device_cus();
     (void)xcd_placement(nullptr);
+    if (int rc = noalloc_setup(nullptr)) {
+        if (prev != device) (void)hipSetDevice(prev);
+        return rc;
+    }
     if (prev != device && (e = hipSetDevice(prev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
     return W4A16_OK;
 }

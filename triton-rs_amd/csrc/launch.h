@@ -210,4 +210,8 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
 int fail(int code, const char* fmt, ...);
 int hip_fail(hipError_t e, const char* what);
 
+// Allocation-free entry point's per-device set-up (noalloc.hip): looks up the device's copy of
+// the scratch array and clears it (on `st`; waited for when st is the null stream).
+int noalloc_setup(hipStream_t st = nullptr);
+
 }  // namespace w4a16
