@@ -112,6 +112,25 @@ W4A16_API int w4a16_gemm_noalloc(void* stream, int fmt, const void* x, const voi
                                  int32_t gptq_zero_offset);
 W4A16_API size_t w4a16_gemm_noalloc_scratch_bytes(void);
 
+/* GPTQ act-order (desc_act) in group order; no reference counterpart (the reference has no
+ * act-order, w4a16_gptq_gemm_typed.rs:221 uses group k / group_size).
+ * w4a16_prepare_act_order, once per checkpoint: perm_out (int32 [K]) = the rows sorted by
+ * g_idx, stable in k; qweight_out (GPTQ qweight [K/8, N], not aliasing qweight) = the rows of
+ * qweight in that order. Every group must hold exactly group_size rows (a desc_act
+ * checkpoint's g_idx is a permutation of repeat(0 .. K/G-1, G)); g_idx is read on the host,
+ * so the call synchronises `stream` and cannot be captured. scales and qzeros are unchanged.
+ * w4a16_gemm_act_order then computes the act-order product x @ W16 from the prepared weights
+ * as x[:, perm] @ W16' with plain group order: a gather of x's columns (into a per-(device,
+ * stream) buffer the library keeps, growing as w4a16_gemm's workspace does), then the kernel
+ * w4a16_gemm plans for (M, N, K) without g_idx (GEMV, small batch or prefill). */
+W4A16_API int w4a16_prepare_act_order(void* stream, int fmt, const void* qweight,
+                                      const int32_t* g_idx, int32_t K, int32_t N,
+                                      int32_t group_size, void* qweight_out, int32_t* perm_out);
+W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const void* qweight,
+                                   const void* scales, const void* qzeros, const int32_t* perm,
+                                   void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
+                                   int32_t gptq_zero_offset);
+
 /* Which kernel w4a16_gemm would run for this problem (no GPU access). */
 W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t group_size,
                               int has_g_idx, int* kernel);

@@ -232,3 +232,17 @@ def test_init_without_device_reports_backend_disabled():
     if torch.cuda.is_available():
         pytest.skip("a device is present")
     assert P.lib().w4a16_init(0) == P.ERR_BACKEND_DISABLED
+
+
+def test_act_order_argument_errors():
+    P = pkg()
+    L = P.lib()
+    v = ctypes.c_void_p(256)
+    w = ctypes.c_void_p(512)
+    assert L.w4a16_prepare_act_order(None, P.FMT_AWQ, v, v, 4096, 512, 128, w, w) == P.ERR_INVALID_ARG
+    assert L.w4a16_prepare_act_order(None, P.FMT_GPTQ, v, v, 4096, 512, 128, v, w) == P.ERR_INVALID_ARG
+    assert "alias" in L.w4a16_last_error().decode()
+    assert L.w4a16_prepare_act_order(None, P.FMT_GPTQ, v, v, 4000, 512, 128, w, w) == P.ERR_INVALID_ARG
+    assert L.w4a16_gemm_act_order(None, P.FMT_AWQ, v, v, v, v, v, v, 1, 512, 4096, 128, 1) == P.ERR_INVALID_ARG
+    assert L.w4a16_gemm_act_order(None, P.FMT_GPTQ, v, v, v, v, None, v, 1, 512, 4096, 128, 1) == P.ERR_INVALID_ARG
+    assert "perm" in L.w4a16_last_error().decode()

@@ -68,7 +68,8 @@ _ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, Module
 
 EXPORTED = (
     "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_noalloc",
-    "w4a16_gemm_noalloc_scratch_bytes", "w4a16_gemm_plan",
+    "w4a16_gemm_noalloc_scratch_bytes", "w4a16_gemm_plan", "w4a16_prepare_act_order",
+    "w4a16_gemm_act_order",
     "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
@@ -98,6 +99,8 @@ def lib() -> ctypes.CDLL:
         L.w4a16_gemm.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_plan.argtypes = [_I, _I, _I, _I, _I, _I, ctypes.POINTER(ctypes.c_int)]
         L.w4a16_init.argtypes = [_I]
+        L.w4a16_prepare_act_order.argtypes = [_P, _I, _P, _P, _I, _I, _I, _P, _P]
+        L.w4a16_gemm_act_order.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc_scratch_bytes.restype = ctypes.c_size_t
         L.w4a16_gemm_noalloc_scratch_bytes.argtypes = []
@@ -241,6 +244,35 @@ def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
             raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
     check(lib().w4a16_gemm(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
                            _ptr(g_idx), _ptr(out), M, N, K, group_size, zero_offset))
+    return out
+
+
+def prepare_act_order(qweight: torch.Tensor, g_idx: torch.Tensor, group_size: int = 128,
+                      fmt="gptq"):
+    """(qweight in group order, perm): the one-time act-order repack (synchronises)."""
+    f = _fmt(fmt)
+    _require(qweight, "qweight", _INT32)
+    _require(g_idx, "g_idx", _INT32, qweight.device)
+    K, N = qweight.shape[0] * 8, qweight.shape[1]
+    qout = torch.empty_like(qweight)
+    perm = torch.empty(K, dtype=torch.int32, device=qweight.device)
+    check(lib().w4a16_prepare_act_order(_stream(qweight), f, _ptr(qweight.contiguous()),
+                                        _ptr(g_idx.contiguous()), K, N, group_size, _ptr(qout),
+                                        _ptr(perm)))
+    return qout, perm
+
+
+def gemm_act_order(x, qweight_prepared, scales, qzeros, perm, fmt="gptq", group_size: int = 128,
+                   zero_offset: int = 1, out=None) -> torch.Tensor:
+    """x @ W16 for an act-order checkpoint prepared by prepare_act_order."""
+    f = _fmt(fmt)
+    M, K = x.shape
+    N = qweight_prepared.shape[1]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    check(lib().w4a16_gemm_act_order(_stream(x), f, _ptr(x), _ptr(qweight_prepared), _ptr(scales),
+                                     _ptr(qzeros), _ptr(perm), _ptr(out), M, N, K, group_size,
+                                     zero_offset))
     return out
 
 

@@ -1,0 +1,73 @@
+// GPTQ act-order (desc_act) in group order: the one-time repack of a checkpoint's qweight
+// rows into the order of their groups, and the per-call gather of the activations' columns
+// into the same order.
+//
+// A desc_act checkpoint stores row k of W in its natural place and assigns it group g_idx[k]
+// (the reference has no act-order; its GEMM uses group k / G, w4a16_gptq_gemm_typed.rs:221).
+// With perm the stable sort of the rows by group (perm[j] = the j-th row in group order) and
+// every group holding exactly G rows, row j of the repacked matrix W'[j] = W[perm[j]] lies
+// in group j / G, so
+//     y = x @ W = sum_k x[:, k] W[k] = sum_j x[:, perm[j]] W'[j] = x' @ W',  x' = x[:, perm]
+// and W' is an ordinary (non-act-order) GPTQ matrix with the same scales and qzeros: every
+// kernel of the plain path applies, the prefill's dequant-to-LDS included.
+#include "device_common.h"
+#include "launch.h"
+
+namespace w4a16 {
+
+// qout[jp, n] nibble i = nibble (perm[8 jp + i] % 8) of q[perm[8 jp + i] / 8, n].
+// Grid (ceil(N / 256), K / 8), 256 threads: one output word per thread, columns coalesced.
+__global__ void __launch_bounds__(256)
+gptq_repack_rows_kernel(const uint32_t* __restrict__ q, const int32_t* __restrict__ perm,
+                        uint32_t* __restrict__ qout, int K, int N) {
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    const int jp = blockIdx.y;
+    if (n >= N) return;
+    uint32_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int src = perm[8 * jp + i];
+        const uint32_t v = q[(size_t)(src >> 3) * N + n];
+        w |= ((v >> (4 * (src & 7))) & 0xFu) << (4 * i);
+    }
+    qout[(size_t)jp * N + n] = w;
+}
+
+// xout[m, j] = x[m, perm[j]]. Grid (ceil(K / 2048), M), 256 threads x 8 columns.
+__global__ void __launch_bounds__(256)
+gather_columns_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
+                      half_t* __restrict__ xout, int K) {
+    const int j0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+    const size_t row = (size_t)blockIdx.y * K;
+    if (j0 >= K) return;
+    if (j0 + 8 <= K) {
+        half8_t v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = x[row + perm[j0 + i]];
+        *reinterpret_cast<half8_t*>(xout + row + j0) = v;
+    } else {
+        for (int j = j0; j < K; ++j) xout[row + j] = x[row + perm[j]];
+    }
+}
+
+hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
+                                   int N, hipStream_t st) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(gptq_repack_rows_kernel, dim3((N + 255) / 256, K / 8), dim3(256), 0, st, q,
+                       perm, qout, K, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
+                                 hipStream_t st) {
+    (void)hipGetLastError();
+    constexpr int MAX_ROWS = 32768;   // grid y per launch
+    for (int m0 = 0; m0 < M; m0 += MAX_ROWS) {
+        const int rows = M - m0 < MAX_ROWS ? M - m0 : MAX_ROWS;
+        hipLaunchKernelGGL(gather_columns_kernel, dim3((K + 2047) / 2048, rows), dim3(256), 0, st,
+                           x + (size_t)m0 * K, perm, xout + (size_t)m0 * K, K);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace w4a16

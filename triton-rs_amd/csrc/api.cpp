@@ -59,33 +59,48 @@ static bool stream_capturing(hipStream_t st) {
     return cs != hipStreamCaptureStatusNone;
 }
 
-static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
+// The buffer of `map` for the current device and stream, at least `need` bytes; a new one
+// (first `zero` bytes cleared, ordered on the stream) replaces a smaller one, which is retired.
+static int stream_buffer(std::map<std::pair<int, hipStream_t>, Workspace>& map, hipStream_t st,
+                         size_t need, size_t zero, const char* what, void** base) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[{dev, st}];
-    const size_t total = COUNTER_BYTES + need;
-    if (w.bytes < total) {
+    Workspace& w = map[{dev, st}];
+    if (w.bytes < need) {
         if (stream_capturing(st))
             return fail(W4A16_ERR_UNSUPPORTED,
-                        "split-K workspace of %zu bytes needed while the stream is being captured: "
-                        "make one call of this size on the stream before capturing", total);
-        const size_t grow = total < (size_t)(8 << 20) ? (size_t)(8 << 20) : total;
+                        "%s of %zu bytes needed while the stream is being captured: "
+                        "make one call of this size on the stream before capturing", what, need);
+        const size_t grow = need < (size_t)(8 << 20) ? (size_t)(8 << 20) : need;
         void* fresh = nullptr;
         e = hipMalloc(&fresh, grow);
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(workspace)");
-        // ordered after everything queued on the stream, before this call's kernels
-        e = hipMemsetAsync(fresh, 0, COUNTER_BYTES, st);
-        if (e != hipSuccess) { (void)hipFree(fresh); return hip_fail(e, "hipMemsetAsync(workspace counters)"); }
+        if (zero) {
+            // ordered after everything queued on the stream, before this call's kernels
+            e = hipMemsetAsync(fresh, 0, zero, st);
+            if (e != hipSuccess) { (void)hipFree(fresh); return hip_fail(e, "hipMemsetAsync(workspace)"); }
+        }
         if (w.base) g_ws_retired.push_back(w.base);
         w.base = fresh;
         w.bytes = grow;
     }
-    *counters = static_cast<uint32_t*>(w.base);
-    *partials = reinterpret_cast<float*>(static_cast<char*>(w.base) + COUNTER_BYTES);
+    *base = w.base;
     return W4A16_OK;
 }
+
+static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float** partials) {
+    void* base = nullptr;
+    if (int rc = stream_buffer(g_ws, st, COUNTER_BYTES + need, COUNTER_BYTES, "split-K workspace", &base))
+        return rc;
+    *counters = static_cast<uint32_t*>(base);
+    *partials = reinterpret_cast<float*>(static_cast<char*>(base) + COUNTER_BYTES);
+    return W4A16_OK;
+}
+
+// Per-(device, stream) buffer for activations gathered into act-order group order.
+static std::map<std::pair<int, hipStream_t>, Workspace> g_gather;
 
 // ------------------------------------------------------------------ validation
 
@@ -371,6 +386,75 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
                          int32_t M, int32_t N, int32_t K, int32_t G, int32_t zero_offset) {
     return gemm_impl(stream, fmt, x, qweight, scales, qzeros, g_idx, out, M, N, K, G, zero_offset,
                      alloc_scratch_source());
+}
+
+// ------------------------------------------------------------------ act-order in group order
+
+W4A16_API int w4a16_prepare_act_order(void* stream, int fmt, const void* qweight,
+                                      const int32_t* g_idx, int32_t K, int32_t N, int32_t G,
+                                      void* qweight_out, int32_t* perm_out) {
+    if (fmt != W4A16_FMT_GPTQ && fmt != W4A16_FMT_GPTQ_SYM)
+        return fail(W4A16_ERR_INVALID_ARG, "act-order repack takes the GPTQ formats (fmt %d)", fmt);
+    if (!qweight || !g_idx || !qweight_out || !perm_out)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (K < 8 || N < 1 || G < 1 || K % 8 || K % G)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (K=%d N=%d group_size=%d)", K, N, G);
+    if (K / 8 > 65535) return fail(W4A16_ERR_UNSUPPORTED, "K (%d) above 524280", K);
+    if (qweight == qweight_out)
+        return fail(W4A16_ERR_INVALID_ARG, "qweight_out must not alias qweight");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (stream_capturing(st))
+        return fail(W4A16_ERR_UNSUPPORTED, "w4a16_prepare_act_order synchronises: not under capture");
+    // the group table is read on the host (once per checkpoint): validated, then sorted
+    std::vector<int32_t> gi((size_t)K), perm((size_t)K);
+    hipError_t e = hipMemcpyAsync(gi.data(), g_idx, (size_t)K * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "reading g_idx");
+    const int groups = K / G;
+    std::vector<int32_t> start((size_t)groups + 1, 0);
+    for (int k = 0; k < K; ++k) {
+        if (gi[k] < 0 || gi[k] >= groups)
+            return fail(W4A16_ERR_INVALID_ARG, "g_idx[%d] = %d outside [0, %d)", k, gi[k], groups);
+        ++start[(size_t)gi[k] + 1];
+    }
+    for (int g = 0; g < groups; ++g) {
+        if (start[(size_t)g + 1] != G)
+            return fail(W4A16_ERR_INVALID_ARG,
+                        "group %d holds %d rows; group order needs exactly group_size (%d) rows "
+                        "per group", g, start[(size_t)g + 1], G);
+        start[(size_t)g + 1] += start[(size_t)g];
+    }
+    for (int k = 0; k < K; ++k) perm[(size_t)start[(size_t)gi[k]]++] = k;   // stable in k
+    e = hipMemcpyAsync(perm_out, perm.data(), (size_t)K * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "writing perm");
+    e = launch_gptq_repack_rows(static_cast<const uint32_t*>(qweight), perm_out,
+                                static_cast<uint32_t*>(qweight_out), K, N, st);
+    // the host copy of perm must outlive the transfer: wait whatever the launch returned
+    const hipError_t es = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "act-order repack launch");
+    return es == hipSuccess ? W4A16_OK : hip_fail(es, "act-order repack");
+}
+
+W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const void* qweight,
+                                   const void* scales, const void* qzeros, const int32_t* perm,
+                                   void* out, int32_t M, int32_t N, int32_t K, int32_t G,
+                                   int32_t zero_offset) {
+    if (fmt != W4A16_FMT_GPTQ && fmt != W4A16_FMT_GPTQ_SYM)
+        return fail(W4A16_ERR_INVALID_ARG, "act-order GEMM takes the GPTQ formats (fmt %d)", fmt);
+    int rc = check_gemm_args(fmt, x, qweight, scales, qzeros, out, M, N, K, G);
+    if (!rc) rc = check_zero_offset(fmt, zero_offset);
+    if (rc) return rc;
+    if (!perm) return fail(W4A16_ERR_INVALID_ARG, "perm is null");
+    if (!aligned(x, 16)) return fail(W4A16_ERR_INVALID_ARG, "x must be 16-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    void* xg = nullptr;
+    rc = stream_buffer(g_gather, st, (size_t)M * K * sizeof(half_t), 0, "act-order gather buffer", &xg);
+    if (rc) return rc;
+    hipError_t e = launch_gather_columns(static_cast<const half_t*>(x), perm,
+                                         static_cast<half_t*>(xg), M, K, st);
+    if (e != hipSuccess) return hip_fail(e, "act-order gather launch");
+    return gemm_impl(stream, fmt, xg, qweight, scales, qzeros, nullptr, out, M, N, K, G,
+                     zero_offset, alloc_scratch_source());
 }
 
 // The reference kernels' parameter lists with arbitrary strides. A call whose tensors are

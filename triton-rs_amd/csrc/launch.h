@@ -182,6 +182,13 @@ struct DequantParams {
 };
 hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st);
 
+// Act-order in group order (act_order.hip): qout = rows of the GPTQ qweight q [K/8, N] taken
+// in the order perm (row j of qout = row perm[j] of q); xout [M, K] = x[:, perm].
+hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
+                                   int N, hipStream_t st);
+hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
+                                 hipStream_t st);
+
 // ------------------------------------------------------------------ op layer (api.cpp)
 
 // Split-K scratch of one call: tile counters (FLAG_STRIDE apart), the fixed-point hand-off's
