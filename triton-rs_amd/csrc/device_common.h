@@ -100,6 +100,18 @@ __device__ __forceinline__ const T* at_bytes(const T* base, uint32_t byte_off) {
     return reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
+// Buffer resource over [base, base + bytes) (raw buffer, no swizzle; gfx9 word 3) and loads
+// through it: address = base + voffset (per lane) + soffset (uniform, an SGPR), so a wave
+// streaming rows of a matrix keeps one per-lane offset and adds the row offset on the scalar
+// unit. aux = 2 is the non-temporal (streaming) hint. Out-of-range offsets read zero.
+typedef __amdgpu_buffer_rsrc_t bufrsrc_t;
+__device__ __forceinline__ bufrsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_ld_stream(bufrsrc_t r, uint32_t voff, uint32_t soff) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 2);
+}
+
 // Streaming (non-temporal) loads for packed weights, which are read exactly once.
 __device__ __forceinline__ uint32_t ld_stream(const uint32_t* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ u32x2 ld_stream2(const uint32_t* p) {

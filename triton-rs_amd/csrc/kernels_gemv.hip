@@ -29,7 +29,14 @@ namespace w4a16 {
 // Tile: 256 columns (32 words per row) x R rows. Lane mapping: LPR = 32 / CW lanes per row,
 // each owning CW words (8*CW columns); RPW = 64 / LPR row-lanes per wave; a lane walks RL
 // consecutive rows (all in one group: G % RL == 0).
-template <int M, int CW, int RL, int WAVES, bool XCD>
+//
+// Load order per wave: x (small, cache-resident after first use), then the RL weight rows
+// (non-temporal buffer loads: one per-lane offset, the row offset in an SGPR), then the
+// group's scales and zero words (non-temporal). Loads complete in issue order, so the weights
+// are consumed while the scales are still in flight; issued first, the scattered scale and
+// zero requests cost 0.3 us at K=4096, N=14336 (7.93 vs 8.28 us, same kernel otherwise), and
+// cached rather than streamed 0.2 us more. The scheduling barriers keep this order.
+template <int M, int CW, int RL, int WAVES, bool XCD, bool FIX>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_awq_kernel(GemvParams p) {
     constexpr int LPR = 32 / CW;
@@ -38,12 +45,13 @@ gemv_awq_kernel(GemvParams p) {
     constexpr int R = RB * RL;
     constexpr int C = 256;
     static_assert(RL % 2 == 0 && RL % 8 == 0, "rows per lane must be a multiple of 8");
+    static_assert(CW == 1 || CW == 2 || CW == 4, "words per lane");
 
     __shared__ float red[RB][M][C];
     __shared__ int flag;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int cl = lane % LPR;
     const int rb = wave * RPW + lane / LPR;
     int ct, split;
@@ -51,11 +59,10 @@ gemv_awq_kernel(GemvParams p) {
     constexpr int SC = XCD ? SCOPE_XCD : SCOPE_DEVICE;
     const int NW = p.N >> 3;                       // words per qweight row
     const int wc0 = ct * 32 + cl * CW;             // first word column of this lane
-    const int k0 = split * R + rb * RL;            // first row of this lane
+    const int kw = split * R + wave * RPW * RL;    // first row of the wave (uniform)
+    const int k0 = kw + (lane / LPR) * RL;         // first row of this lane
     const int g = k0 / p.G;
 
-    // ---- x first (small, cached), so the weight loads below can be consumed in issue
-    // order while later rows are still in flight
     // ---- x pairs (rows 2i, 2i+1 of this lane) for every m, and X = sum of x
     half2_t xs[M][RL / 2];
     float X[M];
@@ -68,29 +75,46 @@ gemv_awq_kernel(GemvParams p) {
             xs[m][4 * i + 0] = as_h2(v.x); xs[m][4 * i + 1] = as_h2(v.y);
             xs[m][4 * i + 2] = as_h2(v.z); xs[m][4 * i + 3] = as_h2(v.w);
         }
-        float s = 0.f;
-        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
-#pragma unroll
-        for (int i = 0; i < RL / 2; ++i) s = dot2(xs[m][i], one2, s);
-        X[m] = s;
     }
 
-    // ---- issue all weight loads (RL rows x CW words) up front
-    // 32-bit element offsets from the uniform base (global_load ... v_off, s_base)
+    // ---- all weight rows of the lane, then its scales and zero words
     uint32_t w[RL][CW];
-    const uint32_t off0 = (uint32_t)k0 * (uint32_t)NW + (uint32_t)wc0;
+    const bufrsrc_t wr = make_rsrc(p.qweight, (uint32_t)((size_t)p.K * p.N / 2));
+    const uint32_t voff = ((uint32_t)(lane / LPR) * (uint32_t)RL * (uint32_t)NW + (uint32_t)wc0) * 4u;
+    const uint32_t row_bytes = (uint32_t)NW * 4u;
+    const uint32_t soff0 = (uint32_t)kw * row_bytes;
 #pragma unroll
     for (int j = 0; j < RL; ++j) {
-        const uint32_t off = off0 + (uint32_t)j * (uint32_t)NW;
+        const uint32_t so = soff0 + (uint32_t)j * row_bytes;
         if constexpr (CW == 4) {
-            const u32x4 v = ld_stream4(at_bytes(p.qweight, 4u * off));
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, voff, so, 2));
             w[j][0] = v.x; w[j][1] = v.y; w[j][2] = v.z; w[j][3] = v.w;
         } else if constexpr (CW == 2) {
-            const u32x2 v = ld_stream2(at_bytes(p.qweight, 4u * off));
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(wr, voff, so, 2));
             w[j][0] = v.x; w[j][1] = v.y;
         } else {
-            w[j][0] = ld_stream(at_bytes(p.qweight, 4u * off));
+            w[j][0] = buf_ld_stream(wr, voff, so);
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t qz[CW];
+    u32x4 sv[CW];
+#pragma unroll
+    for (int c = 0; c < CW; ++c) {
+        qz[c] = p.qzeros ? __builtin_nontemporal_load(p.qzeros + (size_t)g * NW + wc0 + c) : 0u;
+        sv[c] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(p.scales + (size_t)g * p.N + 8 * (wc0 + c)));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float X1024[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+        float sx = 0.f;
+        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+        for (int i = 0; i < RL / 2; ++i) sx = dot2(xs[m][i], one2, sx);
+        X[m] = sx;
+        X1024[m] = 1024.0f * sx;
     }
 
     // ---- main loop: acc[m][cw][slot]
@@ -130,20 +154,17 @@ gemv_awq_kernel(GemvParams p) {
     // ---- zero point and scale, once per lane and column; columns written in natural order
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
-        const int wcol = wc0 + c;
-        uint32_t qz = 0;
-        if (p.qzeros) qz = p.qzeros[(size_t)g * NW + wcol];
-        const uint4 sv = *reinterpret_cast<const uint4*>(p.scales + (size_t)g * p.N + 8 * wcol);
-        const half_t* sh = reinterpret_cast<const half_t*>(&sv);
+        const half_t* sh = reinterpret_cast<const half_t*>(&sv[c]);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             float col[8];
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const int n = awq_col_of_slot(s);
-                const float z = (float)nib(qz, s);
-                const float inv_f = (s & 1) ? (1.0f / 16.0f) : 1.0f;
-                const float u = (acc[m][c][s] - 1024.0f * X[m]) * inv_f - z * X[m];
+                const float z = (float)nib(qz[c], s);
+                // odd slots were unpacked as 1024 + 16 q
+                const float u = (s & 1) ? __builtin_fmaf(acc[m][c][s] - X1024[m], 1.0f / 16.0f, -z * X[m])
+                                        : acc[m][c][s] - X1024[m] - z * X[m];
                 col[n] = (float)sh[n] * u;
             }
             float4* dst = reinterpret_cast<float4*>(&red[rb][m][(cl * CW + c) * 8]);
@@ -155,7 +176,7 @@ gemv_awq_kernel(GemvParams p) {
 
     // ---- reduce over row blocks; write partial (or the output when there is one split)
     const int n0 = ct * C;
-    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+    if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
         constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
         size_t off[E];
         float v[E];
@@ -174,7 +195,7 @@ gemv_awq_kernel(GemvParams p) {
         }
         splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
         return;
-    }
+    } else {
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float s = 0.f;
@@ -187,13 +208,14 @@ gemv_awq_kernel(GemvParams p) {
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
         splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+    }
 }
 
 // ------------------------------------------------------------------ GPTQ GEMV
 
 // Tile: C = LPR * CW columns x R k-rows. A lane owns CW consecutive columns (one 128-bit
 // load per packed row for CW = 4) and RL consecutive packed rows (8*RL k, one group).
-template <int FMT, int M, int CW, int RL, int WAVES, int LPR, bool XCD>
+template <int FMT, int M, int CW, int RL, int WAVES, int LPR, bool XCD, bool FIX>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_gptq_kernel(GemvParams p) {
     constexpr int RPW = 64 / LPR;
@@ -306,7 +328,7 @@ gemv_gptq_kernel(GemvParams p) {
     }
     __syncthreads();
 
-    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+    if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
         constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
         size_t off[E];
         float v[E];
@@ -325,7 +347,7 @@ gemv_gptq_kernel(GemvParams p) {
         }
         splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
         return;
-    }
+    } else {
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float s = 0.f;
@@ -338,6 +360,7 @@ gemv_gptq_kernel(GemvParams p) {
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
         splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+    }
 }
 
 // ------------------------------------------------------------------ AWQ, M = 5..8: matrix-core dot
@@ -361,7 +384,7 @@ gemv_gptq_kernel(GemvParams p) {
 // Tile: WW = 16 CW words (8 WW columns) x WAVES * R rows; lane (j, q) streams rows
 // r0 + (R/4) q + s, s = 0 .. R/4 - 1, of word columns CW j .. CW j + CW - 1 with PF steps of
 // loads in flight.
-template <int M, int CW, int R, int WAVES, int PF, bool XCD>
+template <int M, int CW, int R, int WAVES, int PF, bool XCD, bool FIX>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_awq_mfma_kernel(GemvParams p) {
     constexpr int S = R / 4;          // steps per wave
@@ -508,7 +531,7 @@ gemv_awq_mfma_kernel(GemvParams p) {
 
     // ---- reduce over waves; write partial (or the output when there is one split)
     const int n0 = ct * C;
-    if (p.fixed) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+    if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
         constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
         size_t off[E];
         float v[E];
@@ -527,7 +550,7 @@ gemv_awq_mfma_kernel(GemvParams p) {
         }
         splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
         return;
-    }
+    } else {
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
         const int m = i / C, cidx = i - m * C;
         float sum = 0.f;
@@ -540,6 +563,7 @@ gemv_awq_mfma_kernel(GemvParams p) {
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
         splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+    }
 }
 
 // ------------------------------------------------------------------ host launchers
@@ -591,6 +615,8 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
     } else if (M >= 1 && M <= GEMV_MAX_M && fmt == FMT_AWQ) {
         if (N % 256 || K % AWQ_ROWS || G % AWQ_RL || K % G) return s;
+        // weights are addressed through one buffer resource (32-bit offsets)
+        if ((size_t)K * N / 2 >= ((size_t)1 << 31)) return s;
         s.awq_deep = M == 1 && K % AWQ_ROWS_DEEP == 0;
         // the 256-row tile where the 512-row one leaves fewer than 192 workgroups (4096 ->
         // 4096, 128 workgroups: 5.02 -> 4.33 us; 2048 -> 4096: 4.73 -> 3.74 us), the 512-row
@@ -622,48 +648,48 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     return s;
 }
 
-template <int M, bool XCD>
+template <int M, bool XCD, bool FIX>
 static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     const dim3 block(s.threads);
     if (fmt == FMT_AWQ && s.mfma) {
         if constexpr (M <= GEMV_MFMA_MAX_M) {
             if (s.mfma_wide)
-                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AMW_R, AMW_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AMW_R, AMW_WAVES, AM_PF, XCD, FIX>), grid, block, 0, st, p);
             else
-                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD>), grid, block, 0, st, p);
+                hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AM_R, AM_WAVES, AM_PF, XCD, FIX>), grid, block, 0, st, p);
         }
     } else if constexpr (M <= GEMV_MAX_M) {
         if constexpr (M == 1) {
             if (fmt != FMT_AWQ && s.gptq_deep) {
                 if (fmt == FMT_GPTQ)
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
                 else
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
                 return;
             }
         }
         if constexpr (M > 1) {
             if (fmt != FMT_AWQ && s.gptq_narrow) {
                 if (fmt == FMT_GPTQ)
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX>), grid, block, 0, st, p);
                 else
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX>), grid, block, 0, st, p);
                 return;
             }
         }
         if constexpr (M == 1) {
             if (fmt == FMT_AWQ && s.awq_deep) {
-                hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES_DEEP, XCD>), grid, block, 0, st, p);
+                hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES_DEEP, XCD, FIX>), grid, block, 0, st, p);
                 return;
             }
         }
         if (fmt == FMT_AWQ)
-            hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD, FIX>), grid, block, 0, st, p);
         else if (fmt == FMT_GPTQ)
-            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
         else
-            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
     }
 }
 
@@ -671,8 +697,14 @@ template <int M>
 static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (M > GEMV_MAX_M && !(fmt == FMT_AWQ && s.mfma)) return hipErrorInvalidValue;
-    if (s.xcd) launch_gemv_mx<M, true>(fmt, p, s, st);
-    else launch_gemv_mx<M, false>(fmt, p, s, st);
+    // the hand-off protocol is a template parameter: each kernel carries only the one it uses
+    if (p.fixed) {
+        if (s.xcd) launch_gemv_mx<M, true, true>(fmt, p, s, st);
+        else launch_gemv_mx<M, false, true>(fmt, p, s, st);
+    } else {
+        if (s.xcd) launch_gemv_mx<M, true, false>(fmt, p, s, st);
+        else launch_gemv_mx<M, false, false>(fmt, p, s, st);
+    }
     return hipGetLastError();
 }
 
