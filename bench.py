@@ -192,12 +192,48 @@ def cpu_model() -> str:
 
 # ----------------------------------------------------------------------------- traffic
 
-# workloads a counter run (--pmc-child) can drive: the headline, and config 3's two shapes
+# Workloads a counter run (--pmc-child) can drive, (fmt, M, K, N, G, act_order) each: the
+# configs at the sizes the metric names. "c4_moe" is config 4's fused MoE layer.
 PMC_WORKLOADS = {
-    "headline": HEADLINE,
-    "c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128),
-    "c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128),
+    "headline": HEADLINE + (False,),
+    "c0": ("gptq_sym", 1, 4096, 4096, 128, False),
+    "c1_m1_k14336_n4096": ("awq", 1, 14336, 4096, 128, False),
+    "c1_m4_k4096_n14336": ("awq", 4, 4096, 14336, 128, False),
+    "c1_m4_k14336_n4096": ("awq", 4, 14336, 4096, 128, False),
+    "c1_m8_k4096_n14336": ("awq", 8, 4096, 14336, 128, False),
+    "c1_m8_k14336_n4096": ("awq", 8, 14336, 4096, 128, False),
+    "c2_m16": ("gptq", 16, 4096, 6144, 128, True),
+    "c2_m32": ("gptq", 32, 4096, 6144, 128, True),
+    "c2_m64": ("gptq", 64, 4096, 6144, 128, True),
+    "c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128, False),
+    "c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128, False),
+    "c4_moe": None,
 }
+
+
+def c2_g_idx(torch, dev, K=4096, G=128):
+    """Config 2's act-order groups: a seeded random permutation of repeat(0..K/G-1, G)."""
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(2))
+    return (torch.arange(K) // G)[perm].to(torch.int32).to(dev)
+
+
+def moe_layer(torch, dev, gen):
+    """Config 4's layer: T=512 tokens, 8 experts, top-2, K=4096, I=14336, GPTQ G=128, random
+    packed words, scales in [0.002, 0.02], fp32 router logits ~ N(0, 1)."""
+    T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
+
+    def words(*shape):
+        return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
+
+    def scales(*shape):
+        return (torch.rand(shape, device=dev, generator=gen) * 0.018 + 0.002).half()
+
+    w13 = (words(E, K // 8, 2 * I), scales(E, K // G, 2 * I), words(E, K // G, 2 * I // 8))
+    w2 = (words(E, I // 8, K), scales(E, I // G, K), words(E, I // G, K // 8))
+    x = torch.randn((T, K), device=dev, generator=gen).half()
+    logits = torch.randn((T, E), device=dev, generator=gen)
+    return {"T": T, "E": E, "topk": topk, "K": K, "I": I, "G": G, "w13": w13, "w2": w2,
+            "x": x, "logits": logits}
 
 
 def pmc_child(args) -> int:
@@ -208,15 +244,26 @@ def pmc_child(args) -> int:
     import __graft_entry__
     pkg = __graft_entry__.load_package()
     dev = torch.device("cuda:0")
-    fmt, M, K, N, G = PMC_WORKLOADS[args.pmc_workload]
-    n_sets = args.sets if M <= 64 else 2
-    sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=0x5EED0001)
-    x = torch.randn((M, K), device=dev).half()
-    out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    for i in range(PMC_WARM + PMC_MEASURED):
-        pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G, out=out)
+    if args.pmc_workload == "c4_moe":
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(0x5EED0004)
+        L = moe_layer(torch, dev, gen)
+        out = torch.empty((L["T"], L["K"]), dtype=torch.float16, device=dev)
+        for _ in range(PMC_WARM + PMC_MEASURED):
+            pkg.fused_moe(L["x"], L["logits"], L["w13"], L["w2"], topk=L["topk"], out=out)
+        del L
+    else:
+        fmt, M, K, N, G, act_order = PMC_WORKLOADS[args.pmc_workload]
+        n_sets = args.sets if M <= 64 else 2
+        sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=0x5EED0001)
+        g_idx = c2_g_idx(torch, dev, K, G) if act_order else None
+        x = torch.randn((M, K), device=dev).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        for i in range(PMC_WARM + PMC_MEASURED):
+            pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G, g_idx=g_idx, out=out)
+        del sets
     torch.cuda.synchronize()
-    del sets
+    torch.cuda.empty_cache()
     src = torch.ones(COPY_ELEMS, dtype=torch.int32, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -226,28 +273,87 @@ def pmc_child(args) -> int:
     return 0
 
 
-def _counter_means(csv_dir, counter):
-    """Per-dispatch mean of `counter` for the headline kernel (last PMC_MEASURED dispatches)
-    and for the calibration kernel."""
+def _counter_table(csv_dir):
+    """{kernel name: {counter: [value per dispatch, in dispatch order]}} of a counter run."""
     files = glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True)
-    ours, copy = [], []
+    rows = {}
     for f in files:
         with open(f, newline="") as fh:
             for r in csv.DictReader(fh):
-                if r["Counter_Name"] != counter:
-                    continue
-                name = r["Kernel_Name"]
-                key = (int(r["Dispatch_Id"]), float(r["Counter_Value"]))
-                if "w4a16::" in name:
-                    ours.append(key)
-                elif "neg_kernel" in name:
-                    copy.append(key)
-    ours.sort()
-    ours = [v for _, v in ours[-PMC_MEASURED:]]
-    copy = [v for _, v in copy]
+                rows.setdefault(r["Kernel_Name"], {}).setdefault(r["Counter_Name"], []).append(
+                    (int(r["Dispatch_Id"]), float(r["Counter_Value"])))
+    return {k: {c: [v for _, v in sorted(vals)] for c, vals in cs.items()} for k, cs in rows.items()}
+
+
+def _counter_means(csv_dir, counter):
+    """Per-dispatch mean of `counter` for the library's kernel (last PMC_MEASURED dispatches)
+    and for the calibration kernel."""
+    table = _counter_table(csv_dir)
+    ours = [v for k, cs in table.items() if "w4a16::" in k for v in cs.get(counter, [])]
+    copy = [v for k, cs in table.items() if "neg_kernel" in k for v in cs.get(counter, [])]
+    ours = ours[-PMC_MEASURED:]
     if not ours or not copy:
         raise RuntimeError(f"{counter}: no samples (ours {len(ours)}, copy {len(copy)})")
     return sum(ours) / len(ours), sum(copy) / len(copy)
+
+
+def _rocprof_pass(rocprof, counters, workload, sets, outdir):
+    """One rocprofv3 --pmc run of a --pmc-child process; returns its counter table."""
+    env = dict(os.environ, TMPDIR="/tmp")
+    d = os.path.join(outdir, "_".join(counters)[:80])
+    cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", *counters, "--output-format", "csv",
+           "-d", d, "-o", "pmc", "--", sys.executable, os.path.abspath(__file__),
+           "--pmc-child", "--pmc-workload", workload, "--sets", str(sets)]
+    r = subprocess.run(cmd, cwd="/tmp", env=env, capture_output=True, text=True)
+    if r.returncode != 0:
+        tail = (r.stdout + r.stderr).strip().splitlines()[-3:]
+        raise RuntimeError(f"{counters} pass failed rc={r.returncode}: {tail}")
+    return _counter_table(d)
+
+
+def pmc_report(args) -> int:
+    """Counter report of one workload (--pmc-workload), one JSON line. Default passes:
+    FETCH_SIZE, then WRITE_SIZE, each calibrated against the copy kernel of the same run, per
+    library kernel: HBM bytes per dispatch beside the algorithmic bytes. With --pmc-counters
+    (one pass per ';'-separated group of space-separated counters): the per-dispatch means
+    of those counters per library kernel. Means are over each kernel's last PMC_MEASURED
+    dispatches."""
+    rocprof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    outdir = tempfile.mkdtemp(prefix="w4a16_pmc_", dir="/tmp")
+    groups = ([g.split() for g in args.pmc_counters.split(";") if g.strip()]
+              if args.pmc_counters else [["FETCH_SIZE"], ["WRITE_SIZE"]])
+    rep = {"workload": args.pmc_workload, "passes": [], "measured_dispatches": PMC_MEASURED}
+    spec = PMC_WORKLOADS[args.pmc_workload]
+    if spec is not None:
+        fmt, M, K, N, G, _ = spec
+        rep["algorithmic_bytes"] = algorithmic_bytes(fmt, M, K, N, G)
+    traffic = {}
+    for counters in groups:
+        table = _rocprof_pass(rocprof, counters, args.pmc_workload, args.sets, outdir)
+        kern = {}
+        for name, cs in table.items():
+            if "w4a16::" not in name:
+                continue
+            kern[name] = {c: round(sum(v[-PMC_MEASURED:]) / len(v[-PMC_MEASURED:]), 1)
+                          for c, v in cs.items()}
+            kern[name]["dispatches"] = max(len(v) for v in cs.values())
+        entry = {"counters": counters, "kernels": kern}
+        copy = [v for k, cs in table.items() if "neg_kernel" in k for c, vals in cs.items()
+                for v in vals if c in ("FETCH_SIZE", "WRITE_SIZE")]
+        if copy and counters in (["FETCH_SIZE"], ["WRITE_SIZE"]):
+            factor = (sum(copy) / len(copy)) * 1024.0 / (COPY_ELEMS * 4)
+            entry["calibration_factor"] = round(factor, 4)
+            for name, cs in kern.items():
+                traffic[name] = traffic.get(name, 0.0) + cs[counters[0]] * 1024.0 / factor
+        rep["passes"].append(entry)
+    shutil.rmtree(outdir, ignore_errors=True)
+    if traffic:
+        rep["traffic_bytes_per_dispatch"] = {k: int(v) for k, v in traffic.items()}
+        if "algorithmic_bytes" in rep:
+            rep["traffic_over_algorithmic"] = {
+                k: round(v / rep["algorithmic_bytes"], 3) for k, v in traffic.items()}
+    print(json.dumps(rep), flush=True)
+    return 0
 
 
 def measure_traffic(args):
@@ -313,8 +419,7 @@ def extras(torch, pkg, dev, stream, args):
         gemm_case(f"c1_awq_m{M}_k4096_n14336", "awq", M, 4096, 14336, 128, 20, 1000)
     for M in (1, 4, 8):
         gemm_case(f"c1_awq_m{M}_k14336_n4096", "awq", M, 14336, 4096, 128, 20, 1000)
-    perm = torch.randperm(4096, generator=torch.Generator().manual_seed(2))
-    g_idx = (torch.arange(4096) // 128)[perm].to(torch.int32).to(dev)
+    g_idx = c2_g_idx(torch, dev)
     for M in (16, 32, 64):
         gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 20, 500,
                   g_idx=g_idx)
@@ -363,18 +468,9 @@ def extras(torch, pkg, dev, stream, args):
     typed_case("typed_awq_gemm_int4_m2048_k4096_n14336", 2048, 4096, 14336, 2, 300)
 
     # config 4: fused MoE layer, T=512, 8 experts, top-2, K=4096, I=14336, GPTQ G=128
-    T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
-
-    def words(*shape):
-        return torch.randint(-2 ** 31, 2 ** 31 - 1, shape, dtype=torch.int32, device=dev, generator=gen)
-
-    def scales(*shape):
-        return (torch.rand(shape, device=dev, generator=gen) * 0.018 + 0.002).half()
-
-    w13 = (words(E, K // 8, 2 * I), scales(E, K // G, 2 * I), words(E, K // G, 2 * I // 8))
-    w2 = (words(E, I // 8, K), scales(E, I // G, K), words(E, I // G, K // 8))
-    x = torch.randn((T, K), device=dev, generator=gen).half()
-    logits = torch.randn((T, E), device=dev, generator=gen)
+    L = moe_layer(torch, dev, gen)
+    T, E, topk, K, I = L["T"], L["E"], L["topk"], L["K"], L["I"]
+    w13, w2, x, logits = L["w13"], L["w2"], L["x"], L["logits"]
     out = torch.empty((T, K), dtype=torch.float16, device=dev)
     flops = 2.0 * T * topk * (K * 2 * I + I * K)
     for bm in (64, 128):
@@ -388,7 +484,7 @@ def extras(torch, pkg, dev, stream, args):
             "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
         progress(f"fused moe block_m={bm}: {ms:.3f} ms")
         del ws
-    del w13, w2
+    del w13, w2, L
     torch.cuda.empty_cache()
     res["achievable"] = achievable_refs(torch, dev, stream)
     return res
@@ -451,7 +547,13 @@ def main() -> int:
                          "whose statistics should cover the cold headline dispatches only")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-workload", default="headline", choices=sorted(PMC_WORKLOADS),
-                    help="workload of a --pmc-child run (for counter profiles)")
+                    help="workload of a --pmc-child or --pmc-report run (for counter profiles)")
+    ap.add_argument("--pmc-report", action="store_true",
+                    help="run counter passes over --pmc-workload and print their per-kernel "
+                         "means as one JSON line (FETCH_SIZE/WRITE_SIZE traffic by default)")
+    ap.add_argument("--pmc-counters", default="",
+                    help="counter passes for --pmc-report: groups separated by ';', counters "
+                         "within a group by spaces (one rocprofv3 run per group)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -460,6 +562,8 @@ def main() -> int:
         return 2
     if args.pmc_child:
         return pmc_child(args)
+    if args.pmc_report:
+        return pmc_report(args)
 
     # counter passes run first, in child processes, before this process touches the GPU
     traffic, traffic_detail = (None, {"traffic_note": "skipped (--no-traffic)"})
