@@ -148,16 +148,18 @@ def _disassemble_tu(obj, tmp_path):
 
 
 def test_kernel_choice_evidence_in_isa(tmp_path):
-    """The VALU decode GEMVs use v_dot2 and no MFMA; the AWQ matrix-core GEMV and the strided
-    GEMM use fp16 MFMA. Every GEMV comes in two hand-off variants (device scope, XCD-local)."""
+    """The VALU decode GEMVs use v_dot2 and no MFMA; the AWQ matrix-core GEMVs (block-diagonal
+    and row-paired) and the strided GEMM use fp16 MFMA. Every VALU GEMV comes in two hand-off
+    variants (device scope, XCD-local)."""
     bdir = os.path.join(ROOT, "triton-rs_amd", "_build")
     gemv_o, strided_o = os.path.join(bdir, "kernels_gemv.o"), os.path.join(bdir, "kernels_strided.o")
     if not (os.path.exists(gemv_o) and os.path.exists(strided_o)):
         pytest.skip("build objects not present (run build first)")
     kernels = _disassemble_tu(gemv_o, tmp_path)
     gemv = {k: v for k, v in kernels.items() if "gemv_" in k and "mfma" not in k
-            and "probe" not in k}
-    gemv_mc = {k: v for k, v in kernels.items() if "gemv_awq_mfma_kernel" in k}
+            and "rows" not in k and "probe" not in k}
+    gemv_mc = {k: v for k, v in kernels.items() if "gemv_awq_mfma_kernel" in k
+               or "gemv_awq_rows_kernel" in k}
     strided = {k: v for k, v in _disassemble_tu(strided_o, tmp_path).items()
                if "strided_gemm_kernel" in k}
     assert len(gemv) >= 24 and len(gemv_mc) >= 8 and len(strided) == 3

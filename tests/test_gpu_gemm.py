@@ -53,6 +53,20 @@ def test_gemv_small(torch_cuda, orc, fmt, M):
     assert_parity(y, _oracle(orc, p), what=f"gemv fmt={fmt} M={M}")
 
 
+@pytest.mark.parametrize("M", [3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("K,N,G", [(1024, 256, 128), (3072, 768, 256), (2048, 1280, 1024)])
+def test_gemv_awq_row_paired(torch_cuda, orc, M, K, N, G):
+    """AWQ at M = 3..8 on the row-paired matrix-core kernel (K a multiple of 1024, groups of
+    128 rows or more, N a multiple of 256): one split (K=1024), three (fixed-point hand-off
+    at M <= 4, counter protocol above) and two with one group per split."""
+    p = Problem(AWQ, M=M, K=K, N=N, G=G, seed=5100 + 10 * M + K // 1024)
+    assert pkg().plan("awq", M, N, K, G) == "gemv"
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"awq rows M={M} K={K} N={N} G={G}")
+    # repeated calls are bit-identical (split order fixed; hand-off state left clean)
+    assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
+
+
 @pytest.mark.parametrize("fmt", [GPTQ, SYM])
 @pytest.mark.parametrize("M,K,N", [(2, 1024, 192), (4, 2048, 320), (3, 768, 256), (2, 256, 128)])
 def test_gemv_gptq_tile_widths(torch_cuda, orc, fmt, M, K, N):

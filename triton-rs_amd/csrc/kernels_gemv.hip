@@ -566,6 +566,175 @@ gemv_awq_mfma_kernel(GemvParams p) {
     }
 }
 
+// ------------------------------------------------------------------ AWQ, M = 3..8: matrix cores, row-paired B
+
+// The kernel above makes the MFMA contraction index (row, nibble class), so its A operand
+// carries x block-diagonally and one MFMA does 1/8 useful work; at M = 8 the matrix cores
+// are its bottleneck. Here B holds 8 consecutive rows of one column, as a GEMM wants: the
+// bytes of two AWQ words (rows 2i, 2i+1) are paired with v_perm_b32 and each v_and_or_b32
+// (0x6400 exponent) yields the fp16 pair (1024 + q[2i][slot], 1024 + q[2i+1][slot]) (or
+// 1024 + 16 q for the odd slots, left in place), so per 16 weights: 2 perms, 2 shifts, 8
+// and_or. A is x itself (rows 0..M-1 of the 16; higher rows repeat row M-1 and their D rows
+// are never stored), so one MFMA does M/16 useful work. Zero point and scale are applied
+// once per wave, as in the VALU kernel: s * ((D - 1024 X) / c - z X).
+//
+// Tile: 256 columns (32 words) x 128 W rows; wave w owns rows 128 w .. 128 w + 127 (one
+// quantisation group: G % 128 == 0). Lane (jw, kg) = (lane % 16, lane / 16) loads words
+// 2 jw, 2 jw + 1 (one 64-bit load) of rows 32 b + 8 kg + i, b = 0..3, i = 0..7: all 32 loads
+// of the wave in flight at once. MFMA (c, s), c = word of the pair, s = slot: B lane (jw,
+// kg) = rows 8 kg .. 8 kg + 7 of block b, column of word 2 jw + c in slot s; A lane (m, kg) =
+// x[min(m, M - 1)][rows 8 kg .. 8 kg + 7 of block b]. D lane (jw, kg) holds rows 4 kg + i.
+// Measured against gemv_awq_mfma_kernel (graph replays, 20 rotated weight sets): K=4096 ->
+// N=14336 M=3/4/5/8: 10.9/10.3/13.3/14.4 -> 9.4/9.7/10.8/11.3 us; K=14336 -> N=4096 M=4/8:
+// 10.2/15.6 -> 9.7/12.4 us; at M = 2 (8.4 vs 9.0 us) and M = 1 the other kernels stay.
+template <int M, int W, bool FIX>
+__global__ void __launch_bounds__(64 * W)
+gemv_awq_rows_kernel(GemvParams p) {
+    constexpr int C = 256;
+    constexpr int SC = SCOPE_DEVICE;
+    static_assert(64 * W <= FINISH_MAX_THREADS, "split-K finish buffer");
+    __shared__ float red[W][M][C];
+    __shared__ int flag;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int jw = lane & 15, kg = lane >> 4;
+    const int ct = blockIdx.x, split = blockIdx.y;
+    const int NW = p.N >> 3;
+    const int r0 = (split * W + wave) * 128;       // first row of the wave
+    const int g = r0 / p.G;
+
+    // ---- x of the wave's rows for A row min(jw, M - 1), then the 32 weight loads, then the
+    // group's scales and zero words (loads complete in issue order)
+    const int mx = min(jw, M - 1);
+    u32x4 xv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+        xv[b] = *reinterpret_cast<const u32x4*>(p.x + (size_t)mx * p.K + r0 + 32 * b + 8 * kg);
+    const bufrsrc_t wr = make_rsrc(p.qweight, (uint32_t)((size_t)p.K * p.N / 2));
+    const uint32_t voff = ((uint32_t)(8 * kg) * (uint32_t)NW + (uint32_t)(ct * 32 + 2 * jw)) * 4u;
+    const uint32_t row_bytes = (uint32_t)NW * 4u;
+    u32x2 w[4][8];
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            w[b][i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                          wr, voff, (uint32_t)(r0 + 32 * b + i) * row_bytes, 2));
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t qz[2];
+    u32x4 sv[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        const int word = ct * 32 + 2 * jw + c;
+        qz[c] = __builtin_nontemporal_load(p.qzeros + (size_t)g * NW + word);
+        sv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.scales + (size_t)g * p.N + 8 * word));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- main loop: 16 MFMAs per 32 rows
+    float4_t acc[2][8];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) acc[c][s] = float4_t{0.f, 0.f, 0.f, 0.f};
+    float xs = 0.f;
+    const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const half8_t xa = __builtin_bit_cast(half8_t, xv[b]);
+        xs = dot2(as_h2(xv[b].x), one2, xs); xs = dot2(as_h2(xv[b].y), one2, xs);
+        xs = dot2(as_h2(xv[b].z), one2, xs); xs = dot2(as_h2(xv[b].w), one2, xs);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            uint32_t h[4][8];
+#pragma unroll
+            for (int i2 = 0; i2 < 4; ++i2) {
+                const uint32_t a = c ? w[b][2 * i2].y : w[b][2 * i2].x;
+                const uint32_t bb = c ? w[b][2 * i2 + 1].y : w[b][2 * i2 + 1].x;
+                // bytes {a0, a1, b0, b1} and {a2, a3, b2, b3}: slots 0-3 / 4-7 of the two rows
+                const uint32_t lo = perm(bb, a, 0x05040100u), hi = perm(bb, a, 0x07060302u);
+                const uint32_t lo8 = lo >> 8, hi8 = hi >> 8;
+                h[i2][0] = as_u32(nib_pair(lo));   h[i2][1] = as_u32(nib_pair16(lo));
+                h[i2][2] = as_u32(nib_pair(lo8));  h[i2][3] = as_u32(nib_pair16(lo8));
+                h[i2][4] = as_u32(nib_pair(hi));   h[i2][5] = as_u32(nib_pair16(hi));
+                h[i2][6] = as_u32(nib_pair(hi8));  h[i2][7] = as_u32(nib_pair16(hi8));
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const u32x4 bv = {h[0][s], h[1][s], h[2][s], h[3][s]};
+                acc[c][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, __builtin_bit_cast(half8_t, bv), acc[c][s], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- X[m] = sum of x over the wave's rows for m = lane % 16, then for the lane's D rows
+    xs += __shfl_xor(xs, 16);
+    xs += __shfl_xor(xs, 32);
+    float Xr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) Xr[i] = __shfl(xs, 4 * kg + i);
+    // ---- zero point and scale; D row 4 kg + i, column of word 2 jw + c in slot s
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * kg + i;
+        if (m >= M) continue;
+        const float X = Xr[i], X1024 = 1024.0f * Xr[i];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const half_t* sh = reinterpret_cast<const half_t*>(&sv[c]);
+            float col[8];
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                const int n = awq_col_of_slot(s);
+                const float z = (float)nib(qz[c], s);
+                // odd slots were unpacked as 1024 + 16 q
+                const float u = (s & 1) ? __builtin_fmaf(acc[c][s][i] - X1024, 1.0f / 16.0f, -z * X)
+                                        : acc[c][s][i] - X1024 - z * X;
+                col[n] = (float)sh[n] * u;
+            }
+            float4* dst = reinterpret_cast<float4*>(&red[wave][m][8 * (2 * jw + c)]);
+            dst[0] = make_float4(col[0], col[1], col[2], col[3]);
+            dst[1] = make_float4(col[4], col[5], col[6], col[7]);
+        }
+    }
+    __syncthreads();
+
+    // ---- reduce over waves; split-K hand-off
+    const int n0 = ct * C;
+    if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
+        constexpr int T = 64 * W, E = (M * C + T - 1) / T;
+        size_t off[E];
+        float v[E];
+        int n = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            const int i = (int)threadIdx.x + e * T;
+            if (i >= M * C) break;
+            const int m = i / C, cidx = i - m * C;
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < W; ++r) s += red[r][m][cidx];
+            off[e] = (size_t)m * p.N + n0 + cidx;
+            v[e] = s;
+            n = e + 1;
+        }
+        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+    } else {
+        for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
+            const int m = i / C, cidx = i - m * C;
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < W; ++r) s += red[r][m][cidx];
+            const size_t off = (size_t)m * p.N + n0 + cidx;
+            if (p.splits == 1) p.out[off] = (half_t)s;
+            else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
+        }
+        if (p.splits == 1) return;
+        if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
+            splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+    }
+}
+
 // ------------------------------------------------------------------ host launchers
 
 namespace {
@@ -598,18 +767,28 @@ constexpr int AM_CW = 2, AM_PF = 16;
 constexpr int AM_R = 64, AM_WAVES = 4;
 constexpr int AMW_R = 128, AMW_WAVES = 8;
 constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R * AMW_WAVES;
+// AWQ, M = 3..8, row-paired matrix-core kernel: 8 waves x 128 rows per workgroup
+constexpr int AR_MIN_M = 3, AR_WAVES = 8, AR_ROWS = 128 * AR_WAVES;
 }  // namespace
 
 GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     GemvShape s{};
-    // AWQ: matrix-core dot for M = 2..8 (M = 2: 10.3 vs 11.4 us, M = 4: 12.0 vs 14.5 us at
-    // K=4096, N=14336), VALU dot2 at M = 1 (with the 512-row tile and the fixed-point
+    // AWQ: the row-paired matrix-core kernel for M = 3..8 where its tile fits (K a multiple of
+    // 1024, groups of 128 rows or more); the block-diagonal matrix-core kernel for M = 2 and
+    // for other shapes (M = 2: 10.3 vs 11.4 us, M = 4: 12.0 vs 14.5 us at K=4096, N=14336
+    // against the VALU kernel), VALU dot2 at M = 1 (with the 512-row tile and the fixed-point
     // hand-off: 14336 -> 4096 8.40 vs 8.65 us, 8192 -> 4096 6.25 vs 7.70 us, 4096 -> 14336
     // 8.47 vs 9.20 us against the matrix-core kernel) and for shapes the matrix-core tile
     // rejects
     const bool mfma_fits = N % AM_COLS == 0 && K % AM_ROWS == 0 && G % AM_R == 0 && K % G == 0;
     const bool wide_fits = mfma_fits && K % AMW_ROWS == 0 && G % AMW_R == 0;
-    if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
+    const bool rows_fits = N % 256 == 0 && K % AR_ROWS == 0 && G % 128 == 0 && K % G == 0 &&
+                           (size_t)K * N / 2 < ((size_t)1 << 31);
+    if (fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
+        s.ok = true; s.mfma = true; s.awq_rows = true; s.col_tiles = N / 256;
+        s.splits = K / AR_ROWS;
+        s.threads = 64 * AR_WAVES;
+    } else if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
         s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
         s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
@@ -653,6 +832,12 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     const dim3 block(s.threads);
     if (fmt == FMT_AWQ && s.mfma) {
+        if constexpr (M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
+            if (s.awq_rows) {
+                hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX>), grid, block, 0, st, p);
+                return;
+            }
+        }
         if constexpr (M <= GEMV_MFMA_MAX_M) {
             if (s.mfma_wide)
                 hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AMW_R, AMW_WAVES, AM_PF, XCD, FIX>), grid, block, 0, st, p);

@@ -47,6 +47,7 @@ struct GemvShape {
     bool ok;
     bool mfma;              // AWQ matrix-core kernel (else VALU dot products)
     bool mfma_wide;         // its 8-wave, 1024-row tile (else 4 waves, 256 rows)
+    bool awq_rows;          // AWQ matrix-core kernel with row-paired B operands (M >= 3)
     bool gptq_deep;         // GPTQ at M = 1: 8 packed rows per lane (512 k per workgroup)
     bool gptq_narrow;       // GPTQ at M >= 2: 64-column tile (16 lanes per packed row)
     bool awq_deep;          // AWQ VALU kernel at M = 1: 8 waves, 512 rows per workgroup
