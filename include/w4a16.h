@@ -100,7 +100,7 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same arguments, kernels and
  * results as w4a16_gemm, but the split-K scratch (counters, fixed-point hand-off slots,
  * fp32 partials) lives in a fixed device array of w4a16_gemm_noalloc_scratch_bytes() bytes
- * (8 MiB: at most 1024 split-K tiles and 7 MiB of partials), one per device, held until the
+ * (8 MiB: at most 1024 split-K tiles and 6.9 MiB of partials), one per device, held until the
  * process ends; the call itself allocates nothing. Requests beyond those limits fail with
  * W4A16_ERR_UNSUPPORTED (a prefill whose K split would exceed them runs unsplit instead).
  * All calls on one device share its array: calls that overlap in time on one device (other

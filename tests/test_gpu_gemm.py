@@ -57,8 +57,9 @@ def test_gemv_small(torch_cuda, orc, fmt, M):
 @pytest.mark.parametrize("K,N,G", [(1024, 256, 128), (3072, 768, 256), (2048, 1280, 1024)])
 def test_gemv_awq_row_paired(torch_cuda, orc, M, K, N, G):
     """AWQ at M = 3..8 on the row-paired matrix-core kernel (K a multiple of 1024, groups of
-    128 rows or more, N a multiple of 256): one split (K=1024), three (fixed-point hand-off
-    at M <= 4, counter protocol above) and two with one group per split."""
+    128 rows or more, N a multiple of 256): one split (K=1024), three and two with one group
+    per split, all with the fixed-point hand-off (M * N within its 73728 entries; the counter
+    protocol of larger outputs is covered by test_gemv_split_k_counter_protocol)."""
     p = Problem(AWQ, M=M, K=K, N=N, G=G, seed=5100 + 10 * M + K // 1024)
     assert pkg().plan("awq", M, N, K, G) == "gemv"
     y = _run_gemm(torch_cuda, p)
@@ -122,23 +123,29 @@ def test_gemv_deterministic_and_reusable(torch_cuda, orc):
     assert_parity(ys[0], _oracle(orc, p))
 
 
-@pytest.mark.parametrize("fmt,M", [(AWQ, 1), (GPTQ, 1), (SYM, 1), (GPTQ, 3), (SYM, 4),
-                                   (AWQ, 2), (AWQ, 4), (AWQ, 8)])
-def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
+@pytest.mark.parametrize("fmt,M,K,N,hi,lo",
+                         [(AWQ, 1, 2048, 16384, 16, -8), (GPTQ, 1, 2048, 16384, 16, -8),
+                          (SYM, 1, 2048, 16384, 16, -8), (GPTQ, 3, 2048, 2048, 16, -8),
+                          (SYM, 4, 2048, 2048, 16, -8), (AWQ, 2, 2048, 2048, 16, -8),
+                          (AWQ, 4, 2048, 2048, 16, -8), (AWQ, 8, 2048, 2048, 16, -8),
+                          (AWQ, 1, 2048, 4096, 32, -24), (GPTQ, 1, 2048, 4096, 32, -24),
+                          (SYM, 1, 2048, 4096, 32, -24)])
+def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M, K, N, hi, lo):
     """Split-K partials of magnitude >= 2^15 leave the fixed-point hand-off for its fp32
     path (partial stored, split bit set, added in split order by the last arrival).
 
-    Exact arithmetic, so the output must equal the oracle bit for bit: x[m, k] is 16 * 2^-m
-    on the first half of K and -8 * 2^-m on the second, every scale is 0.5 and q and the
+    Exact arithmetic, so the output must equal the oracle bit for bit: x[m, k] is hi * 2^-m
+    on the first half of K and lo * 2^-m on the second, every scale is 0.5 and q and the
     zero point are constant down each column, so every product, partial sum and output is
-    a small multiple of a power of two. Each split covers 512 rows (VALU kernels: partial
-    4096 c for row 0 in the first half, c = q - z, so >= 2^15 exactly when |c| >= 8; two such
-    splits per entry) or 1024 rows (AWQ matrix-core kernel at M >= 2: 8192 c, |c| >= 4):
-    entries of both kinds in every call. At M = 1, N = 16384 keeps the 512-row tiles (the
-    GEMVs take 256-row tiles for grids this K leaves small)."""
-    K, N = 2048, (16384 if M == 1 else 2048)
-    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=4242 + 10 * fmt + M)
-    g = np.random.default_rng(4243 + 10 * fmt + M)
+    a small multiple of a power of two. With hi = 16, each split covers 512 rows (VALU
+    kernels: partial 4096 c for row 0 in the first half, c = q - z, so >= 2^15 exactly when
+    |c| >= 8; two such splits per entry) or 1024 rows (AWQ matrix-core kernels at M >= 2:
+    8192 c, |c| >= 4): entries of both kinds in every call; at M = 1, N = 16384 keeps the
+    512-row tiles. K=2048, N=4096 at M = 1 leaves grids small enough for the 256-row tiles
+    (8 splits): hi = 32 gives first-half partials of 4096 c (|c| >= 8) and lo = -24
+    second-half partials of -3072 c (|c| >= 11), with outputs 4096 c inside the fp16 range."""
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=4242 + 10 * fmt + M + N)
+    g = np.random.default_rng(4243 + 10 * fmt + M + N)
     col_q = g.integers(0, 16, size=N)
     col_z = g.integers(0, 15, size=N)              # GPTQ zero = nibble + 1 stays <= 15
     p.q = np.broadcast_to(col_q, (K, N)).astype(np.int32)
@@ -150,7 +157,7 @@ def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M):
         p.qweight = synth.pack_gptq_qweight(p.q)
         p.qzeros = synth.pack_along_n(p.zq, awq=False) if fmt == GPTQ else None
     p.scales = np.full((K // 128, N), 0.5, dtype=np.float16)
-    half = np.where(np.arange(K) < K // 2, 16.0, -8.0)
+    half = np.where(np.arange(K) < K // 2, float(hi), float(lo))
     p.x = (half[None, :] * (2.0 ** -np.arange(M))[:, None]).astype(np.float16)
     c = col_q - p.zero_int()[0]
     assert np.any(np.abs(c) >= 8) and np.any(np.abs(c) < 4)
@@ -177,10 +184,12 @@ def test_gemv_awq_m1_tiles(torch_cuda, orc, K, N):
 
 
 @pytest.mark.parametrize("fmt,M,K,N", [(SYM, 1, 16384, 256), (AWQ, 1, 16384, 512),
-                                       (AWQ, 8, 1024, 8448), (AWQ, 8, 4096, 14336)])
+                                       (AWQ, 8, 2048, 9472), (AWQ, 8, 4096, 14336),
+                                       (AWQ, 6, 2048, 14336)])
 def test_gemv_split_k_counter_protocol(torch_cuda, orc, fmt, M, K, N):
-    """Shapes past the fixed-point hand-off's limits (32 splits; M > 4; M * N > 65536 entries)
-    keep the per-tile counter protocol: parity and repeatability."""
+    """Shapes past the fixed-point hand-off's limits (32 splits; more than 73728 entries
+    M * N on the row-paired AWQ kernel) keep the per-tile counter protocol: parity and
+    repeatability."""
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=555 + M)
     assert pkg().plan(FMT_NAME[fmt], M, N, K, 128) == "gemv"
     y = _run_gemm(torch_cuda, p)

@@ -349,7 +349,10 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
             p.counters = sc.counters;
             p.ws = sc.partials;
             // every GEMV kernel takes the fixed-point hand-off where its limits allow
-            p.fixed = s.splits <= FIX_MAX_SPLITS && M <= FIX_MAX_M && (size_t)M * N <= FIX_MAX_ENTRIES;
+            const size_t entries = (size_t)M * N;
+            p.fixed = s.splits <= FIX_MAX_SPLITS &&
+                      ((M <= FIX_MAX_M && entries <= FIX_VALU_MAX_ENTRIES) ||
+                       (s.awq_rows && entries <= FIX_MAX_ENTRIES));
             p.slots = sc.slots;
             p.masks = sc.masks;
         }

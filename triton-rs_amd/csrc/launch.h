@@ -19,14 +19,19 @@ constexpr size_t SPLITK_FLAG_BYTES = 2u << 20;
 constexpr size_t SPLITK_MAX_TILES = SPLITK_FLAG_BYTES / (FLAG_STRIDE * sizeof(uint32_t));
 // Fixed-point split-K hand-off (splitk.h, splitk_fixed_commit): after the counters, one
 // 64-bit slot word per output entry, then one 32-bit split mask per entry, all zero between
-// calls. Used when splits <= FIX_MAX_SPLITS, M <= FIX_MAX_M and M * N <= FIX_MAX_ENTRIES:
-// with more entries the atomics cost more than the counter protocol's reload (AWQ M = 8,
-// 4096 -> 14336, four splits: 14.5 us with the counter, 15.3 us fixed-point), and at M = 8
-// the fixed-point time varied with the weight data (14336 -> 4096: 15.3 to 18.2 us across
-// seeds, no partial near the fp32 path's range; the counter protocol 15.8 us for both).
+// calls (room for FIX_MAX_ENTRIES entries). Used when splits <= FIX_MAX_SPLITS and either
+// M <= FIX_MAX_M and M * N <= FIX_VALU_MAX_ENTRIES, or the kernel is the row-paired AWQ one
+// (M = 3..8) and M * N <= FIX_MAX_ENTRIES. With more entries the atomics cost more than the
+// counter protocol's reload: AWQ M = 8, 4096 -> 14336, four splits: 14.5 us with the counter,
+// 15.3 us fixed-point on the column-interleaved kernel (whose time also varied with the
+// weight data at M = 8, 15.3 to 18.2 us across seeds, so it keeps the counter above M = 4);
+// on the row-paired kernel (graph replays, 20 rotated weight sets) M = 5 at N = 14336
+// (71,680 entries) 10.84 -> 10.17 us, M = 6 (86,016) 10.94 vs 10.99, M = 8 (114,688)
+// 11.27 -> 11.87; at N = 4096 M = 5 / 6 / 8 11.37 / 11.67 / 12.31 -> 10.45 / 11.25 / 12.29.
 constexpr int FIX_MAX_SPLITS = 31;
 constexpr int FIX_MAX_M = 4;
-constexpr size_t FIX_MAX_ENTRIES = 65536;
+constexpr size_t FIX_VALU_MAX_ENTRIES = 65536;
+constexpr size_t FIX_MAX_ENTRIES = 73728;
 constexpr size_t FIX_SLOT_BYTES = FIX_MAX_ENTRIES * (sizeof(uint64_t) + sizeof(uint32_t));
 
 struct GemvParams {

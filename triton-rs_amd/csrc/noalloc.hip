@@ -25,9 +25,9 @@ namespace w4a16 {
 //   then NA_PARTIAL_BYTES of fp32 partials
 constexpr size_t NA_MAX_TILES = 1024;
 constexpr size_t NA_COUNTER_BYTES = NA_MAX_TILES * FLAG_STRIDE * sizeof(uint32_t);   // 256 KiB
-constexpr size_t NA_ZERO_BYTES = NA_COUNTER_BYTES + FIX_SLOT_BYTES;                  // 1 MiB
+constexpr size_t NA_ZERO_BYTES = NA_COUNTER_BYTES + FIX_SLOT_BYTES;                  // 1.09 MiB
 constexpr size_t NA_SCRATCH_BYTES = 8u << 20;
-constexpr size_t NA_PARTIAL_BYTES = NA_SCRATCH_BYTES - NA_ZERO_BYTES;               // 7 MiB
+constexpr size_t NA_PARTIAL_BYTES = NA_SCRATCH_BYTES - NA_ZERO_BYTES;               // 6.9 MiB
 static_assert(NA_ZERO_BYTES % 256 == 0, "partials stay 256-byte aligned");
 
 static __device__ __align__(256) unsigned char scratch[NA_SCRATCH_BYTES];
