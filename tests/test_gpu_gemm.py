@@ -339,9 +339,15 @@ def test_act_order_config2_full_size(torch_cuda, orc, M):
 
 
 @pytest.mark.parametrize("fmt,M,K,N,G,zo", [(SYM, 8, 2048, 512, 128, 1), (GPTQ, 1, 1024, 256, 64, 0),
-                                            (GPTQ, 40, 1408, 640, 128, 1), (GPTQ, 5, 512, 64, 32, 1)])
+                                            (GPTQ, 40, 1408, 640, 128, 1), (GPTQ, 5, 512, 64, 32, 1),
+                                            (GPTQ, 16, 8192, 256, 32, 1), (SYM, 32, 2048, 512, 32, 1),
+                                            (GPTQ, 33, 16384, 3072, 256, 0)])
 def test_act_order_shapes(torch_cuda, orc, fmt, M, K, N, G, zo):
-    """Act-order over formats, zero offsets, group sizes, strip widths and split counts."""
+    """Act-order over formats, zero offsets, group sizes, strip widths and split counts.
+    K=8192 with G=32 fills the LDS budget with the group table (256 groups), so g_idx is
+    read from global memory per step and the table is built after the weight stream is
+    issued; the other shapes stage the workgroup's g_idx slice in LDS, K=16384 over two
+    splits (8192 rows per workgroup) with the slice loaded after the weight stream."""
     p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1310 + M, act_order=True, zero_offset=zo)
     assert pkg().plan(FMT_NAME[fmt], M, N, K, G, has_g_idx=True) == "skinny"
     y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)

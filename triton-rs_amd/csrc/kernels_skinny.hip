@@ -23,6 +23,9 @@
 // for every group and every column of its strip, the scale and the zero (as fp16 1024 + z)
 // in one 32-bit entry; each k row then gathers its entries by g_idx[k]. The arithmetic per
 // weight is unchanged, (fp16(1024 + q) - fp16(1024 + z)) * s, so the weights stay bit-exact.
+// GIDX = 2 also stages the workgroup's slice of g_idx in LDS (one load per thread instead of
+// two 32-byte loads per lane and k32 step, which the 16 lanes of a k block all repeat);
+// GIDX = 1 (slice too large for the LDS budget) reads g_idx per step from global memory.
 #include "device_common.h"
 #include "launch.h"
 #include "splitk.h"
@@ -46,7 +49,7 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 
 // SPW: k32 steps per wave when known at compile time (SPW = PF: the prologue issues every
 // step and no loop is emitted), 0 for the runtime count p.steps_per_wave
-template <int FMT, int BM, int CPL, int PF, bool GIDX, bool XCD, int SPW>
+template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW>
 __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel(SkinnyParams p) {
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
@@ -60,7 +63,9 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
 
     __shared__ float red[W][BM][WN + 1];
     __shared__ int flag;
-    extern __shared__ uint32_t gtab[];   // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16)
+    // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16), then (GIDX = 2) the g_idx of the
+    // workgroup's W * spw * 32 rows
+    extern __shared__ uint32_t gtab[];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kb = lane >> 4;
@@ -77,7 +82,8 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
     uint32_t bw[PF][WPS];
     u32x4 areg[PF][RB];
     uint32_t sreg[PF][SW], zreg[PF];
-    int32_t greg[PF][GIDX ? 8 : 1];
+    int32_t greg[PF][GIDX == 1 ? 8 : 1];
+    int goff[PF];   // GIDX = 2: offset of the lane's 8 rows in the LDS g_idx slice
 
     auto issue = [&](int u, int step) {
         const int kg = 32 * step;
@@ -109,7 +115,10 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
             const int m = min(16 * r + j, p.M - 1);
             areg[u][r] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.K + kg + 8 * kb);
         }
-        if constexpr (GIDX) {
+        if constexpr (GIDX == 2) {
+            goff[u] = (step - split * W * spw) * 32 + 8 * kb;
+            return;
+        } else if constexpr (GIDX == 1) {
             // groups of the lane's 8 k rows
             const u32x4* gp = reinterpret_cast<const u32x4*>(p.g_idx + kg + 8 * kb);
             const u32x4 g0 = gp[0], g1 = gp[1];
@@ -138,31 +147,56 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
 #pragma unroll
         for (int c = 0; c < CPL; ++c) acc[r][c] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Act-order table: entry o = (group o / WN, strip column o % WN). Loads of one wave
-    // complete in issue order, so where the table fits TE entries per thread its scales and
-    // zeros are loaded into registers before the weight stream and written to LDS after it
-    // has been issued; the table is then ready about when the first weights arrive (loaded
-    // after the stream, its build waited for all of it: config 2 M=16 12.5 -> 10.9 us).
+    // Act-order table: entry (g, c) = group g, strip column c at gtab[g * WN + c]. Thread work
+    // comes in chunks of 8 columns of one group: one 16-byte load of their scales and one zero
+    // word. Loads of one wave complete in issue order, so where the chunks fit TC per thread
+    // they are loaded into registers before the weight stream and written to LDS after it has
+    // been issued; the table is then ready about when the first weights arrive (loaded after
+    // the stream, its build waited for all of it: config 2 M=16 12.5 -> 10.9 us). The g_idx
+    // slice of GIDX = 2 is loaded the same way, 4 rows per load.
     const int ngroups = (p.K + p.G - 1) / p.G;
-    constexpr int TE = GIDX ? 8 : 1;
-    const int tab_n = GIDX ? ngroups * WN : 0;
-    const bool tab_early = GIDX && tab_n <= TE * NT;
-    uint32_t tsc[TE], tzw[TE];
-    auto tab_entry = [&](uint32_t sc, uint32_t zw, int o) -> uint32_t {
-        const int g = o / WN, n = n0 + (o - g * WN);
-        const int z = (FMT == FMT_GPTQ_SYM) ? 8 : nib(zw, n & 7) + p.zero_offset;
-        const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
-        return sc | (zf << 16);
+    constexpr int CPW = WN / 8;                       // chunks per group
+    constexpr int TC = GIDX ? 2 : 1;
+    constexpr int GC = GIDX == 2 ? 4 : 1;
+    const int tab_chunks = GIDX ? ngroups * CPW : 0;
+    const int tab_n = ngroups * WN;
+    const bool tab_early = GIDX && tab_chunks <= TC * NT;
+    const int gsl_rows = GIDX == 2 ? W * spw * 32 : 0;      // rows of the workgroup
+    const int gsl_chunks = gsl_rows / 4;
+    const bool gsl_early = GIDX == 2 && gsl_chunks <= GC * NT;
+    const int32_t* gsrc = p.g_idx + (size_t)split * gsl_rows;
+    uint32_t* gsl = gtab + tab_n;
+    u32x4 tsv[TC], gsv[GC];
+    uint32_t tzv[TC];
+    auto tab_load = [&](int c, u32x4& sv, uint32_t& zw) {
+        const int g = c / CPW, b = c - g * CPW;
+        sv = *reinterpret_cast<const u32x4*>(p.scales + (size_t)g * p.N + n0 + 8 * b);
+        zw = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (n0 >> 3) + b];
     };
-    if constexpr (GIDX) {
+    auto tab_store = [&](int c, const u32x4& sv, uint32_t zw) {
+        const int g = c / CPW, b = c - g * CPW;
+        uint32_t e[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {   // column n0 + 8 b + i: nibble i of its zero word
+            const int z = (FMT == FMT_GPTQ_SYM) ? 8 : nib(zw, i) + p.zero_offset;
+            const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
+            const uint32_t sw = i < 2 ? sv.x : i < 4 ? sv.y : i < 6 ? sv.z : sv.w;
+            e[i] = ((i & 1) ? (sw >> 16) : (sw & 0xFFFFu)) | (zf << 16);
+        }
+        uint32_t* dst = gtab + g * WN + 8 * b;
+        reinterpret_cast<u32x4*>(dst)[0] = u32x4{e[0], e[1], e[2], e[3]};
+        reinterpret_cast<u32x4*>(dst)[1] = u32x4{e[4], e[5], e[6], e[7]};
+    };
+    if constexpr (GIDX != 0) {
         if (tab_early) {
 #pragma unroll
-            for (int e = 0; e < TE; ++e) {
-                const int o = min((int)threadIdx.x + e * NT, tab_n - 1);   // in range: loads unconditional
-                const int g = o / WN, n = n0 + (o - g * WN);
-                tsc[e] = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
-                tzw[e] = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (n >> 3)];
-            }
+            for (int e = 0; e < TC; ++e)   // in range: loads unconditional
+                tab_load(min((int)threadIdx.x + e * NT, tab_chunks - 1), tsv[e], tzv[e]);
+        }
+        if (gsl_early) {
+#pragma unroll
+            for (int e = 0; e < GC; ++e)
+                gsv[e] = reinterpret_cast<const u32x4*>(gsrc)[min((int)threadIdx.x + e * NT, gsl_chunks - 1)];
         }
     }
 
@@ -171,19 +205,31 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
 #pragma unroll
     for (int u = 0; u < PF; ++u) issue(u, step0 + min(u, spw - 1));
 
-    if constexpr (GIDX) {
+    if constexpr (GIDX != 0) {
         if (tab_early) {
 #pragma unroll
-            for (int e = 0; e < TE; ++e) {
-                const int o = (int)threadIdx.x + e * NT;
-                if (o < tab_n) gtab[o] = tab_entry(tsc[e], tzw[e], o);
+            for (int e = 0; e < TC; ++e) {
+                const int c = (int)threadIdx.x + e * NT;
+                if (c < tab_chunks) tab_store(c, tsv[e], tzv[e]);
             }
         } else {
-            for (int o = threadIdx.x; o < tab_n; o += NT) {
-                const int g = o / WN, n = n0 + (o - g * WN);
-                const uint32_t sc = __builtin_bit_cast(uint16_t, p.scales[(size_t)g * p.N + n]);
-                const uint32_t zw = (FMT == FMT_GPTQ_SYM) ? 0u : p.qzeros[(size_t)g * NW + (n >> 3)];
-                gtab[o] = tab_entry(sc, zw, o);
+            for (int c = threadIdx.x; c < tab_chunks; c += NT) {
+                u32x4 sv;
+                uint32_t zw;
+                tab_load(c, sv, zw);
+                tab_store(c, sv, zw);
+            }
+        }
+        if constexpr (GIDX == 2) {
+            if (gsl_early) {
+#pragma unroll
+                for (int e = 0; e < GC; ++e) {
+                    const int c = (int)threadIdx.x + e * NT;
+                    if (c < gsl_chunks) reinterpret_cast<u32x4*>(gsl)[c] = gsv[e];
+                }
+            } else {
+                for (int c = threadIdx.x; c < gsl_chunks; c += NT)
+                    reinterpret_cast<u32x4*>(gsl)[c] = reinterpret_cast<const u32x4*>(gsrc)[c];
             }
         }
         __syncthreads();
@@ -194,7 +240,7 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
         // zero point (as fp16 1024 + z) and scale per column, splatted
         half2_t hz[CPL], hs[CPL];
 #pragma unroll
-        for (int c = 0; c < (GIDX ? 0 : CPL); ++c) {
+        for (int c = 0; c < (GIDX != 0 ? 0 : CPL); ++c) {
             const int cw = (nl & 7) + c;   // column within its qzeros word
             int z;
             if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
@@ -235,13 +281,23 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
             }
 #pragma unroll
             for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
-        } else if constexpr (GIDX) {
+        } else if constexpr (GIDX != 0) {
             // entries of rows k0..k7 for the lane's columns; a g_idx outside the table
             // is clamped into [0, groups - 1], as in the generic kernel
+            int32_t gv[8];
+            if constexpr (GIDX == 2) {
+                const u32x4* gp = reinterpret_cast<const u32x4*>(gsl + goff[u]);
+                const u32x4 g0 = gp[0], g1 = gp[1];
+                gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
+                gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) gv[i] = greg[u][i];
+            }
             uint32_t t[8][CPL];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t g = (uint32_t)min(max(greg[u][i], 0), ngroups - 1);
+                const uint32_t g = (uint32_t)min(max(gv[i], 0), ngroups - 1);
                 const uint32_t* row = gtab + g * WN + CPL * j;
                 if constexpr (CPL == 2) {
                     const u32x2 v = *reinterpret_cast<const u32x2*>(row);
@@ -394,6 +450,11 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     const int splits = quads >= wq ? quads / wq : 1;
     s.splits = splits;
     s.steps_per_wave = K / (32 * skinny_waves(fmt, s.bm, cpl) * splits);
+    // act-order: the workgroup's g_idx slice joins the table in LDS where the budget allows
+    if (gidx && s.lds + (size_t)(K / splits) * sizeof(int32_t) <= SKINNY_GIDX_MAX_LDS) {
+        s.gidx_lds = true;
+        s.lds += (size_t)(K / splits) * sizeof(int32_t);
+    }
     s.xcd = xcd_placement && splits > 1 && s.col_tiles % 8 == 0;
     s.ok = true;
     return s;
@@ -416,17 +477,21 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
                 hipLaunchKernelGGL(kern, grid, dim3(64 * skinny_waves(FMT, BM, CPL)), s.lds, st, p);
                 return hipGetLastError();
             };
-            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, true, XCD, PF>);
-            return go(&skinny_kernel<FMT, BM, CPL, PF, true, XCD, 0>);
+            if (s.gidx_lds) {
+                if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, PF>);
+                return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, 0>);
+            }
+            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, PF>);
+            return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, 0>);
         }
     }
     if constexpr (FMT != FMT_AWQ) {
         if (s.steps_per_wave == PF) {   // as above: M=16, 4096 -> 6144 9.4 -> 8.6 us
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, false, XCD, 0>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
     return hipGetLastError();
 }
 

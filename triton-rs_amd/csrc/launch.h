@@ -147,8 +147,9 @@ struct SkinnyParams {
 struct SkinnyShape {
     bool ok;
     bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
+    bool gidx_lds;          // act-order: the workgroup's g_idx slice staged in LDS too
     int bm, cpl, col_tiles, splits, steps_per_wave;
-    size_t lds;             // dynamic LDS bytes (act-order group table)
+    size_t lds;             // dynamic LDS bytes (act-order group table, g_idx slice)
 };
 
 // Largest act-order group table a workgroup stages in LDS.
