@@ -56,8 +56,9 @@ def heavy_tailed_x(g, M, K, n_out=6, mag=300.0, shift=4.0):
     (SYM, 1, 4096, 4096),       # config 0 (GPTQ symmetric GEMV)
     (AWQ, 1, 4096, 14336),      # config 1, M = 1 (VALU GEMV, 512-row tiles)
     (AWQ, 1, 14336, 4096),
-    (AWQ, 4, 4096, 14336),      # matrix-core GEMV, fixed-point hand-off
-    (AWQ, 8, 14336, 4096),      # matrix-core GEMV, counter hand-off
+    (AWQ, 4, 4096, 14336),      # row-paired matrix-core GEMV, fixed-point hand-off
+    (AWQ, 8, 4096, 14336),      # row-paired matrix-core GEMV, counter hand-off
+    (AWQ, 8, 14336, 4096),      # row-paired matrix-core GEMV, fixed-point hand-off
     (GPTQ, 3, 4096, 6144),      # GPTQ VALU GEMV at M > 1
     (AWQ, 1, 2048, 4096),       # 256-row tiles
 ])

@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
     __shared__ int flag;
     // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16), then (GIDX = 2) the g_idx of the
     // workgroup's W * spw * 32 rows
-    extern __shared__ uint32_t gtab[];
+    extern __shared__ __attribute__((aligned(16))) uint32_t gtab[];   // 16-byte table accesses
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int j = lane & 15, kb = lane >> 4;
