@@ -15,7 +15,8 @@ divided by the ratio that the same counter reads for a plain streaming kernel of
 size (torch's neg over 512 MiB of int32) in the same child run.
 
 Secondary figures (same line, "extra"): AWQ prefill M=2048 in both MLP shapes (TFLOP/s,
-2*M*N*K), the other decode/small-batch shapes, and the fused MoE layer of config 4.
+2*M*N*K), the other decode/small-batch shapes, one GPU's share of an 8-way tensor-parallel
+MLP (tp8_*), and the fused MoE layer of config 4.
 cpu_baseline: the CPU oracle (dequant + fp32-accumulate matmul, OpenMP) on a bounded
 sample of the same workload, timed on this host's cores.
 """
@@ -448,6 +449,14 @@ def extras(torch, pkg, dev, stream, args):
 
     gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
     gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
+
+    # one GPU's share of an 8-way tensor-parallel MLP at its real shape: gate/up split by
+    # columns (N / 8 = 1792), down split by rows (K / 8 = 1792); 150 weight sets (> 512 MB)
+    for M in (1, 8):
+        gemm_case(f"tp8_c1_awq_m{M}_k4096_n1792", "awq", M, 4096, 1792, 128, 150, 1000)
+        gemm_case(f"tp8_c1_awq_m{M}_k1792_n4096", "awq", M, 1792, 4096, 128, 150, 1000)
+    gemm_case("tp8_c3_awq_m2048_k4096_n1792", "awq", 2048, 4096, 1792, 128, 2, 300)
+    gemm_case("tp8_c3_awq_m2048_k1792_n4096", "awq", 2048, 1792, 4096, 128, 2, 300)
 
     # the reference-named typed entry point (its 19-parameter list, dense strides) at C1 / C3
     def typed_case(tag, M, K, N, n_sets, calls):

@@ -246,6 +246,26 @@ def test_prefill_full_size_sampled_rows(torch_cuda, orc, K, N):
     assert np.all(np.isfinite(y))
 
 
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 1792), (1, 1792, 4096), (8, 4096, 1792),
+                                   (8, 1792, 4096), (2048, 4096, 1792), (2048, 1792, 4096)])
+def test_tensor_parallel_shares(torch_cuda, orc, M, K, N):
+    """One GPU's share of an 8-way tensor-parallel config-1/3 MLP: the gate/up projection split
+    by columns (N = 14336 / 8) and the down projection by rows (K = 14336 / 8). M = 2048 is
+    checked on 16 sampled rows."""
+    P = pkg()
+    p = Problem(AWQ, M=M, K=K, N=N, G=128, seed=0x5EED0100 + M + K)
+    assert P.plan("awq", M, N, K, 128) == ("prefill" if M > 64 else "gemv")
+    y = _run_gemm(torch_cuda, p)
+    if M <= 8:
+        assert_parity(y, _oracle(orc, p), what=f"tp share M={M} K={K} N={N}")
+        assert np.array_equal(_run_gemm(torch_cuda, p).view(np.uint16), y.view(np.uint16))
+        return
+    rows = np.random.default_rng(5).choice(M, 16, replace=False).astype(np.int32)
+    rows[:2] = [0, M - 1]
+    ref = orc.w4a16_gemm_rows(AWQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"tp share M={M} K={K} N={N}")
+
+
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
 @pytest.mark.parametrize("M,K,N", [(300, 640, 384), (512, 1024, 128), (2048, 1024, 4096)])
 def test_prefill_narrow_tiles(torch_cuda, orc, fmt, M, K, N):

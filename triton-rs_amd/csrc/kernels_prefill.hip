@@ -709,41 +709,39 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int
     (void)fmt;
     if (M < 1 || N % 8 || K % BK || G % 8 || K % G) return s;
     if (dma_ok(N, K, G, M)) {
-        // tile minimising (rounds of tiles over the CUs) x (tile area); ties to larger BM
-        long long best = -1;
-        for (int bn : {256, 224, 128}) {
-            if (N % bn) continue;
-            for (int bm : {256, 128}) {
+        // Tile (BM x BN) and K split from a cost model fitted to graph-replay times of the
+        // pipelined kernel (AWQ, M = 2048, N = 1792 .. 14336, K = 1792 .. 14336):
+        //   rounds x BM x BN x e x K / ks  +  3.2 x ks x M x N  (ks > 1: fp32 partials)
+        // with rounds = ceil(tiles x ks / CUs) and e the relative time per unit of tile area:
+        // 1.00 for 256 x 224 and 256 x 256 tiles, 1.15 for 256 x 128 (a third more LDS operand
+        // reads per MFMA), 1.35 for 128-row tiles (half the rows per dequantised B tile). It
+        // keeps every measured choice at config 3 (4096 -> 14336: 256 x 224, 231 us; 14336 ->
+        // 4096: 256 x 256 with 2 splits, 231 us against 258 us for 256 x 128 unsplit) and fixes
+        // the grids that left CUs idle: one GPU's share of an 8-way tensor-parallel layer,
+        // M=2048, 4096 -> 1792, took 128 x 224 tiles (128 workgroups) in ~75 us, 256 x 128 with
+        // 2 splits 53 us; 4096 -> 3584 128 x 224 ~85 us, 256 x 128 73 us. A split keeps at
+        // least 8 stages of K. Ties go to larger tiles and fewer splits.
+        double best = -1.0;
+        for (int bm : {256, 128}) {
+            for (int bn : {256, 224, 128}) {
+                if (N % bn) continue;
                 if (bn == 128 && bm != 256) continue;   // 128-wide tiles only with 256 rows
+                const double e = bm == 128 ? 1.35 : bn == 128 ? 1.15 : 1.0;
                 const long long tiles = (long long)(N / bn) * ((M + bm - 1) / bm);
-                const long long cost = (tiles + num_cus - 1) / num_cus * bm * bn;
-                if (best < 0 || cost < best || (cost == best && bm > s.bm)) {
-                    best = cost; s.bm = bm; s.bn = bn;
+                for (int ks = 1; ks <= 4; ks *= 2) {
+                    if (ks > 1 && (bm != 256 || ks > max_ksplit || (K / BK) % ks || K / BK / ks < 8))
+                        break;
+                    const long long rounds = (tiles * ks + num_cus - 1) / num_cus;
+                    const double cost = (double)rounds * bm * bn * e * ((double)K / ks) +
+                                        (ks > 1 ? 3.2 * ks * (double)M * N : 0.0);
+                    if (best < 0 || cost < best * (1.0 - 1e-9)) {
+                        best = cost; s.bm = bm; s.bn = bn; s.ksplit = ks;
+                    }
                 }
             }
         }
         if (best >= 0) {
             s.dma = true;
-            s.ksplit = 1;
-            // 256 x 256 tiles with K split across workgroups, where the chosen tiles leave
-            // CUs idle or K is long: a 256 x 256 stage does twice the work of a 256 x 128
-            // one in ~1.4x the time, while the fp32 partials cost a fixed write and reread.
-            // Measured (graph replays): config 3 down (M=2048, 14336 -> 4096) 258 -> 231
-            // us with 2 splits; M=1024 on the same shape 235 -> 140 us with 4; M=512,
-            // 4096 -> 4096 68 -> 64 us; but M=2048, 4096 -> 4096 (256 tiles of 256 x 128
-            // already fill the CUs, 32 stages per split) 76 -> 85 us, so a full grid is
-            // split only from 64 stages (8192 rows of K) per split. Each split keeps at
-            // least 8 stages.
-            const long long wgs = (long long)(N / s.bn) * ((M + s.bm - 1) / s.bm);
-            if (s.bm == 256 && (s.bn == 128 || s.bn == 256) && N % 256 == 0 &&
-                (wgs < num_cus || K / BK / 2 >= 64)) {
-                const int tiles = (N / 256) * ((M + 255) / 256);
-                int ks = 1;
-                while (ks < 4 && ks * 2 <= max_ksplit && tiles * ks * 2 <= num_cus && (K / BK) % (ks * 2) == 0 &&
-                       K / BK / (ks * 2) >= 8)
-                    ks *= 2;
-                if (ks > 1) { s.bn = 256; s.ksplit = ks; }
-            }
             s.col_tiles = N / s.bn;
             s.row_tiles = (M + s.bm - 1) / s.bm;
             s.lds = prefill_dma_lds(s.bm, s.bn);
