@@ -54,12 +54,15 @@ def test_gemv_small(torch_cuda, orc, fmt, M):
 
 
 @pytest.mark.parametrize("M", [3, 4, 5, 6, 7, 8])
-@pytest.mark.parametrize("K,N,G", [(1024, 256, 128), (3072, 768, 256), (2048, 1280, 1024)])
+@pytest.mark.parametrize("K,N,G", [(1024, 256, 128), (3072, 768, 256), (2048, 1280, 1024),
+                                   (2048, 8192, 128)])
 def test_gemv_awq_row_paired(torch_cuda, orc, M, K, N, G):
     """AWQ at M = 3..8 on the row-paired matrix-core kernel (K a multiple of 1024, groups of
-    128 rows or more, N a multiple of 256): one split (K=1024), three and two with one group
-    per split, all with the fixed-point hand-off (M * N within its 73728 entries; the counter
-    protocol of larger outputs is covered by test_gemv_split_k_counter_protocol)."""
+    128 rows or more, N a multiple of 256), all with the fixed-point hand-off (M * N within its
+    73728 entries; the counter protocol of larger outputs is covered by
+    test_gemv_split_k_counter_protocol). The first three shapes leave under 64 workgroups of
+    8 waves, so they take 4-wave, 512-row workgroups (2, 6 and 4 splits; G=1024 spans two
+    workgroups); 2048 x 8192 fills 64 workgroups of 8 waves."""
     p = Problem(AWQ, M=M, K=K, N=N, G=G, seed=5100 + 10 * M + K // 1024)
     assert pkg().plan("awq", M, N, K, G) == "gemv"
     y = _run_gemm(torch_cuda, p)
@@ -138,10 +141,11 @@ def test_gemv_split_k_out_of_range_partials(torch_cuda, orc, fmt, M, K, N, hi, l
     on the first half of K and lo * 2^-m on the second, every scale is 0.5 and q and the
     zero point are constant down each column, so every product, partial sum and output is
     a small multiple of a power of two. With hi = 16, each split covers 512 rows (VALU
-    kernels: partial 4096 c for row 0 in the first half, c = q - z, so >= 2^15 exactly when
-    |c| >= 8; two such splits per entry) or 1024 rows (AWQ matrix-core kernels at M >= 2:
-    8192 c, |c| >= 4): entries of both kinds in every call; at M = 1, N = 16384 keeps the
-    512-row tiles. K=2048, N=4096 at M = 1 leaves grids small enough for the 256-row tiles
+    kernels, and the row-paired AWQ kernel's 4-wave tiles at M = 4, 8: partial 4096 c for
+    row 0 in the first half, c = q - z, so >= 2^15 exactly when |c| >= 8; two such splits per
+    entry) or 1024 rows (AWQ column-interleaved matrix-core kernel at M = 2: 8192 c,
+    |c| >= 4): entries of both kinds in every call; at M = 1, N = 16384 keeps the 512-row
+    tiles. K=2048, N=4096 at M = 1 leaves grids small enough for the 256-row tiles
     (8 splits): hi = 32 gives first-half partials of 4096 c (|c| >= 8) and lo = -24
     second-half partials of -3072 c (|c| >= 11), with outputs 4096 c inside the fp16 range."""
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=4242 + 10 * fmt + M + N)

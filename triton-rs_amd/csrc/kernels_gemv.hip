@@ -767,7 +767,7 @@ constexpr int AM_CW = 2, AM_PF = 16;
 constexpr int AM_R = 64, AM_WAVES = 4;
 constexpr int AMW_R = 128, AMW_WAVES = 8;
 constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R * AMW_WAVES;
-// AWQ, M = 3..8, row-paired matrix-core kernel: 8 waves x 128 rows per workgroup
+// AWQ, M = 3..8, row-paired matrix-core kernel: 8 (or 4) waves x 128 rows per workgroup
 constexpr int AR_MIN_M = 3, AR_WAVES = 8, AR_ROWS = 128 * AR_WAVES;
 }  // namespace
 
@@ -786,8 +786,12 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
                            (size_t)K * N / 2 < ((size_t)1 << 31);
     if (fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
         s.ok = true; s.mfma = true; s.awq_rows = true; s.col_tiles = N / 256;
-        s.splits = K / AR_ROWS;
-        s.threads = 64 * AR_WAVES;
+        // 4 waves (512-row workgroups) where 8 would leave fewer than 64 workgroups (graph
+        // replays, one GPU's share of an 8-way tensor-parallel layer, K=4096 -> N=1792: M=4
+        // 7.7 -> 6.6 us, M=8 9.6 -> 8.6 us; 2 waves, 16 splits, 13.8 us at M=8)
+        const int w = (N / 256) * (K / AR_ROWS) < 64 ? AR_WAVES / 2 : AR_WAVES;
+        s.splits = K / (128 * w);
+        s.threads = 64 * w;
     } else if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
         s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
         s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
@@ -834,7 +838,10 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
     if (fmt == FMT_AWQ && s.mfma) {
         if constexpr (M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
             if (s.awq_rows) {
-                hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX>), grid, block, 0, st, p);
+                if (s.threads == 64 * AR_WAVES)
+                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX>), grid, block, 0, st, p);
+                else
+                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES / 2, FIX>), grid, block, 0, st, p);
                 return;
             }
         }
