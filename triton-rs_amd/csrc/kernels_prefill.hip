@@ -764,18 +764,16 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int
 
 template <typename F>
 static void allow_lds(F* kernel, size_t lds) {
-    // dynamic LDS above 64 KiB must be allowed once per kernel
+    // dynamic LDS above 64 KiB must be allowed for the kernel before it is launched
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
 }
 
+// The dynamic-LDS allowance is set on every launch (a host-side attribute, cheap beside these
+// kernels): once per process would miss other devices and race between host threads.
 template <int FMT, int BM, int BN2, bool MOE>
 static void launch_dma_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t st) {
-    static bool attr_set = false;
-    if (!attr_set) {
-        allow_lds(&prefill_dma_kernel<FMT, BM, BN2, MOE>, prefill_dma_lds(BM, BN2));
-        attr_set = true;
-    }
+    allow_lds(&prefill_dma_kernel<FMT, BM, BN2, MOE>, prefill_dma_lds(BM, BN2));
     hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, MOE>), grid, dim3(PF_THREADS), lds, st, p);
 }
 
@@ -817,12 +815,7 @@ static void launch_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t 
     // stages of loads in flight: deeper rings do not fit beside the accumulators (they end
     // up in AGPRs and every use pays an AGPR->VGPR copy)
     constexpr int D = 1;
-    static bool attr_set = false;   // dynamic LDS above 64 KiB must be allowed once
-    if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_kernel<FMT, BM, D, MOE>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        attr_set = true;
-    }
+    allow_lds(&prefill_kernel<FMT, BM, D, MOE>, lds);   // every launch, as above
     hipLaunchKernelGGL((prefill_kernel<FMT, BM, D, MOE>), grid, dim3(256), lds, st, p);
 }
 
