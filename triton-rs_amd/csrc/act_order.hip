@@ -33,7 +33,8 @@ gptq_repack_rows_kernel(const uint32_t* __restrict__ q, const int32_t* __restric
     qout[(size_t)jp * N + n] = w;
 }
 
-// xout[m, j] = x[m, perm[j]]. Grid (ceil(K / 2048), M), 256 threads x 8 columns.
+// xout[m, j] = x[m, perm[j]] (perm entries outside [0, K) read column K - 1). Grid
+// (ceil(K / 2048), M), 256 threads x 8 columns.
 __global__ void __launch_bounds__(256)
 gather_columns_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
                       half_t* __restrict__ xout, int K) {
@@ -43,10 +44,39 @@ gather_columns_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ 
     if (j0 + 8 <= K) {
         half8_t v;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = x[row + perm[j0 + i]];
+        for (int i = 0; i < 8; ++i) v[i] = x[row + min((uint32_t)perm[j0 + i], (uint32_t)K - 1u)];
         *reinterpret_cast<half8_t*>(xout + row + j0) = v;
     } else {
-        for (int j = j0; j < K; ++j) xout[row + j] = x[row + perm[j]];
+        for (int j = j0; j < K; ++j) xout[row + j] = x[row + min((uint32_t)perm[j], (uint32_t)K - 1u)];
+    }
+}
+
+// xout[m, j] = x[m, perm[j]] with the row staged in LDS: one workgroup per row, read and
+// written with 16-byte coalesced accesses, the permutation applied to the LDS copy (a gather
+// straight from global memory costs one cache request per element). Needs K % 8 == 0, K <=
+// GATHER_LDS_MAX_K and 16-byte aligned x, perm and xout; entries of perm outside [0, K) read
+// column K - 1 instead of memory past the row.
+constexpr int GATHER_LDS_MAX_K = 32768;   // 64 KiB of LDS
+
+__global__ void __launch_bounds__(256)
+gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
+                          half_t* __restrict__ xout, int K) {
+    extern __shared__ __attribute__((aligned(16))) half_t row_s[];
+    const size_t row = (size_t)blockIdx.x * K;
+    const int chunks = K / 8;
+    const u32x4* src = reinterpret_cast<const u32x4*>(x + row);
+    for (int c = threadIdx.x; c < chunks; c += 256) reinterpret_cast<u32x4*>(row_s)[c] = src[c];
+    __syncthreads();
+    const u32x4* pp = reinterpret_cast<const u32x4*>(perm);
+    u32x4* dst = reinterpret_cast<u32x4*>(xout + row);
+    const uint32_t last = (uint32_t)K - 1u;
+    for (int c = threadIdx.x; c < chunks; c += 256) {
+        const u32x4 p0 = pp[2 * c], p1 = pp[2 * c + 1];
+        const uint32_t idx[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        half8_t v;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = row_s[min(idx[i], last)];
+        dst[c] = __builtin_bit_cast(u32x4, v);
     }
 }
 
@@ -61,6 +91,20 @@ hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint3
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
                                  hipStream_t st) {
     (void)hipGetLastError();
+    const bool lds_ok = K % 8 == 0 && K <= GATHER_LDS_MAX_K &&
+                        reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(perm) % 16 == 0 &&
+                        reinterpret_cast<uintptr_t>(xout) % 16 == 0;
+    if (lds_ok) {
+        constexpr int MAX_BLOCKS = 1 << 30;
+        for (int m0 = 0; m0 < M; m0 += MAX_BLOCKS) {
+            const int rows = M - m0 < MAX_BLOCKS ? M - m0 : MAX_BLOCKS;
+            hipLaunchKernelGGL(gather_columns_lds_kernel, dim3(rows), dim3(256),
+                               (size_t)K * sizeof(half_t), st, x + (size_t)m0 * K, perm,
+                               xout + (size_t)m0 * K, K);
+        }
+        return hipGetLastError();
+    }
     constexpr int MAX_ROWS = 32768;   // grid y per launch
     for (int m0 = 0; m0 < M; m0 += MAX_ROWS) {
         const int rows = M - m0 < MAX_ROWS ? M - m0 : MAX_ROWS;
