@@ -306,11 +306,12 @@ def test_prefill_256_row_tiles(torch_cuda, orc, fmt, M, K, N, G):
 
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
-@pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (700, 1024, 2048), (2048, 1024, 4096)])
+@pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (700, 1024, 2048), (2048, 1024, 4096),
+                                   (1024, 14336, 4096)])
 def test_prefill_split_k(torch_cuda, orc, fmt, M, K, N):
-    """Few 256-row tiles: 256 x 256 tiles with K split over 2 or 4 workgroups, the last one
-    summing the fp32 partials in split order (a row tail included); repeated calls are
-    bit-identical."""
+    """Few 256-row tiles: K split over workgroups (256 x 128 tiles in 4 and 2 splits, 256 x 128
+    unsplit, 256 x 256 in 4 splits), the last split of a tile summing the fp32 partials in
+    split order (a row tail included); repeated calls are bit-identical."""
     P = pkg()
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2500 + M + fmt)
     assert P.plan(FMT_NAME[fmt], M, N, K, 128) == "prefill"
