@@ -147,6 +147,60 @@ def test_init_then_capture_replays(torch_cuda, orc):
         assert_parity(out.cpu().numpy(), ref, what="captured decode replay")
 
 
+def test_captured_graph_of_each_kernel_family_replays_exactly(torch_cuda):
+    """One graph holding a call of each kernel family with its split-K state: the row-paired
+    AWQ GEMV (fixed-point hand-off), the act-order small-batch kernel (group table and g_idx
+    slice in LDS), a K-split prefill (fp32 partials, counter hand-off) and the prepared
+    act-order path (LDS column gather, then the small-batch kernel). Replayed three times with
+    other eager calls on the same stream in between, every replay equals the eager outputs bit
+    for bit (the hand-offs leave their counters and slots clean; the launch-time LDS
+    allowances are valid under capture)."""
+    torch = torch_cuda
+    P = pkg()
+    s = torch.cuda.Stream()
+    cases = [
+        (Problem(AWQ, M=4, K=4096, N=2048, G=128, seed=3110), "awq", False, False),
+        (Problem(GPTQ, M=16, K=2048, N=1024, G=128, seed=3111, act_order=True), "gptq", True, False),
+        (Problem(AWQ, M=512, K=2048, N=4096, G=128, seed=3112), "awq", False, False),
+        (Problem(GPTQ, M=64, K=2048, N=1024, G=128, seed=3113, act_order=True), "gptq", True, True),
+    ]
+    assert P.plan("awq", 512, 4096, 2048, 128) == "prefill"
+    calls = []
+    for p, fmt, act, prepared in cases:
+        x, qw, sc, qz = (to_dev(v) for v in (p.x, p.qweight, p.scales, p.qzeros))
+        gi = to_dev(p.g_idx) if act else None
+        out = torch.empty((p.M, p.N), dtype=torch.float16, device="cuda:0")
+        if prepared:
+            qp, perm = P.prepare_act_order(qw, gi, group_size=p.G)
+            calls.append(lambda x=x, qp=qp, sc=sc, qz=qz, perm=perm, out=out, G=p.G:
+                         P.gemm_act_order(x, qp, sc, qz, perm, group_size=G, out=out))
+        else:
+            calls.append(lambda x=x, qw=qw, sc=sc, qz=qz, gi=gi, out=out, fmt=fmt, G=p.G:
+                         P.gemm(x, qw, sc, qz, fmt=fmt, group_size=G, g_idx=gi, out=out))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):                        # eager: sizes the stream's buffers
+        outs = [c() for c in calls]
+    s.synchronize()
+    eager = [o.cpu().numpy().copy() for o in outs]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for c in calls:
+            c()
+    other = Problem(AWQ, M=8, K=2048, N=4096, G=128, seed=3114)
+    oargs = [to_dev(v) for v in (other.x, other.qweight, other.scales, other.qzeros)]
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            P.gemm(*oargs, fmt="awq")                 # eager split-K work between replays
+            g.replay()
+            P.gemm(*oargs, fmt="awq")
+        s.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert np.array_equal(o.cpu().numpy().view(np.uint16), e.view(np.uint16)), (rep, i)
+
+
 # ------------------------------------------------------------------ MoE routing data
 
 def test_align_drops_out_of_range_expert_ids(torch_cuda, orc):
