@@ -46,8 +46,10 @@ def test_route_matches_oracle(torch_cuda, orc):
 
 
 @pytest.mark.parametrize("T,E,topk,bm", [(512, 8, 2, 64), (100, 8, 2, 16), (3000, 16, 4, 128),
-                                         (7, 64, 2, 64)])
+                                         (7, 64, 2, 64), (300, 128, 4, 16), (600, 256, 8, 32)])
 def test_align_matches_oracle(torch_cuda, orc, T, E, topk, bm):
+    """Up to 64 experts the align kernel ranks pairs with a per-wave ballot table, above that
+    expert by expert; both place every pair exactly as the oracle does (stable by pair)."""
     P = pkg()
     g = np.random.default_rng(71 + T)
     ids, _ = orc.moe_route(g.standard_normal((T, E)).astype(np.float32), topk)

@@ -69,6 +69,7 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int ren
 // *num_tiles. A tile never reaches into the padding, so the GEMM computes no padded block.
 constexpr int ALIGN_THREADS = 1024;
 constexpr int ALIGN_MAX_E = 1024;
+constexpr int ALIGN_FAST_E = 64;   // experts ranked with the per-wave ballot table
 
 __global__ void __launch_bounds__(ALIGN_THREADS)
 moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int capacity,
@@ -78,6 +79,7 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
     __shared__ int cnt[ALIGN_MAX_E];
     __shared__ int start[ALIGN_MAX_E];
     __shared__ int wave_tot[ALIGN_THREADS / 64];
+    __shared__ int wtab[ALIGN_FAST_E][ALIGN_THREADS / 64];
     __shared__ int total_sh;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
@@ -132,6 +134,35 @@ moe_align_kernel(const int32_t* __restrict__ ids, int P, int E, int block_m, int
     __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
 
+    if (E <= ALIGN_FAST_E) {
+        // each wave ranks its 64 pairs per expert with one ballot each; one table of wave
+        // totals per chunk gives the ranks across waves (3 barriers per chunk, not 3 E)
+        for (int c0 = 0; c0 < P; c0 += ALIGN_THREADS) {
+            const int p = c0 + tid;
+            int mine = p < P ? ids[p] : -1;
+            if ((unsigned)mine >= (unsigned)E) mine = -1;
+            int inwave = 0;
+            for (int e = 0; e < E; ++e) {
+                const uint64_t bal = __ballot(mine == e);
+                if (lane == 0) wtab[e][wave] = __popcll(bal);
+                if (mine == e) inwave = __popcll(bal & ((1ull << lane) - 1ull));
+            }
+            __syncthreads();
+            if (mine >= 0) {
+                int before = cnt[mine] + inwave;
+                for (int w = 0; w < wave; ++w) before += wtab[mine][w];
+                sorted_ids[start[mine] + before] = p;
+            }
+            __syncthreads();
+            if (tid < E) {
+                int t = 0;
+                for (int w = 0; w < ALIGN_THREADS / 64; ++w) t += wtab[tid][w];
+                cnt[tid] += t;
+            }
+            __syncthreads();
+        }
+        return;
+    }
     for (int c0 = 0; c0 < P; c0 += ALIGN_THREADS) {
         const int p = c0 + tid;
         int mine = p < P ? ids[p] : -1;
