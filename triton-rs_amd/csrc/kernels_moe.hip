@@ -61,8 +61,10 @@ hipError_t launch_moe_route(const float* logits, int T, int E, int topk, int ren
 
 // One workgroup of 1024 threads. Counts per expert, pads, lays the experts out in order and
 // places every pair at start[e] + (number of earlier pairs of the same expert), which keeps
-// the order stable. The rank is built per chunk of 1024 pairs and per expert with wave
-// ballots and a prefix over the 16 waves.
+// the order stable. The rank is built per chunk of 1024 pairs from wave ballots and a prefix
+// over the 16 waves: up to ALIGN_FAST_E experts every wave takes all its ballots first and
+// one table of wave totals serves all experts (3 barriers per chunk); above that, expert by
+// expert (3 barriers per expert and chunk).
 // With `tiles`, it also lists expert tiles for the grouped GEMM: the cnt[e] rows of expert e
 // split into ceil(cnt[e] / tile_bm) tiles of equal height (rounded up to 16 rows, the last
 // one shorter), each {first sorted row, rows, e, 0}, experts in order, and their number in
