@@ -201,6 +201,45 @@ def test_captured_graph_of_each_kernel_family_replays_exactly(torch_cuda):
             assert np.array_equal(o.cpu().numpy().view(np.uint16), e.view(np.uint16)), (rep, i)
 
 
+def test_concurrent_streams_and_threads_keep_split_k_state_apart(torch_cuda):
+    """Split-K calls on two streams at once, issued from two host threads: each stream has its
+    own workspace (counters, fixed-point slots, partials), so the interleaved calls give the
+    single-stream outputs bit for bit (a decode GEMV with the fixed-point hand-off on one
+    stream, a small-batch GEMM with the counter hand-off on the other)."""
+    import threading
+    torch = torch_cuda
+    P = pkg()
+    pa = Problem(AWQ, M=1, K=4096, N=4096, G=128, seed=3120)
+    pb = Problem(GPTQ, M=16, K=2048, N=2048, G=128, seed=3121)
+    aa = [to_dev(v) for v in (pa.x, pa.qweight, pa.scales, pa.qzeros)]
+    ab = [to_dev(v) for v in (pb.x, pb.qweight, pb.scales, pb.qzeros)]
+    ref_a = P.gemm(*aa, fmt="awq").cpu().numpy()
+    ref_b = P.gemm(*ab, fmt="gptq").cpu().numpy()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    outs_a = [torch.empty((pa.M, pa.N), dtype=torch.float16, device="cuda:0") for _ in range(20)]
+    outs_b = [torch.empty((pb.M, pb.N), dtype=torch.float16, device="cuda:0") for _ in range(20)]
+    torch.cuda.synchronize()
+    errors = []
+
+    def run(stream, args, fmt, outs):
+        try:
+            with torch.cuda.stream(stream):
+                for o in outs:
+                    P.gemm(*args, fmt=fmt, out=o)
+            stream.synchronize()
+        except Exception as e:   # reported by the main thread
+            errors.append(e)
+
+    ta = threading.Thread(target=run, args=(sa, aa, "awq", outs_a))
+    tb = threading.Thread(target=run, args=(sb, ab, "gptq", outs_b))
+    ta.start(); tb.start(); ta.join(); tb.join()
+    assert not errors, errors
+    for o in outs_a:
+        assert np.array_equal(o.cpu().numpy().view(np.uint16), ref_a.view(np.uint16))
+    for o in outs_b:
+        assert np.array_equal(o.cpu().numpy().view(np.uint16), ref_b.view(np.uint16))
+
+
 # ------------------------------------------------------------------ MoE routing data
 
 def test_align_drops_out_of_range_expert_ids(torch_cuda, orc):
