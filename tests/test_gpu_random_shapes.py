@@ -3,6 +3,8 @@ matrix-core GEMV, small batch with and without act-order, prefill with and witho
 generic strided kernel), with K, N, group size and format drawn together, checked against
 the CPU oracle on sampled rows. The draws are fixed by the seed, so a failure names its
 case and reproduces on the CPU oracle side."""
+import os
+
 import numpy as np
 import pytest
 
@@ -33,7 +35,10 @@ def _draw_cases(n=80, seed=20261202):
     return cases
 
 
-CASES = _draw_cases()
+# W4A16_RANDOM_CASES / W4A16_RANDOM_SEED widen the sweep for a longer run (defaults: the
+# committed 80 cases)
+CASES = _draw_cases(int(os.environ.get("W4A16_RANDOM_CASES", "80")),
+                    int(os.environ.get("W4A16_RANDOM_SEED", "20261202")))
 
 
 @pytest.fixture(scope="module")
