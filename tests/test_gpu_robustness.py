@@ -240,6 +240,34 @@ def test_concurrent_streams_and_threads_keep_split_k_state_apart(torch_cuda):
         assert np.array_equal(o.cpu().numpy().view(np.uint16), ref_b.view(np.uint16))
 
 
+def test_python_wrappers_reject_bad_layouts_before_launch(torch_cuda):
+    """The C ABI takes contiguous row-major buffers: the Python wrappers of every GEMM entry
+    point refuse a transposed view, a wrong dtype or a missing output before any launch."""
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(GPTQ, M=4, K=256, N=256, G=128, seed=0x5EED5000)
+    x, qw, sc, qz = (to_dev(v) for v in (p.x, p.qweight, p.scales, p.qzeros))
+    x_t = torch.empty((p.K, p.M), dtype=torch.float16, device="cuda:0").t()
+    perm = torch.arange(p.K, dtype=torch.int32, device="cuda:0")
+    out = torch.empty((p.M, p.N), dtype=torch.float16, device="cuda:0")
+    with pytest.raises(P.InvalidArgument, match="x must be contiguous"):
+        P.gemm(x_t, qw, sc, qz, fmt="gptq")
+    with pytest.raises(P.InvalidArgument, match="x must be contiguous"):
+        P.gemm_act_order(x_t, qw, sc, qz, perm)
+    with pytest.raises(P.InvalidArgument, match="x must be contiguous"):
+        P.gemm_noalloc(x_t, qw, sc, qz, out, fmt="gptq")
+    with pytest.raises(P.InvalidArgument, match="perm has dtype"):
+        P.gemm_act_order(x, qw, sc, qz, perm.long())
+    with pytest.raises(P.InvalidArgument, match="scales has dtype"):
+        P.gemm_noalloc(x, qw, sc.float(), qz, out, fmt="gptq")
+    with pytest.raises(P.InvalidArgument, match="out must be given"):
+        P.gemm_noalloc(x, qw, sc, qz, None, fmt="gptq")
+    with pytest.raises(P.InvalidArgument, match="out must be a contiguous"):
+        P.gemm_act_order(x, qw, sc, qz, perm, out=out.t().contiguous())
+    with pytest.raises(P.InvalidArgument, match="qweight must be contiguous"):
+        P.dequant(qw.t().contiguous().t(), sc, qz, fmt="gptq")
+
+
 # ------------------------------------------------------------------ MoE routing data
 
 def test_align_drops_out_of_range_expert_ids(torch_cuda, orc):

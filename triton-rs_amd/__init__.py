@@ -187,6 +187,39 @@ _INT32 = (torch.int32,)
 _HALF = (torch.float16,)
 
 
+def _gemm_operands(f: int, x, qweight, scales, qzeros, idx, idx_name: str):
+    """(M, N, K) of a GEMM call after checking dtypes, devices, ranks and contiguity (the C ABI
+    takes contiguous row-major buffers and checks sizes, not layouts)."""
+    _require(x, "x", _HALF)
+    dev = x.device
+    _require(qweight, "qweight", _INT32, dev)
+    _require(scales, "scales", _HALF, dev)
+    if qzeros is not None:
+        _require(qzeros, "qzeros", _INT32, dev)
+    if idx is not None:
+        _require(idx, idx_name, _INT32, dev)
+    if x.dim() != 2 or qweight.dim() != 2:
+        raise InvalidArgument("x and qweight must be 2-D")
+    for t, n in ((x, "x"), (qweight, "qweight"), (scales, "scales"), (qzeros, "qzeros"),
+                 (idx, idx_name)):
+        if t is not None and not t.is_contiguous():
+            raise InvalidArgument(f"{n} must be contiguous")
+    M, K = x.shape
+    N = qweight.shape[1] * 8 if f == FMT_AWQ else qweight.shape[1]
+    return M, N, K
+
+
+def _gemm_out(out, M: int, N: int, dev: torch.device, required: bool = False):
+    if out is None:
+        if required:
+            raise InvalidArgument("out must be given")
+        return torch.empty((M, N), dtype=torch.float16, device=dev)
+    _require(out, "out", _HALF, dev)
+    if tuple(out.shape) != (M, N) or not out.is_contiguous():
+        raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
+    return out
+
+
 # ------------------------------------------------------------------ op level
 
 def init(device: int = 0) -> None:
@@ -220,28 +253,8 @@ def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
     "gptq_sym" (zero = 8, qzeros unused) or "awq" (qweight [K, N/8], AWQ nibble order).
     """
     f = _fmt(fmt)
-    _require(x, "x", _HALF)
-    dev = x.device
-    _require(qweight, "qweight", _INT32, dev)
-    _require(scales, "scales", _HALF, dev)
-    if qzeros is not None:
-        _require(qzeros, "qzeros", _INT32, dev)
-    if g_idx is not None:
-        _require(g_idx, "g_idx", _INT32, dev)
-    if x.dim() != 2:
-        raise InvalidArgument("x must be 2-D [M, K]")
-    M, K = x.shape
-    N = qweight.shape[1] * 8 if f == FMT_AWQ else qweight.shape[1]
-    for t, n in ((x, "x"), (qweight, "qweight"), (scales, "scales"), (qzeros, "qzeros"),
-                 (g_idx, "g_idx")):
-        if t is not None and not t.is_contiguous():
-            raise InvalidArgument(f"{n} must be contiguous")
-    if out is None:
-        out = torch.empty((M, N), dtype=torch.float16, device=dev)
-    else:
-        _require(out, "out", _HALF, dev)
-        if tuple(out.shape) != (M, N) or not out.is_contiguous():
-            raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
+    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx")
+    out = _gemm_out(out, M, N, x.device)
     check(lib().w4a16_gemm(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
                            _ptr(g_idx), _ptr(out), M, N, K, group_size, zero_offset))
     return out
@@ -266,10 +279,8 @@ def gemm_act_order(x, qweight_prepared, scales, qzeros, perm, fmt="gptq", group_
                    zero_offset: int = 1, out=None) -> torch.Tensor:
     """x @ W16 for an act-order checkpoint prepared by prepare_act_order."""
     f = _fmt(fmt)
-    M, K = x.shape
-    N = qweight_prepared.shape[1]
-    if out is None:
-        out = torch.empty((M, N), dtype=torch.float16, device=x.device)
+    M, N, K = _gemm_operands(f, x, qweight_prepared, scales, qzeros, perm, "perm")
+    out = _gemm_out(out, M, N, x.device)
     check(lib().w4a16_gemm_act_order(_stream(x), f, _ptr(x), _ptr(qweight_prepared), _ptr(scales),
                                      _ptr(qzeros), _ptr(perm), _ptr(out), M, N, K, group_size,
                                      zero_offset))
@@ -281,11 +292,8 @@ def gemm_noalloc(x, qweight, scales, qzeros, out, fmt="awq", group_size: int = 1
     """w4a16_gemm_noalloc: as gemm(), but the library allocates nothing during the call (its
     split-K scratch is a fixed per-device array); `out` must be given."""
     f = _fmt(fmt)
-    M, K = x.shape
-    N = qweight.shape[1] * 8 if f == FMT_AWQ else qweight.shape[1]
-    _require(out, "out", _HALF, x.device)
-    if tuple(out.shape) != (M, N) or not out.is_contiguous():
-        raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
+    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx")
+    out = _gemm_out(out, M, N, x.device, required=True)
     check(lib().w4a16_gemm_noalloc(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales),
                                    _ptr(qzeros), _ptr(g_idx), _ptr(out), M, N, K, group_size,
                                    zero_offset))
@@ -297,6 +305,15 @@ def dequant(qweight, scales, qzeros, fmt="gptq", K: int | None = None, group_siz
     """W16 as fp16, [K, N] (or [N, K] when transposed)."""
     f = _fmt(fmt)
     _require(qweight, "qweight", _INT32)
+    dev = qweight.device
+    _require(scales, "scales", _HALF, dev)
+    if qzeros is not None:
+        _require(qzeros, "qzeros", _INT32, dev)
+    if g_idx is not None:
+        _require(g_idx, "g_idx", _INT32, dev)
+    for t, n in ((qweight, "qweight"), (scales, "scales"), (qzeros, "qzeros"), (g_idx, "g_idx")):
+        if t is not None and not t.is_contiguous():
+            raise InvalidArgument(f"{n} must be contiguous")
     if f == FMT_AWQ:
         K, N = qweight.shape[0], qweight.shape[1] * 8
     else:
