@@ -23,8 +23,9 @@
 // for every group and every column of its strip, the scale and the zero (as fp16 1024 + z)
 // in one 32-bit entry; each k row then gathers its entries by g_idx[k]. The arithmetic per
 // weight is unchanged, (fp16(1024 + q) - fp16(1024 + z)) * s, so the weights stay bit-exact.
-// GIDX = 2 also stages the workgroup's slice of g_idx in LDS (one load per thread instead of
-// two 32-byte loads per lane and k32 step, which the 16 lanes of a k block all repeat);
+// GIDX = 2 also stages the workgroup's slice of g_idx in LDS, as clamped table offsets (one
+// load per thread instead of two 32-byte loads per lane and k32 step, which the 16 lanes of
+// a k block all repeat, and no index arithmetic in the steps);
 // GIDX = 1 (slice too large for the LDS budget) reads g_idx per step from global memory.
 #include "device_common.h"
 #include "launch.h"
@@ -166,6 +167,13 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
     const bool gsl_early = GIDX == 2 && gsl_chunks <= GC * NT;
     const int32_t* gsrc = p.g_idx + (size_t)split * gsl_rows;
     uint32_t* gsl = gtab + tab_n;
+    // the slice holds each row's table offset, clamp(g_idx, 0, groups - 1) * WN, so that the
+    // steps read it without per-lane arithmetic
+    auto gsl_entry = [&](u32x4 g) {
+        const int hi = ngroups - 1;
+        return u32x4{(uint32_t)(min(max((int)g.x, 0), hi) * WN), (uint32_t)(min(max((int)g.y, 0), hi) * WN),
+                     (uint32_t)(min(max((int)g.z, 0), hi) * WN), (uint32_t)(min(max((int)g.w, 0), hi) * WN)};
+    };
     u32x4 tsv[TC], gsv[GC];
     uint32_t tzv[TC];
     auto tab_load = [&](int c, u32x4& sv, uint32_t& zw) {
@@ -225,11 +233,11 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
 #pragma unroll
                 for (int e = 0; e < GC; ++e) {
                     const int c = (int)threadIdx.x + e * NT;
-                    if (c < gsl_chunks) reinterpret_cast<u32x4*>(gsl)[c] = gsv[e];
+                    if (c < gsl_chunks) reinterpret_cast<u32x4*>(gsl)[c] = gsl_entry(gsv[e]);
                 }
             } else {
                 for (int c = threadIdx.x; c < gsl_chunks; c += NT)
-                    reinterpret_cast<u32x4*>(gsl)[c] = reinterpret_cast<const u32x4*>(gsrc)[c];
+                    reinterpret_cast<u32x4*>(gsl)[c] = gsl_entry(reinterpret_cast<const u32x4*>(gsrc)[c]);
             }
         }
         __syncthreads();
@@ -297,8 +305,9 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
             uint32_t t[8][CPL];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const uint32_t g = (uint32_t)min(max(gv[i], 0), ngroups - 1);
-                const uint32_t* row = gtab + g * WN + CPL * j;
+                // GIDX = 2: the slice already holds the clamped group's table offset
+                const uint32_t* row = gtab + CPL * j +
+                    (GIDX == 2 ? (uint32_t)gv[i] : (uint32_t)min(max(gv[i], 0), ngroups - 1) * WN);
                 if constexpr (CPL == 2) {
                     const u32x2 v = *reinterpret_cast<const u32x2*>(row);
                     t[i][0] = v.x; t[i][1] = v.y;
