@@ -49,9 +49,13 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 }  // namespace
 
 // SPW: k32 steps per wave when known at compile time (SPW = PF: the prologue issues every
-// step and no loop is emitted), 0 for the runtime count p.steps_per_wave
-template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW>
+// step and no loop is emitted), 0 for the runtime count p.steps_per_wave.
+// RG (plain group order): every ring round of PF steps lies in one group (G % (32 PF) == 0
+// and steps_per_wave % PF == 0), so the round's first slot alone loads the scales and zeros,
+// and the zero points and scales are splatted once per round instead of once per step.
+template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false>
 __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel(SkinnyParams p) {
+    static_assert(!RG || !GIDX, "one group per round needs plain group order");
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
                   "columns per lane");
@@ -126,6 +130,9 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
             greg[u][0] = g0.x; greg[u][1] = g0.y; greg[u][2] = g0.z; greg[u][3] = g0.w;
             greg[u][4] = g1.x; greg[u][5] = g1.y; greg[u][6] = g1.z; greg[u][7] = g1.w;
             return;
+        }
+        if constexpr (RG) {
+            if (u != 0) return;   // the round's group comes with its first step
         }
         // scales and zero word of the lane's columns for this step's group
         const int g = kg / p.G;
@@ -243,12 +250,14 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
         __syncthreads();
     }
 
+    // zero point (as fp16 1024 + z) and scale per column, splatted; with RG they are set by
+    // the first step of a round and kept for the others
+    half2_t hz[CPL], hs[CPL];
+
     // one k32 step from ring slot u
     auto compute = [&](int u) __attribute__((always_inline)) {
-        // zero point (as fp16 1024 + z) and scale per column, splatted
-        half2_t hz[CPL], hs[CPL];
 #pragma unroll
-        for (int c = 0; c < (GIDX != 0 ? 0 : CPL); ++c) {
+        for (int c = 0; c < (GIDX != 0 || (RG && u != 0) ? 0 : CPL); ++c) {
             const int cw = (nl & 7) + c;   // column within its qzeros word
             int z;
             if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
@@ -495,8 +504,15 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
         }
     }
     if constexpr (FMT != FMT_AWQ) {
+        // one group per ring round (RG): the wave's rounds start on multiples of 32 PF rows
+        const bool rg = p.G % (32 * PF) == 0 && s.steps_per_wave % PF == 0;
         if (s.steps_per_wave == PF) {   // as above: M=16, 4096 -> 6144 9.4 -> 8.6 us
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            if (rg) hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, true>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            else hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            return hipGetLastError();
+        }
+        if (rg) {
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, true>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
             return hipGetLastError();
         }
     }
