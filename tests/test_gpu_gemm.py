@@ -379,13 +379,18 @@ def test_act_order_shapes(torch_cuda, orc, fmt, M, K, N, G, zo):
     assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"act-order fmt={fmt} M={M}")
 
 
-def test_act_order_identity_gidx_equals_plain(torch_cuda):
-    """g_idx[k] = k / G must give exactly the same output as no g_idx (same kernel, same
-    per-weight arithmetic and accumulation order)."""
-    p = Problem(GPTQ, M=16, K=2048, N=512, G=128, seed=1320)
+@pytest.mark.parametrize("M,K,N,G", [(16, 2048, 512, 128), (32, 4096, 1024, 128),
+                                     (64, 4096, 768, 256), (48, 2048, 1024, 64),
+                                     (16, 4096, 6144, 128)])
+def test_act_order_identity_gidx_equals_plain(torch_cuda, M, K, N, G):
+    """g_idx[k] = k / G must give exactly the same output as no g_idx: the same per-weight
+    arithmetic and accumulation order, whether the plain path loads each group's scales and
+    zeros once per ring round (G a multiple of 128) or once per step (G = 64)."""
+    p = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=1320 + M + G)
+    assert pkg().plan("gptq", M, N, K, G) == "skinny"
     plain = _run_gemm(torch_cuda, p)
     ident = _run_gemm(torch_cuda, p, g_idx=(np.arange(p.K) // p.G).astype(np.int32))
-    assert np.array_equal(plain, ident)
+    assert np.array_equal(plain.view(np.uint16), ident.view(np.uint16))
 
 
 def test_act_order_large_m_uses_strided(torch_cuda, orc):
