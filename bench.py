@@ -496,13 +496,14 @@ def extras(torch, pkg, dev, stream, args):
     del w13, w2, L
     torch.cuda.empty_cache()
     res["achievable"] = achievable_refs(torch, dev, stream)
+    res["achievable"].update(dequant_then_mm_refs(torch, pkg, dev, stream, gen))
     return res
 
 
 def achievable_refs(torch, dev, stream):
-    """Measured references on this GPU, beside the spec peaks: a device-to-device copy (bytes
-    read + written) and a read-only fp32 sum of 512 MiB (HBM), and torch's fp16 GEMM
-    (hipBLASLt / rocBLAS, no dequantisation) at config 3's two shapes (MFMA)."""
+    """Measured HBM references on this GPU, beside the spec peak: a device-to-device copy
+    (bytes read + written) and a read-only fp32 sum of 512 MiB. (The MFMA references, torch's
+    fp16 GEMM at config 3's shapes, come from dequant_then_mm_refs, timed like the GEMMs.)"""
     out = {}
     n = 512 << 20
     a = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -530,14 +531,41 @@ def achievable_refs(torch, dev, stream):
     ms = t_ms(lambda: torch.sum(af), 20)
     out["read_sum_f32_GBps"] = round(n / (ms * 1e-3) / 1e9, 1)
     del a, b, af
+    progress(f"achievable references: {out}")
+    return out
+
+
+def dequant_then_mm_refs(torch, pkg, dev, stream, gen):
+    """The unfused dense path at config 3's shapes: this library's dequantisation of the AWQ
+    weights to fp16 [K, N], then torch's fp16 GEMM (hipBLASLt / rocBLAS), per call, against
+    which the fused prefill kernel is compared (rotated weight sets, graph replays, as for the
+    GEMMs); and torch's fp16 GEMM alone timed the same way."""
+    out = {}
     for K, N in ((4096, 14336), (14336, 4096)):
         M = 2048
-        x = torch.randn((M, K), device=dev, dtype=torch.float16)
-        w = torch.randn((K, N), device=dev, dtype=torch.float16)
-        ms = t_ms(lambda: torch.mm(x, w), 20)
+        sets = make_weight_sets(torch, "awq", K, N, 128, 4, dev, seed=zlib.crc32(b"deq%d" % K))
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        w16 = torch.empty((K, N), dtype=torch.float16, device=dev)
+        y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        lib = pkg.lib()
+
+        def fn(i):
+            qw, sc, qz = sets[i % len(sets)]
+            pkg.check(lib.w4a16_dequant(pkg._stream(qw), pkg.FMT_AWQ, pkg._ptr(qw), pkg._ptr(sc),
+                                        pkg._ptr(qz), None, pkg._ptr(w16), K, N, 128, 1, 0))
+            torch.mm(x, w16, out=y)
+        ms = time_calls(torch, fn, 20, 5, stream, len(sets), batch_calls=40, graph_calls=10,
+                        n_graphs=2)[1]
+        out[f"dequant_then_torch_mm_m{M}_k{K}_n{N}_us"] = round(ms * 1e3, 1)
+        # the fp16 GEMM alone, timed the same way (graph replays), over 4 rotated fp16 weights
+        ws16 = [torch.randn((K, N), device=dev, generator=gen).half() for _ in range(4)]
+        ms = time_calls(torch, lambda i: torch.mm(x, ws16[i % 4], out=y), 20, 5, stream, 4,
+                        batch_calls=40, graph_calls=10, n_graphs=2)[1]
+        out[f"torch_fp16_mm_m{M}_k{K}_n{N}_us"] = round(ms * 1e3, 1)
         out[f"torch_fp16_mm_m{M}_k{K}_n{N}_TFLOPs"] = round(2.0 * M * N * K / (ms * 1e-3) / 1e12, 1)
-        del x, w
-    progress(f"achievable references: {out}")
+        del sets, x, w16, y, ws16
+    torch.cuda.empty_cache()
+    progress(f"dequant then fp16 GEMM: {out}")
     return out
 
 
