@@ -206,6 +206,9 @@ PMC_WORKLOADS = {
     "c2_m16": ("gptq", 16, 4096, 6144, 128, True),
     "c2_m32": ("gptq", 32, 4096, 6144, 128, True),
     "c2_m64": ("gptq", 64, 4096, 6144, 128, True),
+    "c2_plain_m16": ("gptq", 16, 4096, 6144, 128, False),
+    "c2_plain_m32": ("gptq", 32, 4096, 6144, 128, False),
+    "c2_plain_m64": ("gptq", 64, 4096, 6144, 128, False),
     "c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128, False),
     "c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128, False),
     "c4_moe": None,
