@@ -8,6 +8,7 @@ GPU, with one untimed replay enqueued just ahead of the start event so that the 
 when the timed work is launched. `value` is algorithmic GB/s (bytes of qweight + scales +
 qzeros + x + out, each counted once) over that region, measured with HIP events on the
 launch stream; the median of five further batches of 1000 calls is reported beside it.
+(Act-order lines in "extra" also count the int32 g_idx, or the prepared path's permutation.)
 
 roofline.traffic: HBM bytes per launch of the headline kernel from two rocprofv3 --pmc
 passes (FETCH_SIZE, then WRITE_SIZE) over a child run of this script (--pmc-child), each
@@ -47,11 +48,15 @@ COPY_ELEMS = 128 * 1024 * 1024   # int32 elements streamed by the calibration ke
 HEADLINE = ("awq", 1, 4096, 14336, 128)
 
 
-def algorithmic_bytes(fmt: str, M: int, K: int, N: int, G: int) -> int:
+def algorithmic_bytes(fmt: str, M: int, K: int, N: int, G: int, act_order: bool = False) -> int:
+    """Bytes a call must move, each tensor counted once: qweight, scales, qzeros (none for
+    the symmetric format), the int32 g_idx (or the prepared path's permutation) for
+    act-order, x and out."""
     qweight = K * N // 2
     scales = (K // G) * N * 2
     qzeros = 0 if fmt == "gptq_sym" else (K // G) * N // 2
-    return qweight + scales + qzeros + M * K * 2 + M * N * 2
+    gidx = K * 4 if act_order else 0
+    return qweight + scales + qzeros + gidx + M * K * 2 + M * N * 2
 
 
 def make_weight_sets(torch, fmt, K, N, G, count, dev, seed):
@@ -329,8 +334,8 @@ def pmc_report(args) -> int:
     rep = {"workload": args.pmc_workload, "passes": [], "measured_dispatches": PMC_MEASURED}
     spec = PMC_WORKLOADS[args.pmc_workload]
     if spec is not None:
-        fmt, M, K, N, G, _ = spec
-        rep["algorithmic_bytes"] = algorithmic_bytes(fmt, M, K, N, G)
+        fmt, M, K, N, G, act_order = spec
+        rep["algorithmic_bytes"] = algorithmic_bytes(fmt, M, K, N, G, act_order)
     traffic = {}
     for counters in groups:
         table = _rocprof_pass(rocprof, counters, args.pmc_workload, args.sets, outdir)
@@ -400,8 +405,8 @@ def extras(torch, pkg, dev, stream, args):
     gen = torch.Generator(device=dev)
     gen.manual_seed(0x5EED0003)
 
-    def record(tag, fmt, M, K, N, G, ms, kernel):
-        nbytes = algorithmic_bytes(fmt, M, K, N, G)
+    def record(tag, fmt, M, K, N, G, ms, kernel, act_order=False):
+        nbytes = algorithmic_bytes(fmt, M, K, N, G, act_order)
         tfl = 2.0 * M * N * K / (ms * 1e-3) / 1e12
         res[tag] = {"kernel": kernel, "us_per_call": round(ms * 1e3, 2),
                     "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "TFLOPs": round(tfl, 2),
@@ -415,7 +420,8 @@ def extras(torch, pkg, dev, stream, args):
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         # graph replays for every size: steady-state clocks, no host launch gaps
         ms = time_graphs(torch, pkg, x, sets, out, fmt, G, calls, 10, stream, g_idx=g_idx)
-        record(tag, fmt, M, K, N, G, ms, pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None))
+        record(tag, fmt, M, K, N, G, ms, pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None),
+               act_order=g_idx is not None)
         del sets
 
     gemm_case("c0_gptq_sym_m1_k4096_n4096", "gptq_sym", 1, 4096, 4096, 128, 60, 1000)
@@ -443,7 +449,8 @@ def extras(torch, pkg, dev, stream, args):
             pkg.gemm_act_order(x, qp, sc, qz, pm, group_size=G, out=out)
         ms = time_calls(torch, fn, GRAPH_CALLS, 10, stream, n_sets, batch_calls=calls,
                         n_graphs=min(10, max(1, 1000 // GRAPH_CALLS)))[1]
-        record(tag, "gptq", M, K, N, G, ms, "gather+" + pkg.plan("gptq", M, N, K, G))
+        record(tag, "gptq", M, K, N, G, ms, "gather+" + pkg.plan("gptq", M, N, K, G),
+               act_order=True)
         del sets, prep
 
     for M in (16, 64):
