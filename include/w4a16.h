@@ -58,6 +58,14 @@ typedef enum {
  * scales are fp16 [K/G, N] for all three. */
 typedef enum { W4A16_FMT_GPTQ = 0, W4A16_FMT_GPTQ_SYM = 1, W4A16_FMT_AWQ = 2 } w4a16_format;
 
+/* OR-ed into `fmt` of w4a16_gemm, w4a16_gemm_noalloc, w4a16_gemm_plan and w4a16_dequant:
+ * x, scales and out are bfloat16 instead of fp16 (the reference kernels are generic over the
+ * element type, w4a16_gptq_gemm_typed.rs:65-67, and name bf16; its v0 instantiates f16).
+ * A weight dequantises to RNE_bf16(f32(q - z) * f32(s)), products accumulate in fp32 and the
+ * output is rounded to bf16 once. These calls run on the generic kernel (no split-K, any
+ * shape). The other entry points reject the flag as an unknown format. */
+#define W4A16_BF16 0x100
+
 /* Kernel regimes reported by w4a16_gemm_plan(). */
 typedef enum {
     W4A16_KERNEL_GEMV = 1,       /* decode: split-K GEMV, VALU dot2, no MFMA */

@@ -62,6 +62,15 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_moe_forward.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
     L.orc_silu_mul_f16.restype = ctypes.c_uint16
     L.orc_silu_mul_f16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+    L.orc_f32_to_bf16.restype = ctypes.c_uint16
+    L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
+    L.orc_bf16_to_f32.restype = ctypes.c_float
+    L.orc_bf16_to_f32.argtypes = [ctypes.c_uint16]
+    L.orc_f32_to_bf16_array.argtypes = [_P, _P, ctypes.c_size_t]
+    L.orc_bf16_to_f32_array.argtypes = [_P, _P, ctypes.c_size_t]
+    L.orc_dequant_bf16.argtypes = [_I, _P, _P, _P, _P, _I, _I, _I, _I, _P]
+    L.orc_dequant_transposed_bf16.argtypes = [_I, _P, _P, _P, _P, _I, _I, _I, _I, _P]
+    L.orc_w4a16_gemm_bf16.argtypes = [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P]
     L.orc_num_threads.restype = _I
     L.orc_set_num_threads.argtypes = [_I]
 
@@ -103,6 +112,52 @@ def f16_bits_to_f32(a) -> np.ndarray:
     out = np.empty(a.shape, dtype=np.float32)
     lib().orc_f16_to_f32_array(_ptr(a), _ptr(out), a.size)
     return out
+
+
+def f32_to_bf16_bits(a) -> np.ndarray:
+    """bfloat16 bit patterns (uint16) of float32 values, rounded to nearest even."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, dtype=np.uint16)
+    lib().orc_f32_to_bf16_array(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def bf16_bits_to_f32(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, dtype=np.float32)
+    lib().orc_bf16_to_f32_array(_ptr(a), _ptr(out), a.size)
+    return out
+
+
+def dequant_bf16(fmt, qweight, scales_bits, qzeros, K, N, G, g_idx=None, zero_offset=1,
+                 transposed=False) -> np.ndarray:
+    """W as bfloat16 bit patterns (uint16) [K, N] (or [N, K]) from bf16 scale bits."""
+    qweight, qzeros, g_idx = _i32(qweight), _i32(qzeros), _i32(g_idx)
+    scales = np.ascontiguousarray(scales_bits, dtype=np.uint16)
+    out = np.empty((N, K) if transposed else (K, N), dtype=np.uint16)
+    fn = lib().orc_dequant_transposed_bf16 if transposed else lib().orc_dequant_bf16
+    rc = fn(fmt, _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), K, N, G,
+            zero_offset, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"oracle dequant failed rc={rc}")
+    return out
+
+
+def w4a16_gemm_bf16(fmt, x_bits, qweight, scales_bits, qzeros, K, N, G, g_idx=None,
+                    zero_offset=1, acc64=True):
+    """(out bf16 bits [M, N], unrounded f32 sums) of the bfloat16 instantiation."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    qweight, qzeros, g_idx = _i32(qweight), _i32(qzeros), _i32(g_idx)
+    scales = np.ascontiguousarray(scales_bits, dtype=np.uint16)
+    M = x.shape[0]
+    out = np.empty((M, N), dtype=np.uint16)
+    of = np.empty((M, N), dtype=np.float32)
+    rc = lib().orc_w4a16_gemm_bf16(fmt, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
+                                   _ptr(g_idx), M, N, K, G, zero_offset, 1 if acc64 else 0,
+                                   _ptr(out), _ptr(of))
+    if rc != 0:
+        raise ValueError(f"oracle gemm failed rc={rc}")
+    return out, of
 
 
 def awq_slot(n: int) -> int:

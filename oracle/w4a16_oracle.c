@@ -89,6 +89,39 @@ void orc_f16_to_f32_array(const uint16_t* src, float* dst, size_t n) {
     for (size_t i = 0; i < n; ++i) dst[i] = h2f(src[i]);
 }
 
+/* ------------------------------------------------------------------ bf16 */
+/* The reference kernels are generic over the element type T and name bf16
+ * (w4a16_gptq_gemm_typed.rs:65-67); as_t::<bf16>(f32) is arith.truncf, round to nearest even
+ * (module.rs:726-731). bfloat16 is the top half of an f32. */
+
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    if ((x & 0x7F800000u) == 0x7F800000u && (x & 0x7FFFFFu))
+        return (uint16_t)((x >> 16) | 0x40u);      /* NaN stays NaN (quiet), sign kept */
+    x += 0x7FFFu + ((x >> 16) & 1u);               /* to nearest, ties to even; may reach inf */
+    return (uint16_t)(x >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t b) {
+    const uint32_t x = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+void orc_f32_to_bf16_array(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_f32_to_bf16(src[i]);
+}
+
+void orc_bf16_to_f32_array(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = orc_bf16_to_f32(src[i]);
+}
+
+/* element type of the 16-bit operands: 0 fp16, 1 bf16 */
+static inline float e2f(uint16_t v, int bf16) { return bf16 ? orc_bf16_to_f32(v) : h2f(v); }
+static inline uint16_t f2e(float v, int bf16) { return bf16 ? orc_f32_to_bf16(v) : orc_f32_to_f16(v); }
+
 /* ------------------------------------------------------------ unpacking */
 
 int orc_awq_slot(int n) {
@@ -120,10 +153,10 @@ int orc_zero_at(int fmt, const int32_t* qzeros, int N, int g, int n, int zero_of
     return orc_nibble(word, n % 8) + zero_offset;        /* gptq :231-236 (+1) */
 }
 
-static inline uint16_t dequant_one(int q, int z, uint16_t s) {
-    /* to_f32(centered) * to_f32(scale) then as_t::<f16> = truncf (RNE):
+static inline uint16_t dequant_one(int q, int z, uint16_t s, int bf16) {
+    /* to_f32(centered) * to_f32(scale) then as_t::<T> = truncf (RNE):
      * w4a16_gptq_gemm_typed.rs:256-260, awq_gemm_int4_typed.rs:224-228 */
-    return orc_f32_to_f16((float)(q - z) * h2f(s));
+    return f2e((float)(q - z) * e2f(s, bf16), bf16);
 }
 
 static int check_gidx(const int32_t* g_idx, int K, int N, int G) {
@@ -135,9 +168,9 @@ static int check_gidx(const int32_t* g_idx, int K, int N, int G) {
     return 0;
 }
 
-int orc_dequant(int fmt, const int32_t* qweight, const uint16_t* scales,
-                const int32_t* qzeros, const int32_t* g_idx, int K, int N, int G,
-                int zero_offset, uint16_t* out) {
+static int dequant_impl(int fmt, const int32_t* qweight, const uint16_t* scales,
+                        const int32_t* qzeros, const int32_t* g_idx, int K, int N, int G,
+                        int zero_offset, int bf16, uint16_t* out) {
     if (check_gidx(g_idx, K, N, G)) return -1;
 #pragma omp parallel for schedule(static)
     for (int k = 0; k < K; ++k) {
@@ -145,15 +178,27 @@ int orc_dequant(int fmt, const int32_t* qweight, const uint16_t* scales,
         for (int n = 0; n < N; ++n) {
             const int q = orc_qweight_at(fmt, qweight, K, N, k, n);
             const int z = orc_zero_at(fmt, qzeros, N, g, n, zero_offset);
-            out[(size_t)k * N + n] = dequant_one(q, z, scales[(size_t)g * N + n]);
+            out[(size_t)k * N + n] = dequant_one(q, z, scales[(size_t)g * N + n], bf16);
         }
     }
     return 0;
 }
 
-int orc_dequant_transposed(int fmt, const int32_t* qweight, const uint16_t* scales,
-                           const int32_t* qzeros, const int32_t* g_idx, int K, int N,
-                           int G, int zero_offset, uint16_t* out_nk) {
+int orc_dequant(int fmt, const int32_t* qweight, const uint16_t* scales,
+                const int32_t* qzeros, const int32_t* g_idx, int K, int N, int G,
+                int zero_offset, uint16_t* out) {
+    return dequant_impl(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, 0, out);
+}
+
+int orc_dequant_bf16(int fmt, const int32_t* qweight, const uint16_t* scales,
+                     const int32_t* qzeros, const int32_t* g_idx, int K, int N, int G,
+                     int zero_offset, uint16_t* out) {
+    return dequant_impl(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, 1, out);
+}
+
+static int dequant_transposed_impl(int fmt, const int32_t* qweight, const uint16_t* scales,
+                                   const int32_t* qzeros, const int32_t* g_idx, int K, int N,
+                                   int G, int zero_offset, int bf16, uint16_t* out_nk) {
     if (check_gidx(g_idx, K, N, G)) return -1;
     /* ferrum_dequant_int4.rs:121-138: store(output + col*K + base_k + i) */
 #pragma omp parallel for schedule(static)
@@ -162,10 +207,24 @@ int orc_dequant_transposed(int fmt, const int32_t* qweight, const uint16_t* scal
             const int g = g_idx ? g_idx[k] : k / G;
             const int q = orc_qweight_at(fmt, qweight, K, N, k, n);
             const int z = orc_zero_at(fmt, qzeros, N, g, n, zero_offset);
-            out_nk[(size_t)n * K + k] = dequant_one(q, z, scales[(size_t)g * N + n]);
+            out_nk[(size_t)n * K + k] = dequant_one(q, z, scales[(size_t)g * N + n], bf16);
         }
     }
     return 0;
+}
+
+int orc_dequant_transposed(int fmt, const int32_t* qweight, const uint16_t* scales,
+                           const int32_t* qzeros, const int32_t* g_idx, int K, int N,
+                           int G, int zero_offset, uint16_t* out_nk) {
+    return dequant_transposed_impl(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, 0,
+                                   out_nk);
+}
+
+int orc_dequant_transposed_bf16(int fmt, const int32_t* qweight, const uint16_t* scales,
+                                const int32_t* qzeros, const int32_t* g_idx, int K, int N,
+                                int G, int zero_offset, uint16_t* out_nk) {
+    return dequant_transposed_impl(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, 1,
+                                   out_nk);
 }
 
 /* ---------------------------------------------------------------- GEMM */
@@ -173,7 +232,8 @@ int orc_dequant_transposed(int fmt, const int32_t* qweight, const uint16_t* scal
 #define COLBLK 256
 
 static void gemm_rows(const uint16_t* x, const uint16_t* w16, const int32_t* rows,
-                      int nrows, int N, int K, int acc64, uint16_t* out, float* out_f32) {
+                      int nrows, int N, int K, int acc64, int bf16, uint16_t* out,
+                      float* out_f32) {
     const int nblk = (N + COLBLK - 1) / COLBLK;
 #pragma omp parallel for schedule(dynamic, 1) collapse(2)
     for (int ri = 0; ri < nrows; ++ri) {
@@ -186,25 +246,25 @@ static void gemm_rows(const uint16_t* x, const uint16_t* w16, const int32_t* row
                 double acc[COLBLK];
                 for (int n = n0; n < n1; ++n) acc[n - n0] = 0.0;
                 for (int k = 0; k < K; ++k) {
-                    const double xv = (double)h2f(xr[k]);
+                    const double xv = (double)e2f(xr[k], bf16);
                     const uint16_t* wr = w16 + (size_t)k * N;
-                    for (int n = n0; n < n1; ++n) acc[n - n0] += xv * (double)h2f(wr[n]);
+                    for (int n = n0; n < n1; ++n) acc[n - n0] += xv * (double)e2f(wr[n], bf16);
                 }
                 for (int n = n0; n < n1; ++n) {
                     const float v = (float)acc[n - n0];
-                    out[(size_t)ri * N + n] = orc_f32_to_f16(v);
+                    out[(size_t)ri * N + n] = f2e(v, bf16);
                     if (out_f32) out_f32[(size_t)ri * N + n] = v;
                 }
             } else {
                 float acc[COLBLK];
                 for (int n = n0; n < n1; ++n) acc[n - n0] = 0.0f;
                 for (int k = 0; k < K; ++k) {
-                    const float xv = h2f(xr[k]);
+                    const float xv = e2f(xr[k], bf16);
                     const uint16_t* wr = w16 + (size_t)k * N;
-                    for (int n = n0; n < n1; ++n) acc[n - n0] += xv * h2f(wr[n]);
+                    for (int n = n0; n < n1; ++n) acc[n - n0] += xv * e2f(wr[n], bf16);
                 }
                 for (int n = n0; n < n1; ++n) {
-                    out[(size_t)ri * N + n] = orc_f32_to_f16(acc[n - n0]);
+                    out[(size_t)ri * N + n] = f2e(acc[n - n0], bf16);
                     if (out_f32) out_f32[(size_t)ri * N + n] = acc[n - n0];
                 }
             }
@@ -214,7 +274,7 @@ static void gemm_rows(const uint16_t* x, const uint16_t* w16, const int32_t* row
 
 void orc_gemm_f16(const uint16_t* x, const uint16_t* w16, int M, int N, int K,
                   int acc64, uint16_t* out, float* out_f32) {
-    gemm_rows(x, w16, NULL, M, N, K, acc64, out, out_f32);
+    gemm_rows(x, w16, NULL, M, N, K, acc64, 0, out, out_f32);
 }
 
 int orc_w4a16_gemm(int fmt, const uint16_t* x, const int32_t* qweight,
@@ -229,6 +289,18 @@ int orc_w4a16_gemm(int fmt, const uint16_t* x, const int32_t* qweight,
     return rc;
 }
 
+int orc_w4a16_gemm_bf16(int fmt, const uint16_t* x, const int32_t* qweight,
+                        const uint16_t* scales, const int32_t* qzeros, const int32_t* g_idx,
+                        int M, int N, int K, int G, int zero_offset, int acc64,
+                        uint16_t* out, float* out_f32) {
+    uint16_t* w16 = (uint16_t*)malloc((size_t)K * N * sizeof(uint16_t));
+    if (!w16) return -2;
+    int rc = dequant_impl(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, 1, w16);
+    if (rc == 0) gemm_rows(x, w16, NULL, M, N, K, acc64, 1, out, out_f32);
+    free(w16);
+    return rc;
+}
+
 int orc_w4a16_gemm_rows(int fmt, const uint16_t* x, const int32_t* qweight,
                         const uint16_t* scales, const int32_t* qzeros,
                         const int32_t* g_idx, int M, int N, int K, int G,
@@ -238,7 +310,7 @@ int orc_w4a16_gemm_rows(int fmt, const uint16_t* x, const int32_t* qweight,
     uint16_t* w16 = (uint16_t*)malloc((size_t)K * N * sizeof(uint16_t));
     if (!w16) return -2;
     int rc = orc_dequant(fmt, qweight, scales, qzeros, g_idx, K, N, G, zero_offset, w16);
-    if (rc == 0) gemm_rows(x, w16, rows, nrows, N, K, 1, out, NULL);
+    if (rc == 0) gemm_rows(x, w16, rows, nrows, N, K, 1, 0, out, NULL);
     free(w16);
     return rc;
 }

@@ -33,6 +33,12 @@ float orc_f16_to_f32(uint16_t h);
 void orc_f32_to_f16_array(const float* src, uint16_t* dst, size_t n);
 void orc_f16_to_f32_array(const uint16_t* src, float* dst, size_t n);
 
+/* bfloat16 (bit patterns): f32 -> bf16 round to nearest even (NaN kept), bf16 -> f32 exact. */
+uint16_t orc_f32_to_bf16(float f);
+float orc_bf16_to_f32(uint16_t b);
+void orc_f32_to_bf16_array(const float* src, uint16_t* dst, size_t n);
+void orc_bf16_to_f32_array(const uint16_t* src, float* dst, size_t n);
+
 /* Nibble slot that column n occupies inside an AWQ word:
  * (n%8)/2 + (n%8)%2*4 (crates/triton-dsl/examples/awq_gemm_int4_typed.rs:139-151). */
 int orc_awq_slot(int n);
@@ -80,6 +86,20 @@ int orc_w4a16_gemm(int fmt, const uint16_t* x, const int32_t* qweight,
                    const uint16_t* scales, const int32_t* qzeros, const int32_t* g_idx,
                    int M, int N, int K, int G, int zero_offset, int acc64,
                    uint16_t* out, float* out_f32);
+
+/* The bfloat16 instantiation (x, scales, W and out as bf16 bits): W = RNE_bf16(f32(q - z) *
+ * f32(scale)), out = RNE_bf16(sum_k f32(x) * f32(W)); the reference kernels are generic over
+ * the element type (w4a16_gptq_gemm_typed.rs:65-67). */
+int orc_dequant_bf16(int fmt, const int32_t* qweight, const uint16_t* scales,
+                     const int32_t* qzeros, const int32_t* g_idx, int K, int N, int G,
+                     int zero_offset, uint16_t* out);
+int orc_dequant_transposed_bf16(int fmt, const int32_t* qweight, const uint16_t* scales,
+                                const int32_t* qzeros, const int32_t* g_idx, int K, int N,
+                                int G, int zero_offset, uint16_t* out_nk);
+int orc_w4a16_gemm_bf16(int fmt, const uint16_t* x, const int32_t* qweight,
+                        const uint16_t* scales, const int32_t* qzeros, const int32_t* g_idx,
+                        int M, int N, int K, int G, int zero_offset, int acc64,
+                        uint16_t* out, float* out_f32);
 
 /* Same, restricted to output rows `rows[0..nrows)` (a sample of a large M). */
 int orc_w4a16_gemm_rows(int fmt, const uint16_t* x, const int32_t* qweight,

@@ -149,8 +149,8 @@ def _disassemble_tu(obj, tmp_path):
 
 def test_kernel_choice_evidence_in_isa(tmp_path):
     """The VALU decode GEMVs use v_dot2 and no MFMA; the AWQ matrix-core GEMVs (block-diagonal
-    and row-paired) and the strided GEMM use fp16 MFMA. Every VALU GEMV comes in two hand-off
-    variants (device scope, XCD-local)."""
+    and row-paired) and the strided GEMM use fp16 MFMA, the strided GEMM's bfloat16 instances
+    bf16 MFMA. Every VALU GEMV comes in two hand-off variants (device scope, XCD-local)."""
     bdir = os.path.join(ROOT, "triton-rs_amd", "_build")
     gemv_o, strided_o = os.path.join(bdir, "kernels_gemv.o"), os.path.join(bdir, "kernels_strided.o")
     if not (os.path.exists(gemv_o) and os.path.exists(strided_o)):
@@ -162,14 +162,34 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
                or "gemv_awq_rows_kernel" in k}
     strided = {k: v for k, v in _disassemble_tu(strided_o, tmp_path).items()
                if "strided_gemm_kernel" in k}
-    assert len(gemv) >= 24 and len(gemv_mc) >= 8 and len(strided) == 3
+    assert len(gemv) >= 24 and len(gemv_mc) >= 8 and len(strided) == 6
     for name, body in gemv.items():
         assert "v_mfma" not in body, name
         assert "v_dot2" in body, name
     for name, body in gemv_mc.items():
         assert "v_mfma_f32_16x16x32_f16" in body, name
     for name, body in strided.items():
-        assert "v_mfma_f32_16x16x32_f16" in body, name
+        bf16 = "DF16b" in name        # the __bf16 element type in the mangled name
+        assert ("v_mfma_f32_16x16x32_bf16" if bf16 else "v_mfma_f32_16x16x32_f16") in body, name
+        assert ("v_cvt_pk_bf16_f32" in body) == bf16, name
+
+
+def test_bf16_flag_plans_generic_kernel_and_is_refused_elsewhere():
+    """W4A16_BF16 selects the generic kernel for every shape; entry points without a
+    bfloat16 instantiation report the flagged value as an unknown format (no GPU call)."""
+    P = pkg()
+    L = P.lib()
+    k = ctypes.c_int(0)
+    for M, N, K in ((1, 14336, 4096), (16, 6144, 4096), (2048, 4096, 14336)):
+        assert L.w4a16_gemm_plan(P.FMT_AWQ | P.BF16, M, N, K, 128, 0, ctypes.byref(k)) == P.OK
+        assert P.KERNELS[k.value] == "strided"
+        assert L.w4a16_gemm_plan(P.FMT_AWQ, M, N, K, 128, 0, ctypes.byref(k)) == P.OK
+        assert P.KERNELS[k.value] != "strided"
+    assert L.w4a16_gemm_plan(P.FMT_AWQ | 0x200, 1, 512, 512, 128, 0, ctypes.byref(k)) == \
+        P.ERR_INVALID_ARG
+    assert L.w4a16_prepare_act_order(None, P.FMT_GPTQ | P.BF16, None, None, 1024, 256, 128,
+                                     None, None) == P.ERR_INVALID_ARG
+    assert "fmt" in L.w4a16_last_error().decode()
 
 
 def test_moe_argument_errors():

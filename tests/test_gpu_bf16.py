@@ -1,0 +1,144 @@
+"""GPU parity of the bfloat16 instantiation (W4A16_BF16 flag): dequantised weights bit-exact
+against the oracle, GEMM outputs within the path's 1e-2 bar of the oracle's float64
+accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32.
+The reference kernels are generic over the element type and name bf16
+(w4a16_gptq_gemm_typed.rs:65-67)."""
+import numpy as np
+import pytest
+
+import synth
+from helpers import assert_parity, pkg, to_dev
+from synth import Problem
+
+pytestmark = pytest.mark.gpu
+GPTQ, SYM, AWQ = 0, 1, 2
+FMT_NAME = {GPTQ: "gptq", SYM: "gptq_sym", AWQ: "awq"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def bf16_bits(torch, a) -> np.ndarray:
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16)
+    return t.view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_dev(torch, bits):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+def dev_bits(t) -> np.ndarray:
+    import torch
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dequant_bf16_bit_exact(torch_cuda, orc, fmt, transposed):
+    torch = torch_cuda
+    p = Problem(fmt, M=1, K=512, N=256, G=128, seed=700 + fmt)
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    out = pkg().dequant(to_dev(p.qweight), bf16_dev(torch, s_bits),
+                        None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[fmt],
+                        group_size=p.G, transposed=transposed)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16
+    want = orc.dequant_bf16(fmt, p.qweight, s_bits, p.qzeros, p.K, p.N, p.G, transposed=transposed)
+    assert np.array_equal(dev_bits(out), want)
+
+
+def test_dequant_bf16_act_order_bit_exact(torch_cuda, orc):
+    torch = torch_cuda
+    p = Problem(GPTQ, M=1, K=1024, N=128, G=128, seed=710, act_order=True)
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    out = pkg().dequant(to_dev(p.qweight), bf16_dev(torch, s_bits), to_dev(p.qzeros),
+                        fmt="gptq", group_size=p.G, g_idx=to_dev(p.g_idx))
+    torch.cuda.synchronize()
+    want = orc.dequant_bf16(GPTQ, p.qweight, s_bits, p.qzeros, p.K, p.N, p.G, g_idx=p.g_idx)
+    assert np.array_equal(dev_bits(out), want)
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
+@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (7, 512, 256), (64, 2048, 768),
+                                   (200, 1024, 512), (33, 384, 136)])
+def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N):
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=720 + M + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, p.G, bf16=True) == "strided"
+    x_bits = bf16_bits(torch, p.x.astype(np.float32))
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    y = P.gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
+               None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[fmt], group_size=p.G)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.bfloat16
+    _, ref = orc.w4a16_gemm_bf16(fmt, x_bits, p.qweight, s_bits, p.qzeros, K, N, p.G)
+    assert_parity(y.float().cpu().numpy(), ref, what=f"bf16 fmt={fmt} M={M} K={K} N={N}")
+
+
+def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
+    torch = torch_cuda
+    p = Problem(GPTQ, M=16, K=1024, N=256, G=128, seed=730, act_order=True)
+    x_bits = bf16_bits(torch, p.x.astype(np.float32))
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    y = pkg().gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
+                   to_dev(p.qzeros), fmt="gptq", group_size=p.G, g_idx=to_dev(p.g_idx))
+    torch.cuda.synchronize()
+    _, ref = orc.w4a16_gemm_bf16(GPTQ, x_bits, p.qweight, s_bits, p.qzeros, p.K, p.N, p.G,
+                                 g_idx=p.g_idx)
+    assert_parity(y.float().cpu().numpy(), ref, what="bf16 act-order")
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
+def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt):
+    """x in multiples of 1/2 up to 2, scales 2^-7: every product and partial sum is exact in
+    fp32, so the output is the exact sum rounded once to bf16, identical to the oracle."""
+    torch = torch_cuda
+    M, K, N, G = 9, 256, 128, 64
+    g = np.random.default_rng(740 + fmt)
+    q = g.integers(0, 16, size=(K, N), dtype=np.int32)
+    zq = g.integers(0, 16, size=(K // G, N), dtype=np.int32)
+    if fmt == AWQ:
+        qweight, qzeros = synth.pack_along_n(q, awq=True), synth.pack_along_n(zq, awq=True)
+    else:
+        qweight = synth.pack_gptq_qweight(q)
+        qzeros = synth.pack_along_n(zq, awq=False) if fmt == GPTQ else None
+    x = g.integers(-4, 5, size=(M, K)).astype(np.float32) / 2
+    x_bits = bf16_bits(torch, x)
+    s_bits = bf16_bits(torch, np.full((K // G, N), 2.0 ** -7, dtype=np.float32))
+    y = pkg().gemm(bf16_dev(torch, x_bits), to_dev(qweight), bf16_dev(torch, s_bits),
+                   None if qzeros is None else to_dev(qzeros), fmt=FMT_NAME[fmt], group_size=G)
+    torch.cuda.synchronize()
+    want, _ = orc.w4a16_gemm_bf16(fmt, x_bits, qweight, s_bits, qzeros, K, N, G)
+    assert np.array_equal(dev_bits(y), want)
+
+
+def test_noalloc_bf16_equals_gemm(torch_cuda):
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(AWQ, M=4, K=1024, N=512, G=128, seed=750)
+    x = bf16_dev(torch, bf16_bits(torch, p.x.astype(np.float32)))
+    s = bf16_dev(torch, bf16_bits(torch, p.scales.astype(np.float32)))
+    qw, qz = to_dev(p.qweight), to_dev(p.qzeros)
+    y = P.gemm(x, qw, s, qz, fmt="awq")
+    out = torch.empty_like(y)
+    P.gemm_noalloc(x, qw, s, qz, out, fmt="awq")
+    torch.cuda.synchronize()
+    assert np.array_equal(dev_bits(out), dev_bits(y))
+
+
+def test_bf16_element_types_must_agree(torch_cuda):
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(AWQ, M=2, K=256, N=256, G=128, seed=760)
+    x = to_dev(p.x).to(torch.bfloat16)
+    with pytest.raises(P.InvalidArgument, match="scales has dtype"):
+        P.gemm(x, to_dev(p.qweight), to_dev(p.scales), to_dev(p.qzeros), fmt="awq")
+    with pytest.raises(P.InvalidArgument, match="out"):
+        P.gemm(x, to_dev(p.qweight), to_dev(p.scales).to(torch.bfloat16), to_dev(p.qzeros),
+               fmt="awq", out=torch.empty((2, 256), dtype=torch.float16, device="cuda:0"))

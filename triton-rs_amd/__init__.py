@@ -22,6 +22,7 @@ HSACO_PATH = os.path.join(HERE, "w4a16_typed.hsaco")
 META_PATH = os.path.join(HERE, "w4a16_typed.json")
 
 FMT_GPTQ, FMT_GPTQ_SYM, FMT_AWQ = 0, 1, 2
+BF16 = 0x100   # W4A16_BF16: bfloat16 activations, scales and output (OR-ed into the format)
 FORMATS = {"gptq": FMT_GPTQ, "gptq_sym": FMT_GPTQ_SYM, "awq": FMT_AWQ}
 KERNELS = {1: "gemv", 2: "skinny", 3: "prefill", 4: "strided"}
 
@@ -185,15 +186,17 @@ def _require(t: torch.Tensor, name: str, dtypes, device: torch.device | None = N
 
 _INT32 = (torch.int32,)
 _HALF = (torch.float16,)
+_ELEM = (torch.float16, torch.bfloat16)   # element types of x, scales and out
 
 
-def _gemm_operands(f: int, x, qweight, scales, qzeros, idx, idx_name: str):
+def _gemm_operands(f: int, x, qweight, scales, qzeros, idx, idx_name: str, elem=_HALF):
     """(M, N, K) of a GEMM call after checking dtypes, devices, ranks and contiguity (the C ABI
-    takes contiguous row-major buffers and checks sizes, not layouts)."""
-    _require(x, "x", _HALF)
+    takes contiguous row-major buffers and checks sizes, not layouts). x and scales share one
+    element type out of `elem`."""
+    _require(x, "x", elem)
     dev = x.device
     _require(qweight, "qweight", _INT32, dev)
-    _require(scales, "scales", _HALF, dev)
+    _require(scales, "scales", (x.dtype,), dev)
     if qzeros is not None:
         _require(qzeros, "qzeros", _INT32, dev)
     if idx is not None:
@@ -209,12 +212,13 @@ def _gemm_operands(f: int, x, qweight, scales, qzeros, idx, idx_name: str):
     return M, N, K
 
 
-def _gemm_out(out, M: int, N: int, dev: torch.device, required: bool = False):
+def _gemm_out(out, M: int, N: int, dev: torch.device, required: bool = False,
+              dtype=torch.float16):
     if out is None:
         if required:
             raise InvalidArgument("out must be given")
-        return torch.empty((M, N), dtype=torch.float16, device=dev)
-    _require(out, "out", _HALF, dev)
+        return torch.empty((M, N), dtype=dtype, device=dev)
+    _require(out, "out", (dtype,), dev)
     if tuple(out.shape) != (M, N) or not out.is_contiguous():
         raise InvalidArgument(f"out must be a contiguous [{M}, {N}] tensor")
     return out
@@ -236,27 +240,35 @@ def typed_plan(fmt, m: int, n: int, k: int, group_size: int, strides, aligned16:
     return KERNELS[k_.value]
 
 
-def plan(fmt, M: int, N: int, K: int, group_size: int, has_g_idx: bool = False) -> str:
+def plan(fmt, M: int, N: int, K: int, group_size: int, has_g_idx: bool = False,
+         bf16: bool = False) -> str:
     """Name of the kernel regime w4a16_gemm would choose (no GPU access)."""
     k = ctypes.c_int(0)
-    check(lib().w4a16_gemm_plan(_fmt(fmt), M, N, K, group_size, int(has_g_idx), ctypes.byref(k)))
+    f = _fmt(fmt) | (BF16 if bf16 else 0)
+    check(lib().w4a16_gemm_plan(f, M, N, K, group_size, int(has_g_idx), ctypes.byref(k)))
     return KERNELS[k.value]
+
+
+def _elem_flag(x: torch.Tensor) -> int:
+    return BF16 if x.dtype == torch.bfloat16 else 0
 
 
 def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
          qzeros: torch.Tensor | None, fmt="awq", group_size: int = 128,
          g_idx: torch.Tensor | None = None, out: torch.Tensor | None = None,
          zero_offset: int = 1) -> torch.Tensor:
-    """out[M, N] = x[M, K] @ dequant(qweight) in fp16 with fp32 accumulation.
+    """out[M, N] = x[M, K] @ dequant(qweight) with fp32 accumulation, in fp16 or, when x and
+    scales are bfloat16, in bfloat16 (the generic kernel).
 
     fmt: "gptq" (qweight int32 [K/8, N], qzeros [K/G, N/8], zero = nibble + zero_offset),
     "gptq_sym" (zero = 8, qzeros unused) or "awq" (qweight [K, N/8], AWQ nibble order).
     """
     f = _fmt(fmt)
-    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx")
-    out = _gemm_out(out, M, N, x.device)
-    check(lib().w4a16_gemm(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros),
-                           _ptr(g_idx), _ptr(out), M, N, K, group_size, zero_offset))
+    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx", _ELEM)
+    out = _gemm_out(out, M, N, x.device, dtype=x.dtype)
+    check(lib().w4a16_gemm(_stream(x), f | _elem_flag(x), _ptr(x), _ptr(qweight), _ptr(scales),
+                           _ptr(qzeros), _ptr(g_idx), _ptr(out), M, N, K, group_size,
+                           zero_offset))
     return out
 
 
@@ -292,21 +304,22 @@ def gemm_noalloc(x, qweight, scales, qzeros, out, fmt="awq", group_size: int = 1
     """w4a16_gemm_noalloc: as gemm(), but the library allocates nothing during the call (its
     split-K scratch is a fixed per-device array); `out` must be given."""
     f = _fmt(fmt)
-    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx")
-    out = _gemm_out(out, M, N, x.device, required=True)
-    check(lib().w4a16_gemm_noalloc(_stream(x), f, _ptr(x), _ptr(qweight), _ptr(scales),
-                                   _ptr(qzeros), _ptr(g_idx), _ptr(out), M, N, K, group_size,
-                                   zero_offset))
+    M, N, K = _gemm_operands(f, x, qweight, scales, qzeros, g_idx, "g_idx", _ELEM)
+    out = _gemm_out(out, M, N, x.device, required=True, dtype=x.dtype)
+    check(lib().w4a16_gemm_noalloc(_stream(x), f | _elem_flag(x), _ptr(x), _ptr(qweight),
+                                   _ptr(scales), _ptr(qzeros), _ptr(g_idx), _ptr(out), M, N, K,
+                                   group_size, zero_offset))
     return out
 
 
 def dequant(qweight, scales, qzeros, fmt="gptq", K: int | None = None, group_size: int = 128,
             g_idx=None, zero_offset: int = 1, transposed: bool = False) -> torch.Tensor:
-    """W16 as fp16, [K, N] (or [N, K] when transposed)."""
+    """The dequantised weights, [K, N] (or [N, K] when transposed), in the scales' element
+    type (fp16, or bfloat16: RNE_bf16((q - z) * s))."""
     f = _fmt(fmt)
     _require(qweight, "qweight", _INT32)
     dev = qweight.device
-    _require(scales, "scales", _HALF, dev)
+    _require(scales, "scales", _ELEM, dev)
     if qzeros is not None:
         _require(qzeros, "qzeros", _INT32, dev)
     if g_idx is not None:
@@ -318,10 +331,10 @@ def dequant(qweight, scales, qzeros, fmt="gptq", K: int | None = None, group_siz
         K, N = qweight.shape[0], qweight.shape[1] * 8
     else:
         K, N = qweight.shape[0] * 8, qweight.shape[1]
-    out = torch.empty((N, K) if transposed else (K, N), dtype=torch.float16, device=qweight.device)
-    check(lib().w4a16_dequant(_stream(qweight), f, _ptr(qweight), _ptr(scales), _ptr(qzeros),
-                              _ptr(g_idx), _ptr(out), K, N, group_size, zero_offset,
-                              int(transposed)))
+    out = torch.empty((N, K) if transposed else (K, N), dtype=scales.dtype, device=qweight.device)
+    check(lib().w4a16_dequant(_stream(qweight), f | _elem_flag(scales), _ptr(qweight),
+                              _ptr(scales), _ptr(qzeros), _ptr(g_idx), _ptr(out), K, N,
+                              group_size, zero_offset, int(transposed)))
     return out
 
 

@@ -232,10 +232,12 @@ W4A16_API int w4a16_init(int32_t device) {
 
 W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t G, int has_g_idx,
                               int* kernel) {
+    const bool bf16 = (fmt & W4A16_BF16) != 0;
+    fmt &= ~W4A16_BF16;
     int rc = check_gemm_args(fmt, (void*)1, (void*)1, (void*)1, (void*)1, (void*)1, M, N, K, G);
     if (rc) return rc;
     if (!kernel) return fail(W4A16_ERR_INVALID_ARG, "kernel out-pointer is null");
-    *kernel = plan(fmt, M, N, K, G, has_g_idx != 0);
+    *kernel = bf16 ? W4A16_KERNEL_STRIDED : plan(fmt, M, N, K, G, has_g_idx != 0);
     return W4A16_OK;
 }
 
@@ -260,6 +262,8 @@ ScratchSource alloc_scratch_source() { return ScratchSource{SIZE_MAX, SPLITK_MAX
 int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const void* scales,
               const void* qzeros, const int32_t* g_idx, void* out, int32_t M, int32_t N,
               int32_t K, int32_t G, int32_t zero_offset, const ScratchSource& src) {
+    const bool bf16 = (fmt & W4A16_BF16) != 0;
+    fmt &= ~W4A16_BF16;
     int rc = check_gemm_args(fmt, x, qweight, scales, qzeros, out, M, N, K, G);
     if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
@@ -269,7 +273,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
                         (!g_idx || aligned(g_idx, 16));
     const int cus = device_cus();
     int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
-    if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
+    if (!vec_ok || bf16) kernel = W4A16_KERNEL_STRIDED;   // bf16: the generic kernel only
     // the placement probe allocates: sources that must not allocate use what is cached
     const bool xcd = src.may_probe ? xcd_placement(st) : xcd_placement_cached();
     auto scratch_for = [&](size_t tiles, size_t partial_bytes, Scratch* sc) -> int {
@@ -375,7 +379,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     p.stride_sk = N; p.stride_sn = 1;
     p.stride_qzk = N / 8; p.stride_qzn = 1;
     p.stride_cm = N; p.stride_cn = 1;
-    hipError_t e = launch_strided_gemm(fmt, p, st);
+    hipError_t e = launch_strided_gemm(fmt, p, st, bf16);
     if (e != hipSuccess) return hip_fail(e, "strided gemm launch");
     return W4A16_OK;
 }
@@ -554,6 +558,8 @@ W4A16_API int awq_gemm_int4_typed(void* stream, const void* a_ptr, const void* q
 static int dequant_common(void* stream, int fmt, const void* qweight, const void* scales,
                           const void* qzeros, const int32_t* g_idx, void* out, int32_t K,
                           int32_t N, int32_t G, int32_t zero_offset, int transposed) {
+    const bool bf16 = (fmt & W4A16_BF16) != 0;
+    fmt &= ~W4A16_BF16;
     int rc = check_gemm_args(fmt, (void*)1, qweight, scales, qzeros, out, 1, N, K, G);
     if (!rc) rc = check_zero_offset(fmt, zero_offset);
     if (rc) return rc;
@@ -568,7 +574,7 @@ static int dequant_common(void* stream, int fmt, const void* qweight, const void
     p.g_idx = g_idx;
     p.out = static_cast<half_t*>(out);
     p.K = K; p.N = N; p.G = G; p.zero_offset = zero_offset; p.transposed = transposed;
-    hipError_t e = launch_dequant(fmt, p, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_dequant(fmt, p, static_cast<hipStream_t>(stream), bf16);
     if (e != hipSuccess) return hip_fail(e, "dequant launch");
     return W4A16_OK;
 }

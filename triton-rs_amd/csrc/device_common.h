@@ -17,6 +17,8 @@ typedef _Float16 half_t;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16_t;
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
 constexpr int FMT_GPTQ = 0;
@@ -89,6 +91,26 @@ __device__ __forceinline__ int zero_of(uint32_t qz_word, int n, int zero_offset)
 __device__ __forceinline__ half_t dequant1(int q, int z, half_t s) {
     return (half_t)(q - z) * s;
 }
+
+// The same for bfloat16 elements (the reference's kernels are generic over the element type,
+// w4a16_gptq_gemm_typed.rs:65-67): RNE_bf16(f32(q - z) * f32(s)); a 5-bit integer times an
+// 8-bit significand is exact in f32, so the only rounding is the final one to bf16.
+__device__ __forceinline__ bf16_t dequant1(int q, int z, bf16_t s) {
+    return (bf16_t)((float)(q - z) * (float)s);
+}
+
+// v_mfma_f32_16x16x32 for either element type
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ float4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, float4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 8-element vector of an element type
+template <typename E> struct vec8;
+template <> struct vec8<half_t> { typedef half8_t type; };
+template <> struct vec8<bf16_t> { typedef bf16x8_t type; };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

@@ -173,7 +173,8 @@ struct StridedParams {
     int stride_qzk, stride_qzn, stride_cm, stride_cn;
     int zero_offset;
 };
-hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st);
+// bf16: activations, scales and output are bfloat16 (same layouts)
+hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st, bool bf16 = false);
 
 // Standalone dequant to a transposed fp16 [N, K] matrix
 // (ferrum_dequant_int4.rs:27-139, ferrum_dequant_int4_sym.rs:24-131), and a row-major
@@ -187,7 +188,7 @@ struct DequantParams {
     int K, N, G, zero_offset;
     int transposed;
 };
-hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st);
+hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st, bool bf16 = false);
 
 // Act-order in group order (act_order.hip): qout = rows of the GPTQ qweight q [K/8, N] taken
 // in the order perm (row j of qout = row perm[j] of q); xout [M, K] = x[:, perm].

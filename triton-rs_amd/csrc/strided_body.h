@@ -1,6 +1,8 @@
 // Generic strided W4A16 GEMM: the reference kernels' full parameter list (any strides,
 // any M/N/K, masked tails), with the dequantised tile staged in LDS and fed to
-// v_mfma_f32_16x16x32_f16.
+// v_mfma_f32_16x16x32_f16 (E = half_t) or v_mfma_f32_16x16x32_bf16 (E = bf16_t: activations,
+// scales and output in bfloat16, W = RNE_bf16((q - z) * s); the reference kernels are generic
+// over the element type, w4a16_gptq_gemm_typed.rs:65-67).
 //
 // Semantics follow crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:130-273 and
 // awq_gemm_int4_typed.rs:116-241: W16 = RNE_f16((q - z) * s) element by element (bit-exact
@@ -17,10 +19,14 @@ namespace w4a16 {
 constexpr int STR_BM = 64, STR_BN = 64, STR_BK = 32;
 constexpr int STR_LDA = STR_BK + 8;  // halfs per LDS row (pad: 80-byte rows)
 
-template <int FMT>
+template <int FMT, typename E = half_t>
 __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
-    __shared__ __attribute__((aligned(16))) half_t As[STR_BM][STR_LDA];
-    __shared__ __attribute__((aligned(16))) half_t Bs[STR_BN][STR_LDA];   // [n][k]
+    typedef typename vec8<E>::type e8_t;
+    __shared__ __attribute__((aligned(16))) E As[STR_BM][STR_LDA];
+    __shared__ __attribute__((aligned(16))) E Bs[STR_BN][STR_LDA];   // [n][k]
+    const E* pa = reinterpret_cast<const E*>(p.a);
+    const E* ps = reinterpret_cast<const E*>(p.scales);
+    E* pc = reinterpret_cast<E*>(p.c);
 
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -40,20 +46,20 @@ __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
 
     for (int kb = 0; kb < p.k; kb += STR_BK) {
         // ---- A tile
-        half_t av[8];
+        E av[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int kk = kb + a_k + i;
             av[i] = (gm < p.m && kk < p.k)
-                        ? p.a[(int64_t)gm * p.stride_am + (int64_t)kk * p.stride_ak]
-                        : (half_t)0.f;
+                        ? pa[(int64_t)gm * p.stride_am + (int64_t)kk * p.stride_ak]
+                        : (E)0.f;
         }
         // ---- B tile: dequantise 8 consecutive k of column gn
-        half_t bv[8];
+        E bv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             const int kk = kb + b_k + i;
-            half_t v = (half_t)0.f;
+            E v = (E)0.f;
             if (gn < p.n && kk < p.k) {
                 uint32_t word;
                 int slot;
@@ -71,32 +77,32 @@ __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
                 uint32_t qz = 0;
                 if constexpr (FMT != FMT_GPTQ_SYM)
                     qz = p.qzeros[(int64_t)g * p.stride_qzk + (int64_t)(gn >> 3) * p.stride_qzn];
-                const half_t s = p.scales[(int64_t)g * p.stride_sk + (int64_t)gn * p.stride_sn];
+                const E s = ps[(int64_t)g * p.stride_sk + (int64_t)gn * p.stride_sn];
                 v = dequant1(nib(word, slot), zero_of<FMT>(qz, gn, p.zero_offset), s);
             }
             bv[i] = v;
         }
         __syncthreads();   // previous iteration's MFMA reads are done
-        *reinterpret_cast<half8_t*>(&As[a_row][a_k]) =
-            half8_t{av[0], av[1], av[2], av[3], av[4], av[5], av[6], av[7]};
-        *reinterpret_cast<half8_t*>(&Bs[b_col][b_k]) =
-            half8_t{bv[0], bv[1], bv[2], bv[3], bv[4], bv[5], bv[6], bv[7]};
+        *reinterpret_cast<e8_t*>(&As[a_row][a_k]) =
+            e8_t{av[0], av[1], av[2], av[3], av[4], av[5], av[6], av[7]};
+        *reinterpret_cast<e8_t*>(&Bs[b_col][b_k]) =
+            e8_t{bv[0], bv[1], bv[2], bv[3], bv[4], bv[5], bv[6], bv[7]};
         __syncthreads();
 
         // ---- 2 x 2 MFMA 16x16x32 per wave (wave tile 32 x 32)
         const int fr = lane & 15, fk = (lane >> 4) * 8;
-        half8_t af[2], bf[2];
+        e8_t af[2], bf[2];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            af[i] = *reinterpret_cast<const half8_t*>(&As[wm * 32 + i * 16 + fr][fk]);
+            af[i] = *reinterpret_cast<const e8_t*>(&As[wm * 32 + i * 16 + fr][fk]);
 #pragma unroll
         for (int j = 0; j < 2; ++j)
-            bf[j] = *reinterpret_cast<const half8_t*>(&Bs[wn * 32 + j * 16 + fr][fk]);
+            bf[j] = *reinterpret_cast<const e8_t*>(&Bs[wn * 32 + j * 16 + fr][fk]);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
     }
 
     // ---- store: lane holds D[4*(lane/16) + r][lane%16]
@@ -109,7 +115,7 @@ __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
                 const int row = m0 + wm * 32 + i * 16 + (lane >> 4) * 4 + r;
                 const int col = n0 + wn * 32 + j * 16 + (lane & 15);
                 if (row < p.m && col < p.n)
-                    p.c[(int64_t)row * p.stride_cm + (int64_t)col * p.stride_cn] = (half_t)acc[i][j][r];
+                    pc[(int64_t)row * p.stride_cm + (int64_t)col * p.stride_cn] = (E)acc[i][j][r];
             }
 }
 
