@@ -104,6 +104,7 @@ def test_gemv_group_sizes(torch_cuda, orc, fmt, G):
     (AWQ, 1, 4096, 14336),         # config 1: gate/up
     (AWQ, 1, 14336, 4096),         # config 1: down
     (AWQ, 4, 4096, 14336),
+    (AWQ, 4, 14336, 4096),         # config 1, M=4, down (its own grid: 16 tiles x 14 splits)
 ])
 def test_gemv_full_size(torch_cuda, orc, fmt, M, K, N):
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0x5EED0000 + (0 if fmt == SYM else 1))
@@ -233,6 +234,20 @@ def test_mfma_full_size(torch_cuda, orc, fmt, M, K, N):
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0x5EED0000 + (1 if fmt == AWQ else 2))
     y = _run_gemm(torch_cuda, p)
     assert_parity(y, _oracle(orc, p), what=f"full fmt={fmt} M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [
+    (GPTQ, 64, 2048, 1024),        # 8 waves, one workgroup per strip
+    (SYM, 48, 4096, 2048),         # 8 waves, K split across workgroups
+    (GPTQ, 40, 1152, 1024),        # K not a multiple of 256: 4 waves
+    (SYM, 64, 384, 512),           # 4 waves
+])
+def test_small_batch_64_row_tiles_both_wave_counts(torch_cuda, orc, fmt, M, K, N):
+    """64-row small-batch tiles run 8 waves (two rounds of LDS reduction) where K is a
+    multiple of 256 per split, else 4 waves."""
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0x5EED6400 + M + K)
+    y = _run_gemm(torch_cuda, p)
+    assert_parity(y, _oracle(orc, p), what=f"64-row tile fmt={fmt} M={M} K={K} N={N}")
 
 
 @pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])

@@ -160,6 +160,29 @@ def test_fused_moe_config4_sampled_tokens(torch_cuda, orc):
     assert_parity(y[toks], ref.astype(np.float64), what="config 4 sampled tokens")
 
 
+def _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, what):
+    """The oracle recomputes up to 5 sampled tokens (first, last, three random ones) of a
+    fused layer through the dequantised weights of their experts."""
+    host = lambda a: a.cpu().numpy() if hasattr(a, "cpu") else np.asarray(a)
+    xs, ls = host(x), host(logits)
+    T, K = xs.shape
+    E = ls.shape[1]
+    h13 = [None if a is None else host(a) for a in w13]
+    h2 = [None if a is None else host(a) for a in w2]
+    I = h2[1].shape[1] * G
+    toks = np.unique(np.concatenate([[0, T - 1], g.integers(0, T, size=3)]))
+    ids, w = orc.moe_route(ls, topk)
+    used = set(ids[toks].ravel().tolist())
+    dummy = np.zeros((8, 8), dtype=np.float16)
+    w13d = [orc.dequant(fmt, h13[0][e], h13[1][e], None if h13[2] is None else h13[2][e], K, 2 * I, G)
+            if e in used else dummy for e in range(E)]
+    w2d = [orc.dequant(fmt, h2[0][e], h2[1][e], None if h2[2] is None else h2[2][e], I, K, G)
+           if e in used else dummy for e in range(E)]
+    ref = orc.moe_forward(np.ascontiguousarray(xs[toks]), np.ascontiguousarray(ids[toks]),
+                          np.ascontiguousarray(w[toks]), w13d, w2d, inter=I)
+    assert_parity(host(y)[toks], ref.astype(np.float64), what=f"{what}, tokens {toks.tolist()}")
+
+
 def _layer_by_pieces(P, x, logits, w13, w2, topk, fmt, G, block_m):
     """The layer composed from the public pieces: route, align, grouped GEMM over block_m
     blocks, silu*mul, grouped GEMM, weighted sum."""
@@ -196,7 +219,7 @@ TILE_CASES = [
 
 @pytest.mark.parametrize("case", TILE_CASES, ids=[f"T{c[0]}_E{c[1]}_I{c[4]}_skew{c[5]}"
                                                   for c in TILE_CASES])
-def test_fused_layer_expert_tiles_equal_block_composition(torch_cuda, case):
+def test_fused_layer_expert_tiles_equal_block_composition(torch_cuda, orc, case):
     torch = torch_cuda
     T, E, topk, K, I, skew, fmt, bm = case
     P = pkg()
@@ -218,6 +241,7 @@ def test_fused_layer_expert_tiles_equal_block_composition(torch_cuda, case):
     got, want = y.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16)
     diff = np.argwhere(got != want)
     assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
+    _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, f"tile case {case}")
     assert np.all(np.isfinite(y.cpu().numpy()))
 
 
@@ -257,9 +281,10 @@ def _moe_cases(n=10, seed=77):
 
 
 @pytest.mark.parametrize("case", _moe_cases(), ids=lambda c: "T{}_E{}_k{}_K{}_I{}_f{}".format(*c))
-def test_fused_layer_random_shapes_equal_block_composition(torch_cuda, case):
+def test_fused_layer_random_shapes_equal_block_composition(torch_cuda, orc, case):
     """Seeded random layers (token counts 1..700, 2..32 experts, top-1..4): the expert-tile
-    layer equals the block_m composition of the pieces bit for bit."""
+    layer equals the block_m composition of the pieces bit for bit, and the oracle recomputes
+    up to 5 sampled tokens (first, last and three random ones) through their experts."""
     torch = torch_cuda
     T, E, topk, K, I, fmt = case
     P = pkg()
@@ -277,3 +302,4 @@ def test_fused_layer_random_shapes_equal_block_composition(torch_cuda, case):
     got, want = y.cpu().numpy().view(np.uint16), ref.cpu().numpy().view(np.uint16)
     diff = np.argwhere(got != want)
     assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
+    _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, f"random layer {case}")

@@ -53,20 +53,25 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 // RG (plain group order): every ring round of PF steps lies in one group (G % (32 PF) == 0
 // and steps_per_wave % PF == 0), so the round's first slot alone loads the scales and zeros,
 // and the zero points and scales are splatted once per round instead of once per step.
-template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false>
-__global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel(SkinnyParams p) {
+// WV: waves per workgroup when it differs from skinny_waves (8 for 64-row GPTQ tiles, chosen
+// on the host where K allows); 0 for the default.
+template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false, int WV = 0>
+__global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) skinny_kernel(SkinnyParams p) {
     static_assert(!RG || !GIDX, "one group per round needs plain group order");
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
                   "columns per lane");
-    constexpr int W = skinny_waves(FMT, BM, CPL), NT = 64 * W;
+    constexpr int W = WV ? WV : skinny_waves(FMT, BM, CPL), NT = 64 * W;
+    // 64-row tiles of 8 waves reduce in two rounds through a 4-wave buffer (the single-round
+    // buffer would take 133 KB of LDS)
+    constexpr int RW = (BM == 64 && W == 8) ? 4 : W;
     static_assert(NT <= FINISH_MAX_THREADS, "split-K finish buffer");
     constexpr int RB = BM / 16;
     constexpr int WN = 16 * CPL;
     constexpr int WPS = (FMT == FMT_AWQ) ? 8 : CPL;   // packed words per lane per k32 step
     constexpr int SW = (CPL + 1) / 2;                  // scale words (2 halfs each) per lane
 
-    __shared__ float red[W][BM][WN + 1];
+    __shared__ float red[RW][BM][WN + 1];
     __shared__ int flag;
     // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16), then (GIDX = 2) the g_idx of the
     // workgroup's W * spw * 32 rows
@@ -388,19 +393,44 @@ __global__ void __launch_bounds__(64 * skinny_waves(FMT, BM, CPL)) skinny_kernel
         if (u < rest) compute(u);
 
     // ------------------------------------------------ reduce the W waves' K ranges
+    if constexpr (RW < W) {
+        // round 1: the upper waves hand their sums to the lower ones
+        if (wave >= RW) {
 #pragma unroll
-    for (int r = 0; r < RB; ++r)
+            for (int r = 0; r < RB; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) red[wave][16 * r + 4 * kb + i][CPL * j + c] = acc[r][c][i];
+                    for (int c = 0; c < CPL; ++c)
+                        red[wave - RW][16 * r + 4 * kb + i][CPL * j + c] = acc[r][c][i];
+        }
+        __syncthreads();
+        if (wave < RW) {
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c)
+                        acc[r][c][i] += red[wave][16 * r + 4 * kb + i][CPL * j + c];
+        }
+        __syncthreads();
+    }
+    if (wave < RW) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) red[wave][16 * r + 4 * kb + i][CPL * j + c] = acc[r][c][i];
+    }
     __syncthreads();
     for (int o = threadIdx.x; o < BM * WN; o += NT) {
         const int m = o / WN, col = o - m * WN;
         if (m >= p.M) continue;
         float v = red[0][m][col];
 #pragma unroll
-        for (int w = 1; w < W; ++w) v += red[w][m][col];
+        for (int w = 1; w < RW; ++w) v += red[w][m][col];
         const size_t off = (size_t)m * p.N + n0 + col;
         if (p.splits == 1) p.out[off] = (half_t)v;
         else st_partial<SC>(p.ws + (size_t)split * p.M * p.N + off, v);
@@ -465,9 +495,16 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
            2 * quads * 32 * M <= K && more(quads))
         quads *= 2;
     const int wq = skinny_waves(fmt, s.bm, cpl) / 4;
-    const int splits = quads >= wq ? quads / wq : 1;
+    int splits = quads >= wq ? quads / wq : 1;
+    s.waves = skinny_waves(fmt, s.bm, cpl);
+    // 64-row GPTQ tiles: 8 waves over the same workgroups (two waves per SIMD instead of one,
+    // each with half the K range) where K divides
+    if (s.bm == 64 && !awq && cpl < 8 && K % (256 * quads) == 0) {
+        s.waves = 8;
+        splits = quads;
+    }
     s.splits = splits;
-    s.steps_per_wave = K / (32 * skinny_waves(fmt, s.bm, cpl) * splits);
+    s.steps_per_wave = K / (32 * s.waves * splits);
     // act-order: the workgroup's g_idx slice joins the table in LDS where the budget allows
     if (gidx && s.lds + (size_t)(K / splits) * sizeof(int32_t) <= SKINNY_GIDX_MAX_LDS) {
         s.gidx_lds = true;
@@ -478,9 +515,11 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     return s;
 }
 
-template <int FMT, int BM, int CPL, bool XCD>
-static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
-    constexpr int PF = FMT == FMT_AWQ ? 3 : 4;
+template <int FMT, int BM, int CPL, bool XCD, int WV>
+static hipError_t launch_xw(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    // 8-wave 64-row tiles keep a 2-step ring: two waves per SIMD need <= 256 registers
+    constexpr int PF = FMT == FMT_AWQ ? 3 : WV == 8 ? 2 : 4;
+    constexpr int NTH = 64 * (WV ? WV : skinny_waves(FMT, BM, CPL));
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     if constexpr (FMT != FMT_AWQ) {
         if (p.g_idx) {
@@ -492,32 +531,40 @@ static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStrea
                 const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)SKINNY_GIDX_MAX_LDS);
                 if (attr != hipSuccess) return attr;
-                hipLaunchKernelGGL(kern, grid, dim3(64 * skinny_waves(FMT, BM, CPL)), s.lds, st, p);
+                hipLaunchKernelGGL(kern, grid, dim3(NTH), s.lds, st, p);
                 return hipGetLastError();
             };
             if (s.gidx_lds) {
-                if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, PF>);
-                return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, 0>);
+                if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, PF, false, WV>);
+                return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, 0, false, WV>);
             }
-            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, PF>);
-            return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, 0>);
+            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, PF, false, WV>);
+            return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, 0, false, WV>);
         }
     }
     if constexpr (FMT != FMT_AWQ) {
         // one group per ring round (RG): the wave's rounds start on multiples of 32 PF rows
         const bool rg = p.G % (32 * PF) == 0 && s.steps_per_wave % PF == 0;
         if (s.steps_per_wave == PF) {   // as above: M=16, 4096 -> 6144 9.4 -> 8.6 us
-            if (rg) hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, true>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
-            else hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            if (rg) hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, true, WV>), grid, dim3(NTH), 0, st, p);
+            else hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, false, WV>), grid, dim3(NTH), 0, st, p);
             return hipGetLastError();
         }
         if (rg) {
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, true>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, true, WV>), grid, dim3(NTH), 0, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0>), grid, dim3(64 * skinny_waves(FMT, BM, CPL)), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, false, WV>), grid, dim3(NTH), 0, st, p);
     return hipGetLastError();
+}
+
+template <int FMT, int BM, int CPL, bool XCD>
+static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    if constexpr (BM == 64 && FMT != FMT_AWQ && CPL < 8) {
+        if (s.waves == 8) return launch_xw<FMT, BM, CPL, XCD, 8>(p, s, st);
+    }
+    return launch_xw<FMT, BM, CPL, XCD, 0>(p, s, st);
 }
 
 template <int FMT, int BM, int CPL>

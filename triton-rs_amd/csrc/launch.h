@@ -149,6 +149,7 @@ struct SkinnyShape {
     bool xcd;               // all splits of a tile on one XCD, hand-off in its L2 (splitk.h)
     bool gidx_lds;          // act-order: the workgroup's g_idx slice staged in LDS too
     int bm, cpl, col_tiles, splits, steps_per_wave;
+    int waves;              // waves per workgroup
     size_t lds;             // dynamic LDS bytes (act-order group table, g_idx slice)
 };
 
