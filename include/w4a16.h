@@ -239,6 +239,11 @@ W4A16_API int w4a16_moe_gemm(void* stream, int fmt, const void* a, int32_t a_div
 W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, void* out,
                                              int32_t inter, int32_t total);
 
+/* replaces fused_silu_mul_interleaved_f32 (crates/triton-kernels/src/elementwise.rs:214-250):
+ * the same indexing over f32 buffers, out[idx] = silu(g) * u in f32. Same argument rules. */
+W4A16_API int fused_silu_mul_interleaved_f32(void* stream, const float* gate_up, float* out,
+                                             int32_t inter, int32_t total);
+
 /* out[t, :] = f16(sum_j topk_weights[t, j] * f32 y_pairs[t * topk + j, :]); K % 8 == 0. */
 W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk_weights,
                             void* out, int32_t T, int32_t topk, int32_t K);

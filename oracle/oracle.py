@@ -62,6 +62,10 @@ def _declare(L: ctypes.CDLL) -> None:
     L.orc_moe_forward.argtypes = [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P]
     L.orc_silu_mul_f16.restype = ctypes.c_uint16
     L.orc_silu_mul_f16.argtypes = [ctypes.c_uint16, ctypes.c_uint16]
+    L.orc_silu_mul_f32.restype = ctypes.c_float
+    L.orc_silu_mul_f32.argtypes = [ctypes.c_float, ctypes.c_float]
+    L.orc_silu_mul_f32_rows.restype = None
+    L.orc_silu_mul_f32_rows.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int64]
     L.orc_f32_to_bf16.restype = ctypes.c_uint16
     L.orc_f32_to_bf16.argtypes = [ctypes.c_float]
     L.orc_bf16_to_f32.restype = ctypes.c_float
@@ -279,6 +283,14 @@ def silu_mul_f16(g, u) -> np.ndarray:
     L = lib()
     return np.array([L.orc_silu_mul_f16(int(a), int(b)) for a, b in zip(g, u)],
                     dtype=np.uint16).view(np.float16)
+
+
+def silu_mul_f32_rows(gate_up, inter, total) -> np.ndarray:
+    """fused_silu_mul_interleaved_f32 over a flat float32 buffer (elementwise.rs:214-250)."""
+    gu = np.ascontiguousarray(gate_up, dtype=np.float32).ravel()
+    out = np.empty(total, dtype=np.float32)
+    lib().orc_silu_mul_f32_rows(_ptr(gu), _ptr(out), int(inter), int(total))
+    return out
 
 
 def num_threads() -> int:

@@ -367,6 +367,21 @@ int orc_moe_align(const int32_t* ids, int T, int topk, int E, int block_m,
     return total;
 }
 
+/* crates/triton-kernels/src/elementwise.rs:214-250: denom = exp(-g) + 1, silu = g / denom,
+ * out = silu * u, every step in f32. */
+float orc_silu_mul_f32(float g, float u) {
+    const float denom = expf(-g) + 1.0f;
+    const float s = g / denom;
+    return s * u;
+}
+
+void orc_silu_mul_f32_rows(const float* gate_up, float* out, int inter, int64_t total) {
+    for (int64_t i = 0; i < total; ++i) {
+        const int64_t b = i / inter, c = i % inter;
+        out[i] = orc_silu_mul_f32(gate_up[b * 2 * inter + c], gate_up[b * 2 * inter + inter + c]);
+    }
+}
+
 uint16_t orc_silu_mul_f16(uint16_t g, uint16_t u) {
     const float gf = h2f(g);
     const float s = gf / (1.0f + expf(-gf));

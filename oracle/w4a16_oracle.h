@@ -136,6 +136,11 @@ void orc_moe_forward(const uint16_t* x, int T, int K, int I, int E, int topk,
 /* silu(g) * u in f32 with the result rounded to f16 (crates/triton-kernels/src/
  * elementwise.rs:188-250 computes silu(x) = x / (1 + exp(-x)) in f32). */
 uint16_t orc_silu_mul_f16(uint16_t g, uint16_t u);
+/* The f32 twin (elementwise.rs:214-250), and the same over the interleaved layout: out[i]
+ * for i < total, b = i / inter, from gate_up[b * 2 * inter + i % inter] and the element
+ * inter further on. */
+float orc_silu_mul_f32(float g, float u);
+void orc_silu_mul_f32_rows(const float* gate_up, float* out, int inter, int64_t total);
 
 /* Threads OpenMP will use (1 when built without OpenMP). */
 int orc_num_threads(void);

@@ -93,6 +93,10 @@ extern "C" {
                        w13_scales: u64, w13_qzeros: u64, w2_qweight: u64, w2_scales: u64,
                        w2_qzeros: u64, group_size: i32, block_m: i32, gptq_zero_offset: i32,
                        workspace: u64, workspace_bytes: usize, out: u64) -> i32;
+    fn fused_silu_mul_interleaved_f16(stream: *mut c_void, gate_up: u64, out: u64, inter: i32,
+                                      total: i32) -> i32;
+    fn fused_silu_mul_interleaved_f32(stream: *mut c_void, gate_up: u64, out: u64, inter: i32,
+                                      total: i32) -> i32;
 }
 
 /// The calling thread's last libw4a16 message, mapped onto the reference's error type:
@@ -354,6 +358,21 @@ pub fn fused_moe(stream: &HipStream, fmt: Format, s: &MoeShape, x: u64, router_l
                         w13.qzeros, w2.qweight, w2.scales, w2.qzeros, s.group_size, s.block_m,
                         gptq_zero_offset, workspace, workspace_bytes, out)
     })
+}
+
+/// `fused_silu_mul_interleaved_f16` (elementwise.rs:188-212): `out[b*inter+i] =
+/// f16(silu(g) * u)`, `g = gate_up[b*2*inter+i]`, `u = gate_up[b*2*inter+inter+i]`.
+pub fn silu_mul_interleaved_f16(stream: &HipStream, gate_up: u64, out: u64, inter: i32,
+                                total: i32) -> Result<(), RuntimeError> {
+    // SAFETY: device pointers from hiprt_malloc; the library validates the sizes.
+    check(unsafe { fused_silu_mul_interleaved_f16(stream.0, gate_up, out, inter, total) })
+}
+
+/// `fused_silu_mul_interleaved_f32` (elementwise.rs:214-250): the same over f32 buffers.
+pub fn silu_mul_interleaved_f32(stream: &HipStream, gate_up: u64, out: u64, inter: i32,
+                                total: i32) -> Result<(), RuntimeError> {
+    // SAFETY: as above.
+    check(unsafe { fused_silu_mul_interleaved_f32(stream.0, gate_up, out, inter, total) })
 }
 
 #[cfg(test)]

@@ -216,6 +216,10 @@ def test_moe_argument_errors():
     assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, -1) == P.ERR_INVALID_ARG
     # any inter and a total that is not a multiple of it are the reference's domain
     assert L.fused_silu_mul_interleaved_f16(None, v, v, 100, 0) == P.OK
+    assert L.fused_silu_mul_interleaved_f32(None, v, v, 0, 250) == P.ERR_INVALID_ARG
+    assert L.fused_silu_mul_interleaved_f32(None, v, v, 100, -1) == P.ERR_INVALID_ARG
+    assert L.fused_silu_mul_interleaved_f32(None, None, v, 100, 10) == P.ERR_INVALID_ARG
+    assert L.fused_silu_mul_interleaved_f32(None, v, v, 100, 0) == P.OK
     assert L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64) > 512 * 2 * 14336 * 2
     ws = L.w4a16_fused_moe_workspace_size(512, 8, 2, 14336, 4096, 64)
     rc = L.w4a16_fused_moe(None, 0, v, v, 512, 4096, 14336, 8, 2, 1, v, v, v, v, v, v, 128, 64, 1,

@@ -340,6 +340,38 @@ def test_grouped_gemm_skips_out_of_range_expert_and_pair_ids(torch_cuda, orc):
 # ------------------------------------------------------------------ silu * mul
 
 @pytest.mark.parametrize("rows,inter,total_cut,offset", [
+    (33, 1024, 0, 0),      # four outputs per thread
+    (7, 100, 0, 0),        # inter a multiple of 4, not of 8
+    (5, 1023, 0, 0),       # odd inter
+    (5, 1024, 0, 1),       # unaligned pointers (one element in)
+    (6, 96, 37, 0),        # total not a multiple of inter: the last row cut short
+    (3, 1, 0, 0),
+])
+def test_silu_mul_f32_entry_point(torch_cuda, orc, rows, inter, total_cut, offset):
+    """fused_silu_mul_interleaved_f32 (elementwise.rs:214-250) against the oracle: both compute
+    exp(-g) + 1, a division and a product in f32; the device and host expf may differ by an
+    ulp, which moves the result by a few f32 ulps at most."""
+    torch = torch_cuda
+    P = pkg()
+    g = np.random.default_rng(3400 + inter + offset)
+    gu = (g.standard_normal((rows, 2 * inter)) * 4).astype(np.float32)
+    special = np.array([0.0, 100.0, -100.0, 30.0], dtype=np.float32)   # zero, saturation,
+    gu[0, :min(4, inter)] = special[:min(4, inter)]                    # overflow of exp(-g)
+    total = rows * inter - total_cut
+    buf = torch.zeros(rows * 2 * inter + offset, dtype=torch.float32, device="cuda:0")
+    buf[offset:] = torch.from_numpy(gu.ravel()).to("cuda:0")
+    obuf = torch.full((rows * inter + offset,), -7.0, dtype=torch.float32, device="cuda:0")
+    P.fused_silu_mul_interleaved_f32(buf[offset:], obuf[offset:], inter, total)
+    torch.cuda.synchronize()
+    got = obuf.cpu().numpy()[offset:].astype(np.float64)
+    ref = orc.silu_mul_f32_rows(gu, inter, total).astype(np.float64)
+    ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got[:total] - ref) <= 4 * ulp + 1e-37)
+    assert np.mean(got[:total] == ref) > 0.9
+    assert np.all(got[total:] == -7.0)               # nothing written past `total`
+
+
+@pytest.mark.parametrize("rows,inter,total_cut,offset", [
     (7, 100, 0, 0),        # inter not a multiple of 8
     (5, 1024, 0, 1),       # unaligned pointers (one element in)
     (6, 96, 37, 0),        # total not a multiple of inter: the last row cut short

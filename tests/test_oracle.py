@@ -310,6 +310,39 @@ def test_moe_forward_composition(orc):
                               acc.astype(np.float32).astype(np.float16).view(np.uint16))
 
 
+def test_silu_mul_f32_closed_form_and_special_values(orc):
+    """elementwise.rs:214-250 in f32: against float64 silu(g) * u within the error of three
+    f32 roundings and one expf (a few ulps), exact special values, and the interleaved
+    indexing (gate first, up `inter` elements on, a last row cut short) against the
+    element function."""
+    g = np.random.default_rng(65)
+    a = (g.standard_normal(5000) * 6).astype(np.float32)
+    b = (g.standard_normal(5000) * 3).astype(np.float32)
+    got = np.array([orc.lib().orc_silu_mul_f32(float(x), float(y)) for x, y in zip(a, b)],
+                   dtype=np.float32).astype(np.float64)
+    af, bf = a.astype(np.float64), b.astype(np.float64)
+    want = af / (1.0 + np.exp(-af)) * bf
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4 * ulp + 1e-37)
+    f = lambda x, y: orc.lib().orc_silu_mul_f32(x, y)
+    assert f(0.0, 5.0) == 0.0
+    assert f(100.0, 3.0) == 300.0                       # exp(-100) vanishes beside 1
+    assert f(-100.0, 3.0) == 0.0                        # exp(100) overflows: g / inf
+    assert f(2.0, 0.0) == 0.0
+    assert abs(f(1.0, 1.0) - 1.0 / (1.0 + np.exp(-1.0))) < 2e-7
+    # interleaved rows: 5 rows of inter = 7, the last row cut after 3 entries
+    rows, inter = 5, 7
+    gu = (g.standard_normal((rows, 2 * inter)) * 4).astype(np.float32)
+    total = rows * inter - 4
+    out = orc.silu_mul_f32_rows(gu, inter, total)
+    elem = np.array([f(float(gu[i // inter, i % inter]), float(gu[i // inter, inter + i % inter]))
+                     for i in range(total)], dtype=np.float32)
+    assert np.array_equal(out.view(np.uint32), elem.view(np.uint32))
+    swapped = np.array([f(float(gu[i // inter, inter + i % inter]), float(gu[i // inter, i % inter]))
+                        for i in range(total)], dtype=np.float32)
+    assert not np.array_equal(out, swapped)             # gate and up are not interchangeable
+
+
 def test_silu_mul_error_bound(orc):
     g = np.random.default_rng(64)
     a = (g.standard_normal(4000) * 4).astype(np.float16)

@@ -74,7 +74,8 @@ EXPORTED = (
     "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
-    "w4a16_moe_gemm", "fused_silu_mul_interleaved_f16", "w4a16_moe_sum",
+    "w4a16_moe_gemm", "fused_silu_mul_interleaved_f16", "fused_silu_mul_interleaved_f32",
+    "w4a16_moe_sum",
     "w4a16_fused_moe_workspace_size", "w4a16_fused_moe",
     "hiprt_create", "hiprt_destroy", "hiprt_module_load", "hiprt_module_unload", "hiprt_launch",
     "hiprt_stream_create", "hiprt_stream_destroy", "hiprt_stream_synchronize", "hiprt_malloc",
@@ -118,6 +119,7 @@ def lib() -> ctypes.CDLL:
         L.w4a16_moe_gemm.argtypes = [_P, _I, _P, _I, _P, _P, _P, _L, _L, _L, _I, _P, _P, _P, _P,
                                      _I, _I, _I, _I, _I, _I, _I]
         L.fused_silu_mul_interleaved_f16.argtypes = [_P, _P, _P, _I, _I]
+        L.fused_silu_mul_interleaved_f32.argtypes = [_P, _P, _P, _I, _I]
         L.w4a16_moe_sum.argtypes = [_P, _P, _P, _P, _I, _I, _I]
         L.w4a16_fused_moe_workspace_size.restype = ctypes.c_size_t
         L.w4a16_fused_moe_workspace_size.argtypes = [_I] * 6
@@ -391,6 +393,12 @@ def fused_silu_mul_interleaved_f16(gate_up, out, inter, total, stream=None):
     """elementwise.rs:188-212 parameter list: out[b*inter+i] = silu(g)*u."""
     st = stream if stream is not None else _stream(gate_up)
     check(lib().fused_silu_mul_interleaved_f16(st, _p(gate_up), _p(out), inter, total))
+
+
+def fused_silu_mul_interleaved_f32(gate_up, out, inter, total, stream=None):
+    """elementwise.rs:214-250 parameter list over float32 tensors: out[b*inter+i] = silu(g)*u."""
+    st = stream if stream is not None else _stream(gate_up)
+    check(lib().fused_silu_mul_interleaved_f32(st, _p(gate_up), _p(out), inter, total))
 
 
 def moe_sum(y_pairs, topk_weights, T, topk, K, out=None):

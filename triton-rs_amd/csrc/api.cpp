@@ -694,6 +694,16 @@ W4A16_API int fused_silu_mul_interleaved_f16(void* stream, const void* gate_up, 
     return e == hipSuccess ? W4A16_OK : hip_fail(e, "silu_mul launch");
 }
 
+W4A16_API int fused_silu_mul_interleaved_f32(void* stream, const float* gate_up, float* out,
+                                             int32_t inter, int32_t total) {
+    if (!gate_up || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (inter < 1 || total < 0)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (inter=%d total=%d)", inter, total);
+    if (total == 0) return W4A16_OK;
+    hipError_t e = launch_silu_mul_f32(gate_up, out, inter, total, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "silu_mul_f32 launch");
+}
+
 W4A16_API int w4a16_moe_sum(void* stream, const void* y_pairs, const float* topk_weights,
                             void* out, int32_t T, int32_t topk, int32_t K) {
     if (!y_pairs || !topk_weights || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");

@@ -143,6 +143,15 @@ __device__ __forceinline__ u32x4 ld_stream4(const uint32_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// silu(g) * u with g, u and the result in f32 (crates/triton-kernels/src/elementwise.rs:
+// 214-250): denominator exp(-g) + 1, one division, one product, each rounded to f32 (no
+// contraction).
+__device__ __forceinline__ float silu_mul_f32(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = g / (expf(-g) + 1.0f);
+    return s * u;
+}
+
 // f16(silu(g) * u) with g, u fp16 and silu(g) = g / (1 + exp(-g)) in f32
 // (crates/triton-kernels/src/elementwise.rs:188-212): the product is rounded to f32, then to
 // f16, as in the reference and the oracle. Contraction is off and the product passes through

@@ -255,6 +255,48 @@ hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_
     return hipGetLastError();
 }
 
+// f32 twin (elementwise.rs:214-250): out[b, i] = silu(g) * u in f32. Four outputs per thread
+// where inter and total are multiples of 4 and both buffers 16-byte aligned; one otherwise.
+__global__ void __launch_bounds__(256)
+silu_mul_f32_kernel(const float* __restrict__ gate_up, float* __restrict__ out, int inter,
+                    int64_t total) {
+    const int64_t i4 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i4 >= total) return;
+    const int64_t b = i4 / inter, i = i4 - b * inter;
+    const float* g = gate_up + b * 2 * inter + i;
+    const float4 gv = *reinterpret_cast<const float4*>(g);
+    const float4 uv = *reinterpret_cast<const float4*>(g + inter);
+    *reinterpret_cast<float4*>(out + i4) =
+        make_float4(silu_mul_f32(gv.x, uv.x), silu_mul_f32(gv.y, uv.y), silu_mul_f32(gv.z, uv.z),
+                    silu_mul_f32(gv.w, uv.w));
+}
+
+__global__ void __launch_bounds__(256)
+silu_mul_f32_scalar_kernel(const float* __restrict__ gate_up, float* __restrict__ out, int inter,
+                           int64_t total) {
+    const int64_t i1 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i1 >= total) return;
+    const int64_t b = i1 / inter, i = i1 - b * inter;
+    const float* g = gate_up + b * 2 * inter + i;
+    out[i1] = silu_mul_f32(g[0], g[inter]);
+}
+
+hipError_t launch_silu_mul_f32(const float* gate_up, float* out, int inter, int64_t total,
+                               hipStream_t st) {
+    (void)hipGetLastError();
+    const bool vec = inter % 4 == 0 && total % 4 == 0 && (reinterpret_cast<uintptr_t>(gate_up) % 16) == 0 &&
+                     (reinterpret_cast<uintptr_t>(out) % 16) == 0;
+    if (vec) {
+        const int64_t threads = total / 4;
+        hipLaunchKernelGGL(silu_mul_f32_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                           st, gate_up, out, inter, total);
+    } else {
+        hipLaunchKernelGGL(silu_mul_f32_scalar_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                           0, st, gate_up, out, inter, total);
+    }
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ combine
 
 // y[t, n] = f16(sum_j w[t, j] * f32(yp[t * topk + j, n])), eight columns per thread.

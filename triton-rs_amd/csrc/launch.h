@@ -128,6 +128,8 @@ hipError_t launch_moe_align(const int32_t* ids, int P, int E, int block_m, int c
 inline int moe_max_tiles(int P, int E, int tile_bm) { return (P + tile_bm - 1) / tile_bm + E; }
 hipError_t launch_silu_mul(const half_t* gate_up, half_t* out, int inter, int64_t total,
                            hipStream_t st);
+hipError_t launch_silu_mul_f32(const float* gate_up, float* out, int inter, int64_t total,
+                               hipStream_t st);
 hipError_t launch_moe_sum(const half_t* y_pairs, const float* weights, half_t* out, int T,
                           int topk, int K, hipStream_t st);
 
