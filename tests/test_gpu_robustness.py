@@ -150,7 +150,8 @@ def test_init_then_capture_replays(torch_cuda, orc):
 def test_captured_graph_of_each_kernel_family_replays_exactly(torch_cuda):
     """One graph holding a call of each kernel family with its split-K state: the row-paired
     AWQ GEMV (fixed-point hand-off), the act-order small-batch kernel (group table and g_idx
-    slice in LDS), a K-split prefill (fp32 partials, counter hand-off) and the prepared
+    slice in LDS; 16 rows with 4 waves, 64 rows with 8 waves and K split in two), a K-split
+    prefill (fp32 partials, counter hand-off) and the prepared
     act-order path (LDS column gather, then the small-batch kernel). Replayed three times with
     other eager calls on the same stream in between, every replay equals the eager outputs bit
     for bit (the hand-offs leave their counters and slots clean; the launch-time LDS
@@ -163,6 +164,8 @@ def test_captured_graph_of_each_kernel_family_replays_exactly(torch_cuda):
         (Problem(GPTQ, M=16, K=2048, N=1024, G=128, seed=3111, act_order=True), "gptq", True, False),
         (Problem(AWQ, M=512, K=2048, N=4096, G=128, seed=3112), "awq", False, False),
         (Problem(GPTQ, M=64, K=2048, N=1024, G=128, seed=3113, act_order=True), "gptq", True, True),
+        # 64-row act-order tile of 8 waves with K split in two (counter hand-off)
+        (Problem(GPTQ, M=64, K=4096, N=1024, G=128, seed=3115, act_order=True), "gptq", True, False),
     ]
     assert P.plan("awq", 512, 4096, 2048, 128) == "prefill"
     calls = []
