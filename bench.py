@@ -512,7 +512,8 @@ def extras(torch, pkg, dev, stream, args):
 
 def achievable_refs(torch, dev, stream):
     """Measured HBM references on this GPU, beside the spec peak: a device-to-device copy
-    (bytes read + written) and a read-only fp32 sum of 512 MiB. (The MFMA references, torch's
+    (bytes read + written), a read-only fp32 sum of 512 MiB, and the per-launch floor of a
+    one-element kernel replayed from HIP graphs like the GEMM calls. (The MFMA references, torch's
     fp16 GEMM at config 3's shapes, come from dequant_then_mm_refs, timed like the GEMMs.)"""
     out = {}
     n = 512 << 20
@@ -541,6 +542,10 @@ def achievable_refs(torch, dev, stream):
     ms = t_ms(lambda: torch.sum(af), 20)
     out["read_sum_f32_GBps"] = round(n / (ms * 1e-3) / 1e9, 1)
     del a, b, af
+    # per-launch floor of a kernel in a graph replay, timed like the GEMMs: one-element add
+    tiny = torch.zeros(1, dtype=torch.int32, device=dev)
+    out["graph_launch_floor_us"] = round(
+        time_calls(torch, lambda i: tiny.add_(1), 1000, 10, stream, 1)[1] * 1e3, 2)
     progress(f"achievable references: {out}")
     return out
 
