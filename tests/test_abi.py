@@ -32,6 +32,39 @@ def test_library_exports_every_declared_symbol():
     assert set(names) <= exported
 
 
+def _c_param_counts():
+    """Parameter count of every W4A16_API function in include/w4a16.h."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"W4A16_API\s+[\w\s\*]+?\b(\w+)\s*\(([^)]*)\)", text):
+        args = m.group(2).strip()
+        out[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def _rust_extern_fns(text):
+    """(name, parameter count) of every fn in the `extern "C" { ... }` blocks of Rust text."""
+    fns = []
+    for block in re.findall(r'extern "C" \{(.*?)\n\}', text, flags=re.S):
+        for m in re.finditer(r"\bfn\s+(\w+)\s*\(([^)]*)\)", block, flags=re.S):
+            args = m.group(2).strip().rstrip(",")
+            fns.append((m.group(1), 0 if not args else args.count(",") + 1))
+    return fns
+
+
+@pytest.mark.parametrize("source", ["rust/triton-runtime-hip/src/lib.rs", "INTEGRATION.md"])
+def test_rust_ffi_block_matches_the_header(source):
+    """The Rust backend cannot be compiled in this image (no cargo): its FFI declarations are
+    checked here instead. Every libw4a16 function they bind is declared in include/w4a16.h
+    with the same number of parameters (the hiprt_* runtime calls included)."""
+    c = _c_param_counts()
+    fns = _rust_extern_fns(open(os.path.join(ROOT, source)).read())
+    assert len(fns) >= 15, source
+    for name, n in fns:
+        assert name in c, f"{source}: fn {name} is not declared in include/w4a16.h"
+        assert c[name] == n, f"{source}: fn {name} takes {n} parameters, the header {c[name]}"
+
+
 def test_version_and_empty_error():
     P = pkg()
     assert "gfx950" in P.version()
