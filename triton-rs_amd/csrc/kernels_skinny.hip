@@ -2,9 +2,9 @@
 // so the kernel is built to keep loads in flight and to need few workgroup-to-workgroup
 // reductions.
 //
-// A workgroup owns a strip of WN = 16*CPL columns; its waves (4, or 8 for 32-row tiles)
-// split the strip's K range and stream independently (no LDS staging, no barrier in the main
-// loop). Each lane keeps a ring of PF k32 steps of loads in flight: its packed words, the
+// A workgroup owns a strip of WN = 16*CPL columns; its waves (4, or 8 for GPTQ 32-row tiles
+// and, where K allows, GPTQ 64-row tiles) split the strip's K range and stream independently
+// (no LDS staging, no barrier in the main loop). Each lane keeps a ring of PF k32 steps of loads in flight: its packed words, the
 // activation fragments and the group's scales/zeros. Every load of the steady state is
 // unconditional (rows past M are loaded clamped and zeroed at use), so the compiler's
 // wait counts let each step wait for its own slot only. Words are dequantised bit-exactly
