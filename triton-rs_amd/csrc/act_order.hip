@@ -10,6 +10,8 @@
 //     y = x @ W = sum_k x[:, k] W[k] = sum_j x[:, perm[j]] W'[j] = x' @ W',  x' = x[:, perm]
 // and W' is an ordinary (non-act-order) GPTQ matrix with the same scales and qzeros: every
 // kernel of the plain path applies, the prefill's dequant-to-LDS included.
+#include <algorithm>
+
 #include "device_common.h"
 #include "launch.h"
 
@@ -60,7 +62,7 @@ constexpr int GATHER_LDS_MAX_K = 32768;   // 64 KiB of LDS
 
 __global__ void __launch_bounds__(256)
 gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
-                          half_t* __restrict__ xout, int K) {
+                          half_t* __restrict__ xout, int K, int per) {
     extern __shared__ __attribute__((aligned(16))) half_t row_s[];
     const size_t row = (size_t)blockIdx.x * K;
     const int chunks = K / 8;
@@ -70,7 +72,9 @@ gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restric
     const u32x4* pp = reinterpret_cast<const u32x4*>(perm);
     u32x4* dst = reinterpret_cast<u32x4*>(xout + row);
     const uint32_t last = (uint32_t)K - 1u;
-    for (int c = threadIdx.x; c < chunks; c += 256) {
+    // this workgroup's share of the row's 8-column output chunks
+    const int c_end = min(chunks, ((int)blockIdx.y + 1) * per);
+    for (int c = (int)blockIdx.y * per + (int)threadIdx.x; c < c_end; c += 256) {
         const u32x4 p0 = pp[2 * c], p1 = pp[2 * c + 1];
         const uint32_t idx[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
         half8_t v;
@@ -99,9 +103,14 @@ hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* x
         constexpr int MAX_BLOCKS = 1 << 30;
         for (int m0 = 0; m0 < M; m0 += MAX_BLOCKS) {
             const int rows = M - m0 < MAX_BLOCKS ? M - m0 : MAX_BLOCKS;
-            hipLaunchKernelGGL(gather_columns_lds_kernel, dim3(rows), dim3(256),
-                               (size_t)K * sizeof(half_t), st, x + (size_t)m0 * K, perm,
-                               xout + (size_t)m0 * K, K);
+            // a few rows: each row's output chunks are shared by several workgroups (each
+            // stages the whole row), so that ~256 workgroups run (M=16, K=4096: 16 -> 256)
+            const int chunks = K / 8;
+            const int share = std::max(1, std::min(chunks / 32, 256 / rows));
+            const int per = (chunks + share - 1) / share;
+            hipLaunchKernelGGL(gather_columns_lds_kernel, dim3(rows, (chunks + per - 1) / per),
+                               dim3(256), (size_t)K * sizeof(half_t), st, x + (size_t)m0 * K,
+                               perm, xout + (size_t)m0 * K, K, per);
         }
         return hipGetLastError();
     }
