@@ -100,3 +100,47 @@ class Problem:
         if self.fmt == 0:
             return self.zq + self.zero_offset
         return self.zq
+
+
+# ------------------------------------------------------------------ prepared layout
+
+PREP_SLOT = tuple((i >> 1) | ((i & 1) << 2) for i in range(8))   # nibble slot of row i of a word
+
+
+def prepared_table_rows(G: int) -> int:
+    """Table rows per 128-row block: the block's groups (G = 32, 64) or its one group."""
+    return 128 // G if G < 128 else 1
+
+
+def prepared_table_words(K: int, G: int) -> int:
+    return ((K // 128) * prepared_table_rows(G) * 16 + 63) // 64 * 64
+
+
+def prepared_strip_bytes(K: int, G: int) -> int:
+    return 4 * prepared_table_words(K, G) + K * 8
+
+
+def prepared_layout(q: np.ndarray, zint: np.ndarray, scales: np.ndarray, G: int) -> np.ndarray:
+    """The prepared layout (include/w4a16.h, w4a16_prepare_layout) written from the integer
+    matrices: q [K, N] nibbles, zint [K/G, N] full zero points, scales fp16 [K/G, N].
+    Strip s: the table, for each block kb of 128 rows R rows r of 16 entries, entry (kb, r, c) =
+    fp16 bits of scales[g, 16 s + c] | zint[g, 16 s + c] << 16 with g = 128 kb // G + r, padded
+    to 256 bytes; then the blocks, 64 lanes x 4 words, lane l = column 16 s + l % 16, word w =
+    rows 128 kb + 32 (l // 16) + 8 w + [0, 8), row i in nibble slot PREP_SLOT[i].
+    Returns uint8 [N/16 * strip bytes]."""
+    K, N = q.shape
+    R = prepared_table_rows(G)
+    tw = prepared_table_words(K, G)
+    out = np.zeros((N // 16, tw + K * 2), dtype=np.uint32)
+    ent = scales.view(np.uint16).astype(np.uint32) | (zint.astype(np.uint32) << np.uint32(16))
+    g = (np.arange(K // 128)[:, None] * 128 // G + np.arange(R)[None, :]).reshape(-1)   # [kb*R + r]
+    tab = ent[g]                                                   # [blocks*R, N]
+    out[:, :len(g) * 16] = tab.reshape(len(g), N // 16, 16).transpose(1, 0, 2).reshape(N // 16, -1)
+    # q as [strip, kb, h, w, i, col]: rows 128 kb + 32 h + 8 w + i, column 16 s + col
+    qq = q.astype(np.uint32).reshape(K // 128, 4, 4, 8, N // 16, 16).transpose(4, 0, 1, 2, 3, 5)
+    words = np.zeros(qq.shape[:4] + (16,), dtype=np.uint32)   # [s, kb, h, w, col]
+    for i in range(8):
+        words |= qq[:, :, :, :, i, :] << np.uint32(4 * PREP_SLOT[i])
+    # lane l = 16 h + col, word w at l * 4 + w: order [s, kb, h, col, w]
+    out[:, tw:] = words.transpose(0, 1, 2, 4, 3).reshape(N // 16, K * 2)
+    return out.view(np.uint8).reshape(-1)

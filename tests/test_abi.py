@@ -305,3 +305,65 @@ def test_act_order_argument_errors():
     assert L.w4a16_gemm_act_order(None, P.FMT_AWQ, v, v, v, v, v, v, 1, 512, 4096, 128, 1) == P.ERR_INVALID_ARG
     assert L.w4a16_gemm_act_order(None, P.FMT_GPTQ, v, v, v, v, None, v, 1, 512, 4096, 128, 1) == P.ERR_INVALID_ARG
     assert "perm" in L.w4a16_last_error().decode()
+
+
+# ------------------------------------------------------------------ prepared layout
+
+def test_prepared_bytes_matches_the_layout():
+    """w4a16_prepared_bytes equals the strip size of the layout's restatement (tests/synth.py)
+    times the strip count, and is 0 for shapes the layout does not take."""
+    from synth import prepared_strip_bytes
+    P = pkg()
+    for K, N, G in ((4096, 14336, 128), (14336, 4096, 128), (4096, 4096, 128), (1024, 64, 32),
+                    (2048, 16, 64), (4096, 32, 256), (4096, 48, 4096)):
+        assert P.prepared_bytes(K, N, G) == N // 16 * prepared_strip_bytes(K, G), (K, N, G)
+    for K, N, G in ((4096, 4104, 128), (4000, 4096, 125), (4096, 4096, 96), (4096, 4096, 16),
+                    (65536, 16, 128), (0, 16, 128)):
+        assert P.prepared_bytes(K, N, G) == 0, (K, N, G)
+
+
+@pytest.mark.parametrize("over,code,needle", [
+    (dict(N=4104), 2, "N % 16"),
+    (dict(G=96, K=3072), 2, "group_size 32, 64"),
+    (dict(K=4000, G=125), 2, "K % 128"),
+    (dict(nbytes=1024), 1, "too small"),
+    (dict(buf=4096 + 16), 1, "256-byte aligned"),
+    (dict(qw=None), 1, "null pointer"),
+    (dict(fmt=2, zo=-3), 0, None),          # the AWQ format ignores the GPTQ zero offset
+    (dict(fmt=0, zo=17), 1, "gptq_zero_offset"),
+])
+def test_prepare_layout_argument_errors(over, code, needle):
+    P = pkg()
+    a = dict(fmt=P.FMT_AWQ, qw=1 << 20, sc=2 << 20, qz=3 << 20, K=4096, N=4096, G=128, zo=0,
+             buf=1 << 30, nbytes=1 << 30)
+    a.update(over)
+    if code == 0:
+        return   # a valid request would launch kernels: not here
+    p = lambda v: None if v is None else ctypes.c_void_p(v)
+    rc = P.lib().w4a16_prepare_layout(None, a["fmt"], p(a["qw"]), p(a["sc"]), p(a["qz"]), a["K"],
+                                      a["N"], a["G"], a["zo"], p(a["buf"]), a["nbytes"])
+    assert rc == code
+    assert needle in P.lib().w4a16_last_error().decode()
+
+
+def test_prepare_layout_rejects_overlap():
+    P = pkg()
+    K, N, G = 4096, 4096, 128
+    base = 1 << 30
+    rc = P.lib().w4a16_prepare_layout(None, P.FMT_AWQ, ctypes.c_void_p(base), ctypes.c_void_p(2 << 30),
+                                      ctypes.c_void_p(3 << 30), K, N, G, 0, ctypes.c_void_p(base + 256),
+                                      P.prepared_bytes(K, N, G))
+    assert rc == P.ERR_INVALID_ARG and "overlap" in P.lib().w4a16_last_error().decode()
+
+
+@pytest.mark.parametrize("M,N,K,G,code,needle", [
+    (0, 4096, 4096, 128, 1, "M (0)"),
+    (1, 4100, 4096, 128, 2, "N % 16"),
+    (1, 4096, 3072, 48, 2, "group_size"),
+])
+def test_gemm_prepared_argument_errors(M, N, K, G, code, needle):
+    P = pkg()
+    rc = P.lib().w4a16_gemm_prepared(None, ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 30), None,
+                                     ctypes.c_void_p(2 << 20), M, N, K, G)
+    assert rc == code
+    assert needle in P.lib().w4a16_last_error().decode()

@@ -1,0 +1,114 @@
+"""Prepared (kernel-native) layout: the one-time repack (w4a16_prepare_layout) against an
+independent numpy restatement of the layout, the dequantisation of prepared weights bit for
+bit against the oracle's dequantisation of the checkpoint, and the GEMM on prepared weights
+against the oracle's GEMM on the checkpoint (crates/triton-dsl/examples/
+w4a16_gptq_gemm_typed.rs:130-273, awq_gemm_int4_typed.rs:116-241), for all three formats,
+act-order through the group-order repack included."""
+import numpy as np
+import pytest
+
+from helpers import assert_parity, pkg, to_dev
+from synth import Problem, prepared_layout
+
+pytestmark = pytest.mark.gpu
+GPTQ, SYM, AWQ = 0, 1, 2
+NAME = {GPTQ: "gptq", SYM: "gptq_sym", AWQ: "awq"}
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch
+
+
+def _prep(P, p, zo=None):
+    zo = p.zero_offset if zo is None else zo
+    return P.prepare_layout(to_dev(p.qweight), to_dev(p.scales),
+                            None if p.qzeros is None else to_dev(p.qzeros), fmt=NAME[p.fmt],
+                            group_size=p.G, zero_offset=zo)
+
+
+@pytest.mark.parametrize("fmt,K,N,G,zo", [
+    (AWQ, 256, 64, 128, 0), (GPTQ, 512, 96, 64, 1), (SYM, 384, 48, 32, 0), (GPTQ, 1024, 32, 256, 0),
+    (AWQ, 4096, 128, 4096, 0), (AWQ, 1536, 32, 512, 0),
+])
+def test_prepare_layout_bytes(torch_cuda, fmt, K, N, G, zo):
+    P = pkg()
+    p = Problem(fmt, M=1, K=K, N=N, G=G, seed=7000 + K + N, zero_offset=zo)
+    w = _prep(P, p)
+    torch_cuda.cuda.synchronize()
+    assert w.buffer.numel() == P.prepared_bytes(K, N, G)
+    want = prepared_layout(p.q, p.zero_int(), p.scales, G)
+    assert np.array_equal(w.buffer.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("fmt,K,N,G", [(AWQ, 1024, 256, 128), (GPTQ, 512, 160, 32), (SYM, 768, 64, 64)])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_dequant_prepared_bit_exact(torch_cuda, orc, fmt, K, N, G, transposed):
+    P = pkg()
+    p = Problem(fmt, M=1, K=K, N=N, G=G, seed=7100 + K)
+    w16 = P.dequant_prepared(_prep(P, p), transposed=transposed).cpu().numpy()
+    ref = orc.dequant(fmt, p.qweight, p.scales, p.qzeros, K, N, G, zero_offset=p.zero_offset)
+    if transposed:
+        ref = ref.T
+    assert np.array_equal(w16.view(np.uint16), np.ascontiguousarray(ref).view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt,M,K,N,G", [
+    (AWQ, 1, 4096, 14336, 128),     # config 1 (M = 1), both MLP shapes
+    (AWQ, 1, 14336, 4096, 128),
+    (SYM, 1, 4096, 4096, 128),      # config 0
+    (GPTQ, 1, 4096, 6144, 128),
+    (AWQ, 1, 1024, 512, 32), (GPTQ, 1, 2048, 1792, 64), (SYM, 1, 384, 80, 128),
+    (AWQ, 1, 1792, 4096, 128), (AWQ, 1, 4096, 1792, 128),   # one GPU's share of an 8-way TP MLP
+    (GPTQ, 1, 32768, 256, 128), (AWQ, 1, 128, 16, 128), (AWQ, 1, 4096, 512, 256),
+    (GPTQ, 1, 2048, 256, 2048), (SYM, 1, 4096, 1024, 32),
+])
+def test_gemm_prepared_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=0x5EED0001 + K + N)
+    w = _prep(P, p)
+    y = P.gemm_prepared(to_dev(p.x), w)
+    y2 = P.gemm_prepared(to_dev(p.x), w)
+    torch_cuda.cuda.synchronize()
+    y, y2 = y.cpu().numpy(), y2.cpu().numpy()
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), "repeated calls differ"
+    ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, G,
+                         zero_offset=p.zero_offset, want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"prepared {NAME[fmt]} M={M} K={K} N={N} G={G}")
+
+
+def test_gemm_prepared_exact_arithmetic(torch_cuda, orc):
+    """x = j/4 and power-of-two scales: every product and partial sum is exact in fp32, so the
+    output is the exact sum rounded once to fp16 — bit for bit the oracle's."""
+    P = pkg()
+    g = np.random.default_rng(77)
+    for fmt in (AWQ, GPTQ, SYM):
+        p = Problem(fmt, M=1, K=2048, N=512, G=128, seed=78 + fmt)
+        p.x = (g.integers(-8, 9, size=p.x.shape) / 4.0).astype(np.float16)
+        p.scales = (2.0 ** g.integers(-8, -4, size=p.scales.shape)).astype(np.float16)
+        y = P.gemm_prepared(to_dev(p.x), _prep(P, p)).cpu().numpy()
+        ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
+                             zero_offset=p.zero_offset)
+        assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), NAME[fmt]
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 6144), (1, 1024, 384)])
+def test_act_order_then_prepared(torch_cuda, orc, M, K, N):
+    """An act-order checkpoint: group-order repack, then the prepared layout of the repacked
+    weights; the product with x gathered by perm equals the act-order GEMM."""
+    P = pkg()
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED0002 + K, act_order=True)
+    qout, perm = P.prepare_act_order(to_dev(p.qweight), to_dev(p.g_idx), group_size=128)
+    w = P.prepare_layout(qout, to_dev(p.scales), to_dev(p.qzeros), fmt="gptq", group_size=128,
+                         zero_offset=1)
+    w16 = P.dequant_prepared(w).cpu().numpy()
+    ref_w = orc.dequant(GPTQ, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx)
+    perm_h = perm.cpu().numpy()
+    assert np.array_equal(w16.view(np.uint16), ref_w[perm_h].view(np.uint16))
+    y = P.gemm_prepared(to_dev(p.x), w, perm=perm).cpu().numpy()
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx,
+                         want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what="act-order prepared")

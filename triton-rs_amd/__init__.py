@@ -70,7 +70,8 @@ _ERRORS = {c.code: c for c in (InvalidArgument, Unsupported, DeviceError, Module
 EXPORTED = (
     "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_noalloc",
     "w4a16_gemm_noalloc_scratch_bytes", "w4a16_gemm_plan", "w4a16_prepare_act_order",
-    "w4a16_gemm_act_order",
+    "w4a16_gemm_act_order", "w4a16_prepared_bytes", "w4a16_prepare_layout",
+    "w4a16_gemm_prepared", "w4a16_dequant_prepared",
     "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
@@ -103,6 +104,11 @@ def lib() -> ctypes.CDLL:
         L.w4a16_init.argtypes = [_I]
         L.w4a16_prepare_act_order.argtypes = [_P, _I, _P, _P, _I, _I, _I, _P, _P]
         L.w4a16_gemm_act_order.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
+        L.w4a16_prepared_bytes.restype = ctypes.c_size_t
+        L.w4a16_prepared_bytes.argtypes = [_I, _I, _I]
+        L.w4a16_prepare_layout.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _Z]
+        L.w4a16_gemm_prepared.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
+        L.w4a16_dequant_prepared.argtypes = [_P, _P, _P, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc_scratch_bytes.restype = ctypes.c_size_t
         L.w4a16_gemm_noalloc_scratch_bytes.argtypes = []
@@ -298,6 +304,73 @@ def gemm_act_order(x, qweight_prepared, scales, qzeros, perm, fmt="gptq", group_
     check(lib().w4a16_gemm_act_order(_stream(x), f, _ptr(x), _ptr(qweight_prepared), _ptr(scales),
                                      _ptr(qzeros), _ptr(perm), _ptr(out), M, N, K, group_size,
                                      zero_offset))
+    return out
+
+
+class PreparedWeights:
+    """A weight matrix in the prepared layout (w4a16_prepare_layout): a uint8 device buffer
+    plus the (K, N, group_size) it was made for. The checkpoint's format and zero convention
+    are folded into it."""
+
+    def __init__(self, buffer: torch.Tensor, K: int, N: int, group_size: int):
+        self.buffer, self.K, self.N, self.group_size = buffer, K, N, group_size
+
+
+def prepared_bytes(K: int, N: int, group_size: int = 128) -> int:
+    """Bytes of the prepared layout for this shape (0: shape not supported)."""
+    return lib().w4a16_prepared_bytes(K, N, group_size)
+
+
+def prepare_layout(qweight, scales, qzeros, fmt="awq", group_size: int = 128,
+                   zero_offset: int = 1) -> PreparedWeights:
+    """One-time rewrite of a GPTQ / GPTQ_SYM / AWQ checkpoint into the prepared layout."""
+    f = _fmt(fmt)
+    _require(qweight, "qweight", _INT32)
+    dev = qweight.device
+    _require(scales, "scales", _HALF, dev)
+    if qzeros is not None:
+        _require(qzeros, "qzeros", _INT32, dev)
+    for t, n in ((qweight, "qweight"), (scales, "scales"), (qzeros, "qzeros")):
+        if t is not None and not t.is_contiguous():
+            raise InvalidArgument(f"{n} must be contiguous")
+    if f == FMT_AWQ:
+        K, N = qweight.shape[0], qweight.shape[1] * 8
+    else:
+        K, N = qweight.shape[0] * 8, qweight.shape[1]
+    nbytes = prepared_bytes(K, N, group_size)
+    if nbytes == 0:
+        raise Unsupported(f"no prepared layout for K={K} N={N} group_size={group_size}")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    check(lib().w4a16_prepare_layout(_stream(qweight), f, _ptr(qweight), _ptr(scales),
+                                     _ptr(qzeros), K, N, group_size, zero_offset, _ptr(buf),
+                                     nbytes))
+    return PreparedWeights(buf, K, N, group_size)
+
+
+def gemm_prepared(x: torch.Tensor, w: PreparedWeights, perm: torch.Tensor | None = None,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[M, N] = x[M, K] @ W16 from prepared weights (perm: an act-order checkpoint repacked
+    by prepare_act_order before prepare_layout; x's columns are gathered by it first)."""
+    _require(x, "x", _HALF)
+    if perm is not None:
+        _require(perm, "perm", _INT32, x.device)
+    if x.dim() != 2 or not x.is_contiguous():
+        raise InvalidArgument("x must be a contiguous 2-D tensor")
+    M, K = x.shape
+    if K != w.K:
+        raise InvalidArgument(f"x has K={K}, the prepared weights K={w.K}")
+    out = _gemm_out(out, M, w.N, x.device)
+    check(lib().w4a16_gemm_prepared(_stream(x), _ptr(x), _ptr(w.buffer), _ptr(perm), _ptr(out),
+                                    M, w.N, K, w.group_size))
+    return out
+
+
+def dequant_prepared(w: PreparedWeights, transposed: bool = False) -> torch.Tensor:
+    """fp16 weights of a prepared matrix, [K, N] (or [N, K] when transposed)."""
+    out = torch.empty((w.N, w.K) if transposed else (w.K, w.N), dtype=torch.float16,
+                      device=w.buffer.device)
+    check(lib().w4a16_dequant_prepared(_stream(w.buffer), _ptr(w.buffer), _ptr(out), w.K, w.N,
+                                       w.group_size, int(transposed)))
     return out
 
 

@@ -31,7 +31,7 @@ COMMON = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
           f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}"]
 
-SOURCES = ["api.cpp", "hiprt.cpp", "kernels_gemv.hip", "kernels_prefill.hip", "kernels_skinny.hip", "kernels_strided.hip", "kernels_moe.hip", "act_order.hip", "noalloc.hip"]
+SOURCES = ["api.cpp", "hiprt.cpp", "kernels_gemv.hip", "kernels_prefill.hip", "kernels_skinny.hip", "kernels_strided.hip", "kernels_moe.hip", "act_order.hip", "noalloc.hip", "prepared.hip"]
 
 
 def _run(cmd):

@@ -464,6 +464,97 @@ W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const v
                      zero_offset, alloc_scratch_source());
 }
 
+// ------------------------------------------------------------------ prepared layout
+
+static int check_prep_shape(int32_t K, int32_t N, int32_t G) {
+    if (K < 1 || N < 1 || G < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "sizes must be positive (K=%d N=%d group_size=%d)", K, N, G);
+    if (K % G) return fail(W4A16_ERR_INVALID_ARG, "K (%d) must be a multiple of group_size (%d)", K, G);
+    if (N % 16 || K % 128 || !prep_group_ok(G) || K > PREP_MAX_K)
+        return fail(W4A16_ERR_UNSUPPORTED,
+                    "the prepared layout needs N %% 16 == 0, K %% 128 == 0, group_size 32, 64 or a "
+                    "multiple of 128, and K <= %d (K=%d N=%d group_size=%d)", PREP_MAX_K, K, N, G);
+    return W4A16_OK;
+}
+
+W4A16_API size_t w4a16_prepared_bytes(int32_t K, int32_t N, int32_t G) {
+    if (K < 1 || N < 1 || G < 1 || K % G || N % 16 || K % 128 || !prep_group_ok(G) || K > PREP_MAX_K)
+        return 0;
+    return prep_total_bytes(K, N, G);
+}
+
+W4A16_API int w4a16_prepare_layout(void* stream, int fmt, const void* qweight, const void* scales,
+                                   const void* qzeros, int32_t K, int32_t N, int32_t G,
+                                   int32_t zero_offset, void* prepared, size_t prepared_bytes) {
+    int rc = check_gemm_args(fmt, (void*)1, qweight, scales, qzeros, (void*)1, 1, N, K, G);
+    if (!rc) rc = check_zero_offset(fmt, zero_offset);
+    if (!rc) rc = check_prep_shape(K, N, G);
+    if (rc) return rc;
+    if (!prepared) return fail(W4A16_ERR_INVALID_ARG, "prepared is null");
+    const size_t need = prep_total_bytes(K, N, G);
+    if (prepared_bytes < need)
+        return fail(W4A16_ERR_INVALID_ARG, "prepared buffer too small (%zu < %zu bytes)", prepared_bytes, need);
+    if (!aligned(prepared, 256)) return fail(W4A16_ERR_INVALID_ARG, "prepared must be 256-byte aligned");
+    const char* pb = static_cast<const char*>(prepared);
+    auto overlaps = [&](const void* q, size_t n) {
+        const char* c = static_cast<const char*>(q);
+        return q && c < pb + need && pb < c + n;
+    };
+    if (overlaps(qweight, (size_t)K * N / 2) || overlaps(scales, (size_t)(K / G) * N * 2) ||
+        (fmt != W4A16_FMT_GPTQ_SYM && overlaps(qzeros, (size_t)(K / G) * N / 2)))
+        return fail(W4A16_ERR_INVALID_ARG, "prepared must not overlap the checkpoint tensors");
+    hipError_t e = launch_prepare_layout(
+        fmt, static_cast<const uint32_t*>(qweight), static_cast<const half_t*>(scales),
+        fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros), prepared, K, N,
+        G, zero_offset, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepare layout launch");
+}
+
+W4A16_API int w4a16_dequant_prepared(void* stream, const void* prepared, void* out, int32_t K,
+                                     int32_t N, int32_t G, int transposed) {
+    if (int rc = check_prep_shape(K, N, G)) return rc;
+    if (!prepared || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (!aligned(prepared, 256) || !aligned(out, 16))
+        return fail(W4A16_ERR_INVALID_ARG, "prepared must be 256-byte and out 16-byte aligned");
+    hipError_t e = launch_prep_dequant(prepared, static_cast<half_t*>(out), K, N, G,
+                                       transposed ? 1 : 0, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared dequant launch");
+}
+
+W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepared,
+                                  const int32_t* perm, void* out, int32_t M, int32_t N, int32_t K,
+                                  int32_t G) {
+    if (int rc = check_prep_shape(K, N, G)) return rc;
+    if (!x || !prepared || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (M < 1) return fail(W4A16_ERR_INVALID_ARG, "M (%d) must be positive", M);
+    if (!aligned(x, 16) || !aligned(prepared, 256) || !aligned(out, 16) || (perm && !aligned(perm, 16)))
+        return fail(W4A16_ERR_INVALID_ARG,
+                    "x, out and perm must be 16-byte aligned, prepared 256-byte aligned");
+    const PrepGemvShape gs = prep_gemv_shape(M, N, K, G);
+    if (!gs.ok)
+        return fail(W4A16_ERR_UNSUPPORTED, "no prepared-layout kernel for M=%d N=%d K=%d group_size=%d",
+                    M, N, K, G);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const void* xa = x;
+    if (perm) {   // act-order checkpoint prepared in group order: x' = x[:, perm]
+        void* xg = nullptr;
+        int rc = stream_buffer(g_gather, st, (size_t)M * K * sizeof(half_t), 0, "act-order gather buffer", &xg);
+        if (rc) return rc;
+        hipError_t e = launch_gather_columns(static_cast<const half_t*>(x), perm,
+                                             static_cast<half_t*>(xg), M, K, st);
+        if (e != hipSuccess) return hip_fail(e, "act-order gather launch");
+        xa = xg;
+    }
+    PrepParams p{};
+    p.x = static_cast<const half_t*>(xa);
+    p.prep = static_cast<const unsigned char*>(prepared);
+    p.out = static_cast<half_t*>(out);
+    p.M = M; p.N = N; p.K = K; p.G = G;
+    p.strip_bytes = (uint32_t)prep_strip_bytes(K, G);
+    hipError_t e = launch_prep_gemv(p, gs, st);
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared gemv launch");
+}
+
 // The reference kernels' parameter lists with arbitrary strides. A call whose tensors are
 // the dense row-major layouts of the checkpoint formats (the usual case: a linear layer's
 // weights and activations) is the same problem w4a16_gemm solves, and goes through its

@@ -200,6 +200,42 @@ hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint3
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
                                  hipStream_t st);
 
+// Prepared layout (prepared.hip): strips of 16 columns, each one contiguous run of
+// prep_strip_bytes(K, G) bytes: the strip's table (per block of 128 rows, R = max(1, 128/G)
+// rows of 16 entries, fp16 scale | zero point << 16; padded to 256 bytes), then K / 128 blocks
+// of 1 KiB. Needs N % 16 == 0, K % 128 == 0, K % G == 0 and G one of 32, 64 or a multiple
+// of 128.
+constexpr bool prep_group_ok(int G) { return G == 32 || G == 64 || (G >= 128 && G % 128 == 0); }
+constexpr int prep_table_rows(int G) { return G < 128 ? 128 / G : 1; }   // per block
+constexpr uint32_t prep_table_words(int K, int G) {
+    return (uint32_t)(((K / 128) * prep_table_rows(G) * 16 + 63) & ~63);
+}
+constexpr size_t prep_strip_bytes(int K, int G) { return (size_t)K * 8 + (size_t)prep_table_words(K, G) * 4; }
+inline size_t prep_total_bytes(int K, int N, int G) { return (size_t)(N / 16) * prep_strip_bytes(K, G); }
+constexpr int PREP_MAX_K = 32768;
+
+struct PrepParams {
+    const half_t* x;              // [M, K]
+    const unsigned char* prep;    // prepared weights
+    half_t* out;                  // [M, N]
+    int M, N, K, G;
+    uint32_t strip_bytes;
+};
+struct PrepGemvShape {
+    bool ok;
+    int bpw;      // blocks (128 rows x 16 columns) per wave, at most
+    int waves;    // waves per workgroup (one workgroup per strip)
+    bool mfma;    // matrix-core dot products (group_size % 128 == 0), else VALU dot2
+    size_t lds;   // dynamic LDS bytes
+};
+hipError_t launch_prepare_layout(int fmt, const uint32_t* qweight, const half_t* scales,
+                                 const uint32_t* qzeros, void* out, int K, int N, int G,
+                                 int zero_offset, hipStream_t st);
+hipError_t launch_prep_dequant(const void* prep, half_t* out, int K, int N, int G, int transposed,
+                               hipStream_t st);
+PrepGemvShape prep_gemv_shape(int M, int N, int K, int G);
+hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st);
+
 // ------------------------------------------------------------------ op layer (api.cpp)
 
 // Split-K scratch of one call: tile counters (FLAG_STRIDE apart), the fixed-point hand-off's

@@ -1,0 +1,439 @@
+// Prepared (kernel-native) weight layout and the kernels that read it.
+//
+// A GPTQ, GPTQ_SYM or AWQ checkpoint (crates/triton-dsl/examples/w4a16_gptq_gemm_typed.rs:15-32,
+// awq_gemm_int4_typed.rs:10-31; ferrum's loader ships qweight, scales and qzeros as stored,
+// w4a16_gptq_gemm_typed.rs:11-13, :55-60) is rewritten once into one format for all three:
+//
+//   the matrix is cut into strips of 16 columns; strip s (columns 16 s .. 16 s + 15) is one
+//   contiguous run of prep_strip_bytes(K, G) bytes:
+//     [table: per block, R = max(1, 128 / G) rows of 16 entries of 32 bits; padded to 256
+//      bytes][K/128 blocks of 1 KiB]
+//   row r of block kb's table holds group (128 kb / G) + r (G <= 128: the groups of the
+//   block's rows in order; G a multiple of 128: the block's one group, repeated for every
+//   block in it). Entry c holds that group's fp16 scale for column 16 s + c in its low 16
+//   bits and the column's full zero point in its high 16 bits: the GPTQ nibble +
+//   zero_offset, 8 for GPTQ_SYM, the AWQ nibble; W16 = RNE_f16((q - z) * s) as in the
+//   checkpoint formats (w4a16_gptq_gemm_typed.rs:246-260, awq_gemm_int4_typed.rs:213-228).
+//   block kb holds rows 128 kb .. 128 kb + 127 of the strip as 64 lanes x 16 bytes: lane l
+//   covers column 16 s + l % 16 and rows 128 kb + 32 (l / 16) + [0, 32), as four 32-bit
+//   words of 8 consecutive rows each (word w: rows + 8 w .. + 8 w + 7). Row i of a word sits
+//   in nibble slot (i >> 1) | ((i & 1) << 2) (the AWQ slot order), so that
+//     (w & 0x000F000F) | 0x64006400        = (1024 + q0, 1024 + q1)
+//     (w & 0x00F000F0) | 0x64006400        = (1024 + 16 q2, 1024 + 16 q3)
+//     ((w >> 8) & 0x000F000F) | 0x64006400 = (1024 + q4, 1024 + q5)
+//     ((w >> 8) & 0x00F000F0) | 0x64006400 = (1024 + 16 q6, 1024 + 16 q7)
+//   pair up with the activations (x0, x1) .. (x6, x7) as they lie in memory.
+//
+// So a workgroup that owns a strip reads one contiguous run of HBM (no 128-byte row segments
+// at a stride of N/2 bytes, no separate scale and zero streams; the group table, read first,
+// shares DRAM pages with the first blocks), and one workgroup covers the whole K range of its
+// 16 columns: the GEMV needs no split-K hand-off at all.
+#include "device_common.h"
+#include "launch.h"
+
+namespace w4a16 {
+
+// nibble slot of row i (0..7) of a prepared word
+__host__ __device__ constexpr int prep_slot(int i) { return (i >> 1) | ((i & 1) << 2); }
+
+// ------------------------------------------------------------------ one-time repack
+
+// One thread per prepared word: grid (N / 16 strips, K / 128 blocks), 256 threads = the
+// block's 64 lanes x 4 words, so the stores of a workgroup are one contiguous 1 KiB.
+template <int FMT>
+__global__ void __launch_bounds__(256)
+prep_weights_kernel(const uint32_t* __restrict__ qw, uint32_t* __restrict__ out, int K, int N,
+                    uint32_t strip_words, uint32_t table_words) {
+    const int s = blockIdx.x, kb = blockIdx.y, t = threadIdx.x;
+    const int l = t >> 2, w = t & 3;
+    const int n = 16 * s + (l & 15);
+    const int k0 = 128 * kb + 32 * (l >> 4) + 8 * w;
+    uint32_t r = 0;
+    if constexpr (FMT == FMT_AWQ) {
+        const int NW = N >> 3, sl = awq_slot(n);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t v = qw[(size_t)(k0 + i) * NW + (n >> 3)];
+            r |= ((v >> (4 * sl)) & 0xFu) << (4 * prep_slot(i));
+        }
+    } else {
+        const uint32_t v = qw[(size_t)(k0 >> 3) * N + n];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r |= ((v >> (4 * i)) & 0xFu) << (4 * prep_slot(i));
+    }
+    out[(size_t)s * strip_words + table_words + (size_t)kb * 256 + t] = r;
+}
+
+// One thread per table entry (block, row, column) of every strip; the same threads also
+// clear the table's padding (so the buffer's bytes are a function of the checkpoint alone).
+template <int FMT>
+__global__ void __launch_bounds__(256)
+prep_meta_kernel(const half_t* __restrict__ scales, const uint32_t* __restrict__ qz,
+                 uint32_t* __restrict__ out, int K, int N, int G, int zero_offset,
+                 uint32_t strip_words) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int R = prep_table_rows(G);
+    const uint32_t used = (uint32_t)(K / 128) * (uint32_t)R * 16u, tw = prep_table_words(K, G);
+    const uint32_t pad = tw - used;
+    if (i < (int64_t)(N / 16) * pad) {
+        const int64_t s = i / pad;
+        out[s * strip_words + used + (i - s * pad)] = 0u;
+    }
+    if (i >= (int64_t)(N / 16) * used) return;
+    const int s = (int)(i / used), e = (int)(i - (int64_t)s * used);
+    const int kb = e / (16 * R), r = (e / 16) % R, n = 16 * s + (e & 15);
+    const int g = kb * 128 / G + r;
+    uint32_t word = 0;
+    if constexpr (FMT != FMT_GPTQ_SYM) word = qz[(size_t)g * (N >> 3) + (n >> 3)];
+    const uint32_t z = (uint32_t)zero_of<FMT>(word, n, zero_offset);
+    const uint32_t sc = __builtin_bit_cast(uint16_t, scales[(size_t)g * N + n]);
+    out[(size_t)s * strip_words + e] = sc | (z << 16);
+}
+
+hipError_t launch_prepare_layout(int fmt, const uint32_t* qweight, const half_t* scales,
+                                 const uint32_t* qzeros, void* out, int K, int N, int G,
+                                 int zero_offset, hipStream_t st) {
+    (void)hipGetLastError();
+    const uint32_t sw = (uint32_t)(prep_strip_bytes(K, G) / 4), tw = prep_table_words(K, G);
+    uint32_t* ow = static_cast<uint32_t*>(out);
+    const dim3 gw(N / 16, K / 128);
+    const int64_t metas = (int64_t)(N / 16) * tw;   // entries and padding
+    const dim3 gm((unsigned)((metas + 255) / 256));
+    if (fmt == FMT_AWQ) {
+        hipLaunchKernelGGL(prep_weights_kernel<FMT_AWQ>, gw, dim3(256), 0, st, qweight, ow, K, N, sw, tw);
+        hipLaunchKernelGGL(prep_meta_kernel<FMT_AWQ>, gm, dim3(256), 0, st, scales, qzeros, ow, K, N, G, zero_offset, sw);
+    } else if (fmt == FMT_GPTQ) {
+        hipLaunchKernelGGL(prep_weights_kernel<FMT_GPTQ>, gw, dim3(256), 0, st, qweight, ow, K, N, sw, tw);
+        hipLaunchKernelGGL(prep_meta_kernel<FMT_GPTQ>, gm, dim3(256), 0, st, scales, qzeros, ow, K, N, G, zero_offset, sw);
+    } else {
+        hipLaunchKernelGGL(prep_weights_kernel<FMT_GPTQ_SYM>, gw, dim3(256), 0, st, qweight, ow, K, N, sw, tw);
+        hipLaunchKernelGGL(prep_meta_kernel<FMT_GPTQ_SYM>, gm, dim3(256), 0, st, scales, qzeros, ow, K, N, G, zero_offset, sw);
+    }
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ dequant of prepared weights
+
+// W16 = RNE_f16((q - z) * s) for every weight, to [K, N] or (transposed) [N, K]. Grid
+// (N / 16, K / 128), one thread per prepared word (8 weights of one column).
+__global__ void __launch_bounds__(256)
+prep_dequant_kernel(const unsigned char* __restrict__ prep, half_t* __restrict__ out, int K,
+                    int N, int G, uint32_t strip_bytes, int transposed) {
+    const int s = blockIdx.x, kb = blockIdx.y, t = threadIdx.x;
+    const int l = t >> 2, w = t & 3;
+    const int n = 16 * s + (l & 15);
+    const int k0 = 128 * kb + 32 * (l >> 4) + 8 * w;
+    const uint32_t* strip = reinterpret_cast<const uint32_t*>(prep + (size_t)s * strip_bytes);
+    const uint32_t word = strip[prep_table_words(K, G) + kb * 256 + t];
+    const int R = prep_table_rows(G);
+    const uint32_t e = strip[(kb * R + (G < 128 ? (k0 % 128) / G : 0)) * 16 + (l & 15)];
+    const half_t sc = __builtin_bit_cast(half_t, (uint16_t)e);
+    const int z = (int)(e >> 16);
+    half8_t v;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = dequant1(nib(word, prep_slot(i)), z, sc);
+    if (transposed) {
+        *reinterpret_cast<half8_t*>(out + (size_t)n * K + k0) = v;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) out[(size_t)(k0 + i) * N + n] = v[i];
+    }
+}
+
+hipError_t launch_prep_dequant(const void* prep, half_t* out, int K, int N, int G, int transposed,
+                               hipStream_t st) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(prep_dequant_kernel, dim3(N / 16, K / 128), dim3(256), 0, st,
+                       static_cast<const unsigned char*>(prep), out, K, N, G,
+                       (uint32_t)prep_strip_bytes(K, G), transposed);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ M = 1 GEMV
+
+// One workgroup per strip, W waves over its K / 128 blocks: wave w takes blocks w BPW + j,
+// j = 0 .. BPW - 1, so that a wave's activations, table entries and weights are each one
+// contiguous range. Order of a lane's loads: the activations of its wave's blocks, their
+// table entries, then the blocks (non-temporal). Loads complete in issue order, so x and the
+// table have landed while the weights are still arriving, and each block is consumed as it
+// lands. Every load is issued unconditionally: offsets past the end of their buffer resource
+// read zero without touching memory, and a block past the end of the strip (weights, x and
+// scale all zero) adds exactly zero, so no wave branches on its block count.
+//
+// Each wave stages what its own blocks need in a private LDS region (no wave waits for
+// another before its block loop; the workgroup meets once, to add its waves' sums). The
+// activations are stored as 80-byte rows of 32 rows of x: a block's four rows are 80 bytes
+// apart and fall in disjoint banks.
+constexpr int PREP_SEG_BYTES = 80;
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// v summed over the 4 lanes of its quad (DPP quad permutations)
+__device__ __forceinline__ float quad_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    return v;
+}
+
+// v summed over the 16 lanes of its row (DPP row rotations, then quad permutations)
+__device__ __forceinline__ float row16_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+    return quad_sum(v);
+}
+
+// Matrix-core kernel (G % 128 == 0, so a block lies in one group). A prepared word is
+// exactly a B operand of v_mfma_f32_16x16x32_f16 after one shift and four v_and_or_b32:
+// lane l supplies column l % 16 and rows 8 (l / 16) + e, e = 0..7, of the MFMA's 32-row
+// step; step st of block kb takes word st of every lane, i.e. rows 128 kb + 32 h + 8 st + e
+// (h = l / 16), and the A operand of lane l is x at the same rows. The B values are
+// 1024 + c_e q_e with c_e = 1, 1, 16, 16, 1, 1, 16, 16 (the exponent trick without the
+// shifts the odd pairs would need), so A carries x'_e = x_e / c_e (a power-of-two scaling,
+// exact in fp16 down to the subnormal range), and
+//   D = sum_k x'_k (1024 + c_k q_k) = 1024 S' + sum_k x_k q_k,
+//   S' = sum_k x'_k, S = sum_k x_k over the block,
+// so y += s (D - 1024 S' - z S) = s sum_k x_k (q_k - z). Every row of A is the same x', so
+// every row of D holds the result and each lane keeps the sum of its column. VALU per 8
+// weights: one shift and four v_and_or_b32.
+// LDS per wave: BPW x 4 rows of x'; BPW float pairs (1024 S', S); BPW x 16 table entries.
+template <int BPW>
+constexpr size_t prep_mfma_wave_lds() { return (size_t)BPW * (4 * PREP_SEG_BYTES + 8 + 16 * 4); }
+
+template <int BPW>
+__global__ void __launch_bounds__(1024)
+gemv_prep_mfma_kernel(PrepParams p) {
+    constexpr int XC = BPW / 4;   // 16-byte chunks of x per lane: 16 per block
+    constexpr int EC = BPW / 4;   // (block, column) table entries per lane: 16 per block
+    static_assert(BPW % 4 == 0, "blocks per wave");
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int W = blockDim.x >> 6;
+    const int s = blockIdx.x;
+    const int blocks = p.K >> 7;
+    const unsigned char* strip = p.prep + (size_t)s * p.strip_bytes;
+    const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
+    unsigned char* xs = lds + (size_t)wave * prep_mfma_wave_lds<BPW>();        // BPW x 4 rows
+    float2* bsum = reinterpret_cast<float2*>(xs + BPW * 4 * PREP_SEG_BYTES);   // BPW
+    uint32_t* tab = reinterpret_cast<uint32_t*>(bsum + BPW);                    // BPW x 16
+    float* red = reinterpret_cast<float*>(lds + (size_t)W * prep_mfma_wave_lds<BPW>());
+
+    // ---- loads: the x of the wave's blocks, their table entries, then the blocks
+    const bufrsrc_t xr = make_rsrc(p.x, (uint32_t)p.K * 2u);
+    const bufrsrc_t tr = make_rsrc(strip, tbytes);
+    const bufrsrc_t wr = make_rsrc(strip + tbytes, (uint32_t)p.K * 8u);
+    u32x4 xv[XC], wv[BPW];
+    uint32_t ev[EC];
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int c = lane + 64 * i, kb = wave * BPW + (c >> 4);   // chunk c: block c / 16 of the wave
+        const uint32_t off = kb < blocks ? (uint32_t)(kb * 128 + (c & 15) * 8) * 2u : (uint32_t)p.K * 2u;
+        xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    }
+    {   // the wave's BPW x 16 entries are contiguous: EC consecutive ones per lane, one load
+        // (streaming: with the default policy the same entries cost 0.3 us more per call)
+        const uint32_t off = (uint32_t)(wave * BPW * 16 + EC * lane) * 4u;
+        if constexpr (EC == 1) {
+            ev[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(tr, off, 0, 2);
+        } else if constexpr (EC == 2) {
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(tr, off, 0, 2));
+            ev[0] = v.x; ev[1] = v.y;
+        } else {
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tr, off, 0, 2));
+            ev[0] = v.x; ev[1] = v.y; ev[2] = v.z; ev[3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const uint32_t off = (uint32_t)(wave * BPW + j) * 1024u + (uint32_t)lane * 16u;
+        wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2));
+    }
+
+    // ---- stage x' (odd pairs / 16), the per-block sums and the table entries
+    const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+    const half2_t s16 = {(half_t)(1.0f / 16.0f), (half_t)(1.0f / 16.0f)};
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int c = lane + 64 * i;              // block c / 16, row c / 4 of the region
+        const u32x4 v = xv[i];
+        const half2_t a0 = as_h2(v.x), a2 = as_h2(v.z);
+        const half2_t a1 = as_h2(v.y) * s16, a3 = as_h2(v.w) * s16;
+        const float sp = row16_sum(dot2(a0, one2, dot2(a1, one2, dot2(a2, one2, dot2(a3, one2, 0.f)))));
+        const float sx = row16_sum(dot2(a0, one2, dot2(as_h2(v.y), one2, dot2(a2, one2, dot2(as_h2(v.w), one2, 0.f)))));
+        unsigned char* row = xs + (size_t)(c >> 2) * PREP_SEG_BYTES;
+        *reinterpret_cast<u32x4*>(row + (c & 3) * 16) = u32x4{as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)};
+        if ((c & 15) == 0) bsum[c >> 4] = make_float2(1024.0f * sp, sx);
+    }
+#pragma unroll
+    for (int i = 0; i < EC; ++i) tab[EC * lane + i] = ev[i];
+    // the region is this wave's alone: its LDS writes are ordered before its reads below
+
+    // ---- blocks: four MFMAs each
+    const int col = lane & 15, h = lane >> 4;
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const unsigned char* row = xs + (size_t)(j * 4 + h) * PREP_SEG_BYTES;
+        const float2 bx = bsum[j];
+        const uint32_t e = tab[j * 16 + col];
+        float4_t d = {0.f, 0.f, 0.f, 0.f};
+        const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            const half8_t a = *reinterpret_cast<const half8_t*>(row + 16 * st);
+            const uint32_t q = wd[st], q8 = q >> 8;
+            const u32x4 bw = {as_u32(nib_pair(q)), as_u32(nib_pair16(q)), as_u32(nib_pair(q8)),
+                              as_u32(nib_pair16(q8))};
+            d = mfma16x16x32(a, __builtin_bit_cast(half8_t, bw), d);
+        }
+        const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e), z = (float)(e >> 16);
+        y = __builtin_fmaf(sc, d[0] - __builtin_fmaf(z, bx.y, bx.x), y);
+    }
+
+    // ---- reduce over the waves (every lane of a column holds the same sum)
+    if (lane < 16) red[wave * 16 + lane] = y;
+    __syncthreads();
+    if (t < 16) {
+        float acc = 0.f;
+        for (int w = 0; w < W; ++w) acc += red[w * 16 + t];
+        p.out[(size_t)s * 16 + t] = (half_t)acc;
+    }
+}
+
+// VALU kernel for group sizes 32 and 64 (a block then spans groups; a lane's 32 rows still
+// lie in one). Per lane and block:
+//   A = sum_i x_i (1024 + c_i q_i), c_i = 1 or 16 by pair (the exponent trick above),
+//   y += s * (A_1 + A_16 / 16 - (1024 X_1 + 64 X_16) - z (X_1 + X_16))
+// where X_1, X_16 are the sums of x over the rows of each kind, computed per 32-row segment
+// while x is staged and kept in the 16 bytes that pad the segment's row. Each lane loads the
+// table entry of its own (segment, column) for every block. The four lanes of a column
+// (l, l+16, l+32, l+48) and the waves are then reduced.
+template <int BPW>
+constexpr size_t prep_valu_wave_lds() { return (size_t)BPW * 4 * PREP_SEG_BYTES; }
+
+template <int BPW>
+__global__ void __launch_bounds__(1024)
+gemv_prep_valu_kernel(PrepParams p) {
+    constexpr int XC = BPW / 4;
+    static_assert(BPW % 4 == 0, "blocks per wave");
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int W = blockDim.x >> 6;
+    const int s = blockIdx.x;
+    const int blocks = p.K >> 7;
+    const int col = lane & 15, h = lane >> 4;
+    const unsigned char* strip = p.prep + (size_t)s * p.strip_bytes;
+    const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
+    unsigned char* xs = lds + (size_t)wave * prep_valu_wave_lds<BPW>();
+    float* red = reinterpret_cast<float*>(lds + (size_t)W * prep_valu_wave_lds<BPW>());
+
+    const bufrsrc_t xr = make_rsrc(p.x, (uint32_t)p.K * 2u);
+    const bufrsrc_t tr = make_rsrc(strip, tbytes);
+    const bufrsrc_t wr = make_rsrc(strip + tbytes, (uint32_t)p.K * 8u);
+    u32x4 xv[XC], wv[BPW];
+    uint32_t ev[BPW];
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int c = lane + 64 * i, kb = wave * BPW + (c >> 4);
+        const uint32_t off = kb < blocks ? (uint32_t)(kb * 128 + (c & 15) * 8) * 2u : (uint32_t)p.K * 2u;
+        xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const int kb = wave * BPW + j;
+        // table row of this lane's 32 rows: (32 h) / G of the block's R = 128 / G rows
+        const uint32_t off = kb < blocks ? ((uint32_t)(kb * (128 / p.G) + 32 * h / p.G) * 16u + (uint32_t)col) * 4u : tbytes;
+        ev[j] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(tr, off, 0, 2);
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const uint32_t off = (uint32_t)(wave * BPW + j) * 1024u + (uint32_t)lane * 16u;
+        wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2));
+    }
+
+    // ---- stage x with the per-segment sums
+    const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+        const int c = lane + 64 * i;              // segment c / 4 of the region, quarter c % 4
+        const u32x4 v = xv[i];
+        const float x1 = quad_sum(dot2(as_h2(v.x), one2, dot2(as_h2(v.z), one2, 0.f)));    // rows 0,1,4,5
+        const float x16 = quad_sum(dot2(as_h2(v.y), one2, dot2(as_h2(v.w), one2, 0.f)));   // rows 2,3,6,7
+        unsigned char* row = xs + (size_t)(c >> 2) * PREP_SEG_BYTES;
+        *reinterpret_cast<u32x4*>(row + (c & 3) * 16) = v;
+        if ((c & 3) == 0)
+            *reinterpret_cast<float2*>(row + 64) = make_float2(1024.0f * x1 + 64.0f * x16, x1 + x16);
+    }
+
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const unsigned char* row = xs + (size_t)(j * 4 + h) * PREP_SEG_BYTES;
+        const float2 bx = *reinterpret_cast<const float2*>(row + 64);
+        float a1 = 0.f, a16 = 0.f;
+        const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const u32x4 xq = *reinterpret_cast<const u32x4*>(row + 16 * w);
+            const uint32_t d = wd[w], d8 = d >> 8;
+            a1 = dot2(nib_pair(d), as_h2(xq.x), a1);
+            a16 = dot2(nib_pair16(d), as_h2(xq.y), a16);
+            a1 = dot2(nib_pair(d8), as_h2(xq.z), a1);
+            a16 = dot2(nib_pair16(d8), as_h2(xq.w), a16);
+        }
+        const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)ev[j]), z = (float)(ev[j] >> 16);
+        const float u = __builtin_fmaf(a16, 1.0f / 16.0f, a1) - __builtin_fmaf(z, bx.y, bx.x);
+        y = __builtin_fmaf(sc, u, y);
+    }
+
+    y += shfl_xor_f(y, 16);
+    y += shfl_xor_f(y, 32);
+    if (lane < 16) red[wave * 16 + lane] = y;
+    __syncthreads();
+    if (t < 16) {
+        float acc = 0.f;
+        for (int w = 0; w < W; ++w) acc += red[w * 16 + t];
+        p.out[(size_t)s * 16 + t] = (half_t)acc;
+    }
+}
+
+PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
+    PrepGemvShape s{};
+    if (M != 1 || N % 16 || K % 128 || !prep_group_ok(G) || K % G || K > PREP_MAX_K) return s;
+    const int blocks = K / 128;
+    // blocks per wave: 8 (up to 16 waves), 16 beyond; 4 where 8 would leave fewer than 4 waves
+    int bpw = blocks <= 8 * 16 ? 8 : 16;
+    if (bpw == 8 && blocks < 32) bpw = 4;
+    const int waves = (blocks + bpw - 1) / bpw;
+    s.mfma = G % 128 == 0;
+    s.bpw = bpw;
+    s.waves = waves;
+    const size_t wave_lds = s.mfma ? (bpw == 16 ? prep_mfma_wave_lds<16>() : bpw == 8 ? prep_mfma_wave_lds<8>()
+                                                                                   : prep_mfma_wave_lds<4>())
+                                   : (bpw == 16 ? prep_valu_wave_lds<16>() : bpw == 8 ? prep_valu_wave_lds<8>()
+                                                                                   : prep_valu_wave_lds<4>());
+    s.lds = (size_t)waves * wave_lds + (size_t)waves * 16 * 4;
+    s.ok = waves <= 16 && s.lds <= 160 * 1024;
+    return s;
+}
+
+template <int BPW>
+static void launch_prep_m1_b(const PrepParams& p, const PrepGemvShape& s, hipStream_t st) {
+    const dim3 grid(p.N / 16), block(64 * s.waves);
+    if (s.mfma) hipLaunchKernelGGL((gemv_prep_mfma_kernel<BPW>), grid, block, s.lds, st, p);
+    else hipLaunchKernelGGL((gemv_prep_valu_kernel<BPW>), grid, block, s.lds, st, p);
+}
+
+hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st) {
+    (void)hipGetLastError();
+    switch (s.bpw) {
+        case 4: launch_prep_m1_b<4>(p, s, st); break;
+        case 8: launch_prep_m1_b<8>(p, s, st); break;
+        case 16: launch_prep_m1_b<16>(p, s, st); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace w4a16
