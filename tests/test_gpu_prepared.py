@@ -65,6 +65,11 @@ def test_dequant_prepared_bit_exact(torch_cuda, orc, fmt, K, N, G, transposed):
     (AWQ, 1, 1792, 4096, 128), (AWQ, 1, 4096, 1792, 128),   # one GPU's share of an 8-way TP MLP
     (GPTQ, 1, 32768, 256, 128), (AWQ, 1, 128, 16, 128), (AWQ, 1, 4096, 512, 256),
     (GPTQ, 1, 2048, 256, 2048), (SYM, 1, 4096, 1024, 32),
+    # M = 2..8: config 1's shapes at M = 4 and 8, every M on a smaller shape
+    (AWQ, 4, 4096, 14336, 128), (AWQ, 8, 4096, 14336, 128), (AWQ, 4, 14336, 4096, 128),
+    (AWQ, 8, 14336, 4096, 128), (GPTQ, 2, 1024, 512, 128), (GPTQ, 3, 1024, 512, 128),
+    (SYM, 5, 2048, 256, 128), (AWQ, 6, 1536, 64, 256), (GPTQ, 7, 512, 32, 128),
+    (AWQ, 2, 128, 16, 128), (AWQ, 8, 16384, 128, 128),
 ])
 def test_gemm_prepared_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
     P = pkg()

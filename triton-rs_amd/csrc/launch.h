@@ -226,8 +226,10 @@ struct PrepGemvShape {
     int bpw;      // blocks (128 rows x 16 columns) per wave, at most
     int waves;    // waves per workgroup (one workgroup per strip)
     bool mfma;    // matrix-core dot products (group_size % 128 == 0), else VALU dot2
+    int mp;       // M > 1: rows per block slot of the A operand (2, 4 or 8)
     size_t lds;   // dynamic LDS bytes
 };
+constexpr int PREP_GEMV_MAX_M = 8;
 hipError_t launch_prepare_layout(int fmt, const uint32_t* qweight, const half_t* scales,
                                  const uint32_t* qzeros, void* out, int K, int N, int G,
                                  int zero_offset, hipStream_t st);

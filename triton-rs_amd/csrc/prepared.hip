@@ -398,15 +398,137 @@ gemv_prep_valu_kernel(PrepParams p) {
     }
 }
 
+// M = 2..8: the same strips, waves and blocks, with the activations as MFMA A operands read
+// straight from global memory (x is a few hundred KiB at most and stays in the caches). An
+// A operand has 16 rows and M <= MP rows are needed, so one A register set carries P = 16 / MP
+// blocks: rows [b MP, b MP + MP) hold block b's activations (rows past M repeat row M - 1),
+// and the MFMA of block b leaves its result in those rows of D. The zero point is taken out
+// of the B operand exactly, (1024 + c q) - (1024 + c z) = c (q - z), c = 1 or 16 as in the
+// M = 1 kernel (A carries x / c), so D = sum_k x_k (q_k - z) per block, and y += s D per
+// block and row slot. VALU per 8 weights: one shift, four v_and_or_b32, four v_pk_add_f16.
+// Requires G % 128 == 0 (a block in one group) and blocks per wave BPW = 8.
+template <int MP>
+__global__ void __launch_bounds__(1024)
+gemv_prep_rows_kernel(PrepParams p) {
+    constexpr int BPW = 8, P = 16 / MP, S = BPW / P;   // blocks per A set, A sets per wave
+    constexpr int EC = BPW / 4;
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int W = blockDim.x >> 6;
+    const int s = blockIdx.x;
+    const int M = p.M, blocks = p.K >> 7;
+    const int col = lane & 15, h = lane >> 4;
+    const unsigned char* strip = p.prep + (size_t)s * p.strip_bytes;
+    const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
+    uint32_t* tab = reinterpret_cast<uint32_t*>(lds) + (size_t)wave * BPW * 16;   // BPW x 16
+    float* red = reinterpret_cast<float*>(lds + (size_t)W * BPW * 16 * 4);          // W x P x M x 16
+
+    // ---- loads: table entries, the A sets, then the blocks
+    const bufrsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
+    const bufrsrc_t tr = make_rsrc(strip, tbytes);
+    const bufrsrc_t wr = make_rsrc(strip + tbytes, (uint32_t)p.K * 8u);
+    uint32_t ev[EC];
+    {
+        const uint32_t off = (uint32_t)(wave * BPW * 16 + EC * lane) * 4u;
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(tr, off, 0, 2));
+        ev[0] = v.x; ev[1] = v.y;
+    }
+    u32x4 av[S][4], wv[BPW];
+    {
+        const int slot = col / MP, r = min(col % MP, M - 1);
+#pragma unroll
+        for (int a = 0; a < S; ++a) {
+            const int kb = wave * BPW + a * P + slot;
+            const uint32_t base = kb < blocks ? ((uint32_t)r * (uint32_t)p.K + (uint32_t)(kb * 128 + 32 * h)) * 2u
+                                              : (uint32_t)M * (uint32_t)p.K * 2u;
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                av[a][st] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, base + 16u * st, 0, 0));
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        const uint32_t off = (uint32_t)(wave * BPW + j) * 1024u + (uint32_t)lane * 16u;
+        wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2));
+    }
+#pragma unroll
+    for (int i = 0; i < EC; ++i) tab[EC * lane + i] = ev[i];
+
+    float y[P][4];
+#pragma unroll
+    for (int b = 0; b < P; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) y[b][i] = 0.f;
+#pragma unroll
+    for (int a = 0; a < S; ++a) {
+        half8_t A[4];
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {   // x' = x with the rows of the 16 q pairs / 16
+            const u32x4 v = av[a][st];
+            const half2_t h1 = as_h2(v.y) * (half2_t){(half_t)(1.0f / 16.0f), (half_t)(1.0f / 16.0f)};
+            const half2_t h3 = as_h2(v.w) * (half2_t){(half_t)(1.0f / 16.0f), (half_t)(1.0f / 16.0f)};
+            A[st] = __builtin_bit_cast(half8_t, u32x4{v.x, as_u32(h1), v.z, as_u32(h3)});
+        }
+#pragma unroll
+        for (int b = 0; b < P; ++b) {
+            const int j = a * P + b;
+            const uint32_t e = tab[j * 16 + col];
+            const uint32_t z = e >> 16;
+            // -(1024 + z) and -(1024 + 16 z) as fp16 pairs (z <= 31: exact, bit patterns)
+            const uint32_t ze = ((0x6400u + z) * 0x10001u) | 0x80008000u;
+            const uint32_t zo = ((0x6400u + 16u * z) * 0x10001u) | 0x80008000u;
+            float4_t d = {0.f, 0.f, 0.f, 0.f};
+            const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t q = wd[st], q8 = q >> 8;
+                const u32x4 bw = {as_u32(nib_pair(q) + as_h2(ze)), as_u32(nib_pair16(q) + as_h2(zo)),
+                                  as_u32(nib_pair(q8) + as_h2(ze)), as_u32(nib_pair16(q8) + as_h2(zo))};
+                d = mfma16x16x32(A[st], __builtin_bit_cast(half8_t, bw), d);
+            }
+            const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[b][i] = __builtin_fmaf(sc, d[i], y[b][i]);
+        }
+    }
+
+    // ---- reduce over the waves and the slots: row 4 h + i of slot b is output row
+    // 4 h + i - b MP (each slot holds the sums of its own blocks)
+#pragma unroll
+    for (int b = 0; b < P; ++b)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = 4 * h + i - b * MP;
+            if (m >= 0 && m < MP && m < M) red[((wave * P + b) * M + m) * 16 + col] = y[b][i];
+        }
+    __syncthreads();
+    for (int o = t; o < M * 16; o += blockDim.x) {
+        float acc = 0.f;
+        for (int wb = 0; wb < W * P; ++wb) acc += red[wb * M * 16 + o];
+        p.out[(size_t)(o >> 4) * p.N + (size_t)s * 16 + (o & 15)] = (half_t)acc;
+    }
+}
+
 PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
     PrepGemvShape s{};
-    if (M != 1 || N % 16 || K % 128 || !prep_group_ok(G) || K % G || K > PREP_MAX_K) return s;
+    if (M < 1 || M > PREP_GEMV_MAX_M || N % 16 || K % 128 || !prep_group_ok(G) || K % G || K > PREP_MAX_K)
+        return s;
     const int blocks = K / 128;
+    s.mfma = G % 128 == 0;
+    if (M > 1) {   // rows kernel: 8 blocks per wave, up to 16 waves
+        if (!s.mfma || blocks > 8 * 16) return s;
+        s.bpw = 8;
+        s.waves = (blocks + 7) / 8;
+        s.mp = M <= 2 ? 2 : M <= 4 ? 4 : 8;
+        s.lds = (size_t)s.waves * 8 * 16 * 4 + (size_t)s.waves * (16 / s.mp) * M * 16 * 4;
+        s.ok = true;
+        return s;
+    }
     // blocks per wave: 8 (up to 16 waves), 16 beyond; 4 where 8 would leave fewer than 4 waves
     int bpw = blocks <= 8 * 16 ? 8 : 16;
     if (bpw == 8 && blocks < 32) bpw = 4;
     const int waves = (blocks + bpw - 1) / bpw;
-    s.mfma = G % 128 == 0;
     s.bpw = bpw;
     s.waves = waves;
     const size_t wave_lds = s.mfma ? (bpw == 16 ? prep_mfma_wave_lds<16>() : bpw == 8 ? prep_mfma_wave_lds<8>()
@@ -427,6 +549,13 @@ static void launch_prep_m1_b(const PrepParams& p, const PrepGemvShape& s, hipStr
 
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st) {
     (void)hipGetLastError();
+    if (p.M > 1) {
+        const dim3 grid(p.N / 16), block(64 * s.waves);
+        if (s.mp == 2) hipLaunchKernelGGL(gemv_prep_rows_kernel<2>, grid, block, s.lds, st, p);
+        else if (s.mp == 4) hipLaunchKernelGGL(gemv_prep_rows_kernel<4>, grid, block, s.lds, st, p);
+        else hipLaunchKernelGGL(gemv_prep_rows_kernel<8>, grid, block, s.lds, st, p);
+        return hipGetLastError();
+    }
     switch (s.bpw) {
         case 4: launch_prep_m1_b<4>(p, s, st); break;
         case 8: launch_prep_m1_b<8>(p, s, st); break;
