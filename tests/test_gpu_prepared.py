@@ -117,3 +117,48 @@ def test_act_order_then_prepared(torch_cuda, orc, M, K, N):
     ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx,
                          want_f32=True)[1]
     assert_parity(y, ref.astype(np.float64), what="act-order prepared")
+
+
+@pytest.mark.parametrize("fmt,M,K,N,G", [
+    (AWQ, 9, 1024, 512, 128), (GPTQ, 16, 2048, 768, 128), (AWQ, 64, 4096, 1024, 64),
+    (SYM, 100, 1024, 256, 256), (GPTQ, 300, 2048, 4096, 128),    # prefill tiles, K split
+    (AWQ, 130, 1024, 224, 128),                                  # 224-column tiles
+    (GPTQ, 40, 512, 48, 32), (AWQ, 12, 16384 + 128, 32, 128),    # generic kernel (G = 32, K)
+])
+def test_gemm_prepared_large_m_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=0x5EED0003 + M + K + N)
+    y = P.gemm_prepared(to_dev(p.x), _prep(P, p)).cpu().numpy()
+    rows = np.arange(M) if M <= 64 else np.unique(np.r_[0, M - 1, np.random.default_rng(M).choice(M, 30)])
+    ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, G,
+                              rows.astype(np.int32), zero_offset=p.zero_offset)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"prepared {NAME[fmt]} M={M} K={K} N={N} G={G}")
+
+
+@pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)])
+def test_gemm_prepared_config3_sampled_rows(torch_cuda, orc, K, N):
+    """Config 3 (AWQ, M = 2048) through the prepared layout; 32 sampled rows against the
+    oracle, and bit-identical to the checkpoint kernel on exactly representable inputs is not
+    required (different accumulation order), so the bar is the tolerance."""
+    P = pkg()
+    M = 2048
+    p = Problem(AWQ, M=M, K=K, N=N, G=128, seed=0x5EED0003 + K)
+    y = P.gemm_prepared(to_dev(p.x), _prep(P, p)).cpu().numpy()
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(K).choice(M, 30)]).astype(np.int32)
+    ref = orc.w4a16_gemm_rows(AWQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows, zero_offset=0)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"prepared config 3 K={K} N={N}")
+
+
+def test_gemm_prepared_prefill_exact_arithmetic(torch_cuda, orc):
+    """Exactly representable products and sums: the prefill and generic kernels on prepared
+    weights give the oracle's bits."""
+    P = pkg()
+    g = np.random.default_rng(79)
+    for fmt, M, K, N, G in ((AWQ, 96, 1024, 256, 128), (GPTQ, 20, 512, 48, 32), (SYM, 70, 2048, 512, 64)):
+        p = Problem(fmt, M=M, K=K, N=N, G=G, seed=80 + fmt)
+        p.x = (g.integers(-8, 9, size=p.x.shape) / 4.0).astype(np.float16)
+        p.scales = (2.0 ** g.integers(-8, -4, size=p.scales.shape)).astype(np.float16)
+        y = P.gemm_prepared(to_dev(p.x), _prep(P, p)).cpu().numpy()
+        ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
+                             zero_offset=p.zero_offset)
+        assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), (NAME[fmt], M)

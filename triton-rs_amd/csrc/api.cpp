@@ -530,10 +530,6 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
     if (!aligned(x, 16) || !aligned(prepared, 256) || !aligned(out, 16) || (perm && !aligned(perm, 16)))
         return fail(W4A16_ERR_INVALID_ARG,
                     "x, out and perm must be 16-byte aligned, prepared 256-byte aligned");
-    const PrepGemvShape gs = prep_gemv_shape(M, N, K, G);
-    if (!gs.ok)
-        return fail(W4A16_ERR_UNSUPPORTED, "no prepared-layout kernel for M=%d N=%d K=%d group_size=%d",
-                    M, N, K, G);
     hipStream_t st = static_cast<hipStream_t>(stream);
     const void* xa = x;
     if (perm) {   // act-order checkpoint prepared in group order: x' = x[:, perm]
@@ -545,14 +541,59 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
         if (e != hipSuccess) return hip_fail(e, "act-order gather launch");
         xa = xg;
     }
-    PrepParams p{};
-    p.x = static_cast<const half_t*>(xa);
-    p.prep = static_cast<const unsigned char*>(prepared);
-    p.out = static_cast<half_t*>(out);
-    p.M = M; p.N = N; p.K = K; p.G = G;
-    p.strip_bytes = (uint32_t)prep_strip_bytes(K, G);
-    hipError_t e = launch_prep_gemv(p, gs, st);
-    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared gemv launch");
+    // M <= 8: the GEMV kernels (one workgroup per strip, no split-K)
+    const PrepGemvShape gs = prep_gemv_shape(M, N, K, G);
+    if (gs.ok) {
+        PrepParams p{};
+        p.x = static_cast<const half_t*>(xa);
+        p.prep = static_cast<const unsigned char*>(prepared);
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G;
+        p.strip_bytes = (uint32_t)prep_strip_bytes(K, G);
+        hipError_t e = launch_prep_gemv(p, gs, st);
+        return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared gemv launch");
+    }
+    // larger M: the pipelined prefill kernel reading the prepared strips (64-row stages: the
+    // group size must be a multiple of 64; 32-bit offsets into the prepared buffer)
+    const int cus = device_cus();
+    PrefillShape ps = prefill_shape(FMT_PREP, M, N, K, G, cus);
+    const bool pre_ok = ps.ok && ps.dma && G % 64 == 0 && prep_total_bytes(K, N, G) < ((size_t)1 << 31);
+    if (pre_ok) {
+        PrefillParams p{};
+        p.x = static_cast<const half_t*>(xa);
+        p.qweight = static_cast<const uint32_t*>(prepared);
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G;
+        p.ksplit = ps.ksplit;
+        if (ps.ksplit > 1) {
+            uint32_t* counters = nullptr;
+            float* partials = nullptr;
+            const size_t tiles = (size_t)ps.col_tiles * ps.row_tiles;
+            if (tiles > SPLITK_MAX_TILES) {
+                ps = prefill_shape(FMT_PREP, M, N, K, G, cus, 1);
+                p.ksplit = 1;
+            } else {
+                if (int rc = get_workspace(st, (size_t)ps.ksplit * M * N * sizeof(float), &counters, &partials))
+                    return rc;
+                p.counters = counters;
+                p.ws = partials;
+            }
+        }
+        hipError_t e = launch_prefill(FMT_PREP, p, ps, st);
+        return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared prefill launch");
+    }
+    // any other shape: the generic kernel, dequantising each element from the strips
+    StridedParams p{};
+    p.a = static_cast<const half_t*>(xa);
+    p.qweight = static_cast<const uint32_t*>(prepared);
+    p.c = static_cast<half_t*>(out);
+    p.m = M; p.n = N; p.k = K; p.group_size = G;
+    p.stride_am = K; p.stride_ak = 1;
+    p.stride_qwk = (int)(prep_strip_bytes(K, G) / 4);   // words per strip
+    p.stride_qwn = (int)prep_table_words(K, G);         // words of the strip's table
+    p.stride_cm = N; p.stride_cn = 1;
+    hipError_t e = launch_strided_gemm(FMT_PREP, p, st);
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared strided gemm launch");
 }
 
 // The reference kernels' parameter lists with arbitrary strides. A call whose tensors are

@@ -24,6 +24,9 @@ typedef float float16_t __attribute__((ext_vector_type(16)));
 constexpr int FMT_GPTQ = 0;
 constexpr int FMT_GPTQ_SYM = 1;
 constexpr int FMT_AWQ = 2;
+// Nibble slot of row i (0..7) of a prepared word: (i >> 1) | ((i & 1) << 2), so that
+// (w >> 4 j) & 0x000F000F holds rows (2 j, 2 j + 1).
+__host__ __device__ constexpr int prep_slot(int i) { return (i >> 1) | ((i & 1) << 2); }
 
 constexpr uint32_t MAGIC2 = 0x64006400u;  // (1024, 1024) as two fp16
 

@@ -439,12 +439,21 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     // words] (GPTQ) in eight 1 KB blocks, one per wave; scales by wave 0, zeros by the other
     // waves (identical bytes to one place: a harmless race that keeps the stage free of
     // branches)
-    const i32x4_t wrs = buffer_rsrc(p.qweight, (uint32_t)((size_t)p.K * p.N / 2));
+    // prepared layout: strips of 16 columns, sb bytes each, the table's tb bytes first
+    const uint32_t sb = FMT == FMT_PREP ? (uint32_t)prep_strip_bytes(p.K, p.G) : 0u;
+    const uint32_t tb = FMT == FMT_PREP ? prep_table_words(p.K, p.G) * 4u : 0u;
+    const i32x4_t wrs = buffer_rsrc(p.qweight, FMT == FMT_PREP ? (uint32_t)(p.N / 16) * sb
+                                                               : (uint32_t)((size_t)p.K * p.N / 2));
     const i32x4_t srs = buffer_rsrc(p.scales, (uint32_t)((size_t)(p.K / p.G) * p.N * 2));
     const i32x4_t zrs = buffer_rsrc(p.qzeros ? (const void*)p.qzeros : (const void*)p.scales,
                                     p.qzeros ? (uint32_t)((size_t)(p.K / p.G) * NW * 4) : 0u);
     uint32_t woff;
-    if constexpr (FMT == FMT_AWQ) {
+    if constexpr (FMT == FMT_PREP) {
+        // a stage is half a block (64 rows, 512 bytes) of each of the tile's 16 strips: wave w
+        // loads strips 2 w and 2 w + 1
+        const int sl = 2 * wave + (lane >> 5);
+        woff = 16 * sl < BN ? (uint32_t)(n0 / 16 + sl) * sb + tb + (uint32_t)(lane & 31) * 16u : DMA_OOB;
+    } else if constexpr (FMT == FMT_AWQ) {
         const int row = wave * 8 + (lane >> 3), chunk = lane & 7;   // 4 words per lane
         woff = 4 * chunk < BWC
                    ? ((uint32_t)row * (uint32_t)NW + (uint32_t)(n0 >> 3) + 4u * chunk) * 4u
@@ -453,15 +462,23 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         woff = 4 * lane < BN ? ((uint32_t)wave * (uint32_t)p.N + (uint32_t)n0 + 4u * lane) * 4u
                              : DMA_OOB;                          // packed row `wave`
     }
-    const bool zw_wave = FMT != FMT_GPTQ_SYM && wave != 0;
-    const i32x4_t szrs = zw_wave ? zrs : srs;
-    const uint32_t szoff = zw_wave ? (lane * 4 < BWC ? ((uint32_t)(n0 >> 3) + 4u * lane) * 4u : DMA_OOB)
+    const bool zw_wave = FMT != FMT_GPTQ_SYM && FMT != FMT_PREP && wave != 0;
+    const i32x4_t szrs = FMT == FMT_PREP ? wrs : zw_wave ? zrs : srs;
+    // prepared: the stage's table row (64 bytes of each strip, 1 KB), by wave 0
+    const uint32_t szoff = FMT == FMT_PREP ? (16 * (lane >> 2) < BN ? (uint32_t)(n0 / 16 + (lane >> 2)) * sb + (uint32_t)(lane & 3) * 16u : DMA_OOB)
+                         : zw_wave ? (lane * 4 < BWC ? ((uint32_t)(n0 >> 3) + 4u * lane) * 4u : DMA_OOB)
                                    : (lane < BWC ? ((uint32_t)n0 + 8u * lane) * 2u : DMA_OOB);
     const uint32_t szrow = zw_wave ? (uint32_t)NW * 4u : (uint32_t)p.N * 2u;   // bytes per group
     const int szdst = RAW_W + (zw_wave ? RAW_S : 0);
     auto dma_b = [&](int slot, int s) {
         char* dst = Raw + slot * RAW_ST;
         const int k0 = (s0 + s) * BK, g = k0 / p.G;
+        if constexpr (FMT == FMT_PREP) {
+            const int row = (k0 >> 7) * prep_table_rows(p.G) + (p.G < 128 ? (k0 & 127) / p.G : 0);
+            if (wave == 0) dma16(szrs, dst + szdst, szoff + (uint32_t)row * 64u);
+            dma16(wrs, dst + wave * 1024, woff + (uint32_t)(k0 >> 7) * 1024u + (uint32_t)((k0 >> 6) & 1) * 512u);
+            return;
+        }
         const uint32_t wstep = (FMT == FMT_AWQ) ? (uint32_t)k0 * (uint32_t)NW * 4u
                                                 : (uint32_t)(k0 >> 3) * (uint32_t)p.N * 4u;
         dma16(szrs, dst + szdst, szoff + (uint32_t)g * szrow);
@@ -478,15 +495,36 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     const int bw = DQC == 4 ? (t & 31) : (t & 15);
     const int hh = DQC == 4 ? ((t >> 5) & 1) : ((t >> 4) & 3);
     const int kq = t >> 6;
+    // prepared layout: thread t dequantises column pn, half ph (rows 32 ph .. 32 ph + 31 of
+    // the stage), words DQC pq .. of its lane chunk
+    const int pn = DQC == 4 ? (t & 255) : (t & 127);
+    const int ph = DQC == 4 ? (t >> 8) : ((t >> 7) & 1);
+    const int pq = DQC == 4 ? 0 : (t >> 8);
+    (void)pn; (void)ph; (void)pq;
     static_assert(BN <= 128 || BN > 192, "tile width");
     (void)DQW;
 
     // The dequantisation comes in three parts, so that its VALU work can be placed between
     // the MFMAs of a stage: raw reads from the ring slot, per-column arithmetic, LDS writes.
-    struct DqRaw { uint32_t sv[2]; uint32_t zw; uint32_t w[8]; };
+    struct DqRaw { uint32_t sv[2]; uint32_t zw; uint32_t w[8]; uint32_t e[4]; };
     auto dq_load = [&](int slot) {
         DqRaw d;
         const char* src = Raw + slot * RAW_ST;
+        if constexpr (FMT == FMT_PREP) {
+            // thread (column pn, half ph, part pq): words DQC pq .. DQC pq + DQC - 1 of lane
+            // pn % 16 + 16 ph of strip pn / 16 (16-byte lane chunks read whole, conflict-free),
+            // and the column's table entry
+            const uint32_t* wp = reinterpret_cast<const uint32_t*>(src + (pn >> 4) * 512 + ((pn & 15) + 16 * ph) * 16) + DQC * pq;
+            if constexpr (DQC == 4) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(wp);
+                d.w[0] = v.x; d.w[1] = v.y; d.w[2] = v.z; d.w[3] = v.w;
+            } else {
+                const u32x2 v = *reinterpret_cast<const u32x2*>(wp);
+                d.w[0] = v.x; d.w[1] = v.y;
+            }
+            d.e[0] = reinterpret_cast<const uint32_t*>(src + RAW_W)[pn];
+            return d;
+        }
         const uint32_t* sc32 = reinterpret_cast<const uint32_t*>(src + RAW_W);
         if constexpr (DQC == 4) { d.sv[0] = sc32[4 * bw + 2 * hh]; d.sv[1] = sc32[4 * bw + 2 * hh + 1]; }
         else { d.sv[0] = sc32[4 * bw + hh]; d.sv[1] = 0u; }
@@ -510,6 +548,15 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     // column c (0 .. DQC-1) of the thread's columns, as the 8 k of one B-operand chunk
     auto dq_col = [&](const DqRaw& d, int c) -> u32x4 {
         const int cc = DQC * hh + c;   // column within its 8-column group
+        if constexpr (FMT == FMT_PREP) {
+            // word c: 8 rows of the thread's column; scale and zero point from the entry;
+            // rows in natural order, pairs (2 i, 2 i + 1)
+            const uint32_t e = d.e[0], zb = 0x6400u + (e >> 16);
+            const half2_t hz = as_h2(zb | (zb << 16)), hs = as_h2(perm(e, e, 0x01000100u));
+            const uint32_t w = d.w[c];
+            return pack8(deq2(nib_pair(w), hz, hs), deq2(nib_pair(w >> 4), hz, hs),
+                         deq2(nib_pair(w >> 8), hz, hs), deq2(nib_pair(w >> 12), hz, hs));
+        }
         const uint32_t sw = DQC == 4 ? d.sv[c >> 1] : d.sv[0];
         const half2_t hs = as_h2(perm(sw, sw, (c & 1) ? 0x07060706u : 0x05040504u));
         if constexpr (FMT == FMT_AWQ) {
@@ -541,6 +588,12 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         }
     };
     auto dq_store = [&](int buf, const u32x4 (&col)[DQC]) {
+        if constexpr (FMT == FMT_PREP) {   // k chunks 4 ph + DQC pq + c of column pn
+#pragma unroll
+            for (int c = 0; c < DQC; ++c)
+                *reinterpret_cast<u32x4*>(Bs + buf * B_ST + (4 * ph + DQC * pq + c) * 256 * 8 + 8 * bpos(pn)) = col[c];
+            return;
+        }
         half_t* B = Bs + buf * B_ST + kq * 256 * 8;
 #pragma unroll
         for (int c = 0; c < DQC; ++c)
@@ -806,7 +859,9 @@ static hipError_t launch_dma_any(int fmt, const PrefillParams& p, int bm, int bn
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (fmt == FMT_AWQ) launch_dma_fmt<FMT_AWQ, MOE>(p, bm, bn, grid, lds, st);
     else if (fmt == FMT_GPTQ) launch_dma_fmt<FMT_GPTQ, MOE>(p, bm, bn, grid, lds, st);
-    else launch_dma_fmt<FMT_GPTQ_SYM, MOE>(p, bm, bn, grid, lds, st);
+    else if (fmt == FMT_GPTQ_SYM) launch_dma_fmt<FMT_GPTQ_SYM, MOE>(p, bm, bn, grid, lds, st);
+    else if constexpr (!MOE) launch_dma_fmt<FMT_PREP, false>(p, bm, bn, grid, lds, st);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -1,4 +1,6 @@
 // Launchers for the generic strided GEMM (strided_body.h) and the standalone dequant kernels.
+#include <type_traits>
+
 #include "strided_body.h"
 
 namespace w4a16 {
@@ -13,7 +15,9 @@ static void launch_strided_e(int fmt, const StridedParams& p, hipStream_t st) {
     const dim3 grid((p.m + STR_BM - 1) / STR_BM, (p.n + STR_BN - 1) / STR_BN), block(256);
     if (fmt == FMT_AWQ) hipLaunchKernelGGL((strided_gemm_kernel<FMT_AWQ, E>), grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ) hipLaunchKernelGGL((strided_gemm_kernel<FMT_GPTQ, E>), grid, block, 0, st, p);
-    else hipLaunchKernelGGL((strided_gemm_kernel<FMT_GPTQ_SYM, E>), grid, block, 0, st, p);
+    else if (fmt == FMT_GPTQ_SYM) hipLaunchKernelGGL((strided_gemm_kernel<FMT_GPTQ_SYM, E>), grid, block, 0, st, p);
+    else if constexpr (std::is_same<E, half_t>::value)   // prepared layout: fp16 only
+        hipLaunchKernelGGL((strided_gemm_kernel<FMT_PREP, E>), grid, block, 0, st, p);
 }
 
 hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st, bool bf16) {

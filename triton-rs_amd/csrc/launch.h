@@ -8,6 +8,10 @@ namespace w4a16 {
 
 typedef _Float16 half_t;
 
+// Kernel-internal format id of the prepared layout (prepared.hip), beside the w4a16_format
+// values 0..2; never accepted from callers.
+constexpr int FMT_PREP = 3;
+
 constexpr int GEMV_MAX_M = 4;        // VALU dot products
 constexpr int GEMV_MFMA_MAX_M = 8;   // AWQ with matrix-core dot products
 

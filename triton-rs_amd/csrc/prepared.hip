@@ -33,9 +33,6 @@
 
 namespace w4a16 {
 
-// nibble slot of row i (0..7) of a prepared word
-__host__ __device__ constexpr int prep_slot(int i) { return (i >> 1) | ((i & 1) << 2); }
-
 // ------------------------------------------------------------------ one-time repack
 
 // One thread per prepared word: grid (N / 16 strips, K / 128 blocks), 256 threads = the

@@ -63,6 +63,20 @@ __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
             if (gn < p.n && kk < p.k) {
                 uint32_t word;
                 int slot;
+                if constexpr (FMT == FMT_PREP) {
+                    // prepared layout: strip gn / 16 is stride_qwk words, its table the first
+                    // stride_qwn of them (rows of 16 entries, R per 128-row block)
+                    const uint32_t* strip = p.qweight + (int64_t)(gn >> 4) * p.stride_qwk;
+                    const int kb = kk >> 7, col = gn & 15;
+                    word = strip[p.stride_qwn + kb * 256 + (col + 16 * ((kk >> 5) & 3)) * 4 + ((kk >> 3) & 3)];
+                    const int R = p.group_size < 128 ? 128 / p.group_size : 1;
+                    const int r = p.group_size < 128 ? (kk & 127) / p.group_size : 0;
+                    const uint32_t e = strip[(kb * R + r) * 16 + col];
+                    const E s = (E)(float)__builtin_bit_cast(half_t, (uint16_t)e);
+                    v = dequant1(nib(word, prep_slot(kk & 7)), (int)(e >> 16), s);
+                    bv[i] = v;
+                    continue;
+                }
                 if constexpr (FMT == FMT_AWQ) {
                     word = p.qweight[(int64_t)kk * p.stride_qwk + (int64_t)(gn >> 3) * p.stride_qwn];
                     slot = awq_slot(gn);
