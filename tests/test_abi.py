@@ -195,7 +195,7 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
                or "gemv_awq_rows_kernel" in k}
     strided = {k: v for k, v in _disassemble_tu(strided_o, tmp_path).items()
                if "strided_gemm_kernel" in k}
-    assert len(gemv) >= 24 and len(gemv_mc) >= 8 and len(strided) == 6
+    assert len(gemv) >= 24 and len(gemv_mc) >= 8 and len(strided) == 7   # 6 + prepared (fp16)
     for name, body in gemv.items():
         assert "v_mfma" not in body, name
         assert "v_dot2" in body, name
@@ -205,6 +205,24 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
         bf16 = "DF16b" in name        # the __bf16 element type in the mangled name
         assert ("v_mfma_f32_16x16x32_bf16" if bf16 else "v_mfma_f32_16x16x32_f16") in body, name
         assert ("v_cvt_pk_bf16_f32" in body) == bf16, name
+
+
+def test_prepared_kernels_isa(tmp_path):
+    """Prepared-layout kernels: the M = 1 and M = 2..8 GEMVs run their dot products on fp16
+    MFMA (one shift and four v_and_or_b32 per word feed them), the group-size-32/64 GEMV on
+    v_dot2 without MFMA; no split-K atomics anywhere in them."""
+    o = os.path.join(ROOT, "triton-rs_amd", "_build", "prepared.o")
+    if not os.path.exists(o):
+        pytest.skip("build objects not present (run build first)")
+    k = _disassemble_tu(o, tmp_path)
+    mf = {n: b for n, b in k.items() if "gemv_prep_mfma_kernel" in n or "gemv_prep_rows_kernel" in n}
+    va = {n: b for n, b in k.items() if "gemv_prep_valu_kernel" in n}
+    assert len(mf) >= 6 and len(va) >= 3
+    for n, b in mf.items():
+        assert "v_mfma_f32_16x16x32_f16" in b and "v_and_or_b32" in b, n
+        assert "atomic" not in b, n
+    for n, b in va.items():
+        assert "v_mfma" not in b and "v_dot2" in b and "atomic" not in b, n
 
 
 def test_bf16_flag_plans_generic_kernel_and_is_refused_elsewhere():
