@@ -217,6 +217,13 @@ PMC_WORKLOADS = {
     "c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128, False),
     "c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128, False),
     "c4_moe": None,
+    # the same shapes on weights in the prepared layout (w4a16_prepare_layout)
+    "prep_headline": HEADLINE + (False,),
+    "prep_c0": ("gptq_sym", 1, 4096, 4096, 128, False),
+    "prep_c1_m1_k14336_n4096": ("awq", 1, 14336, 4096, 128, False),
+    "prep_c1_m8_k4096_n14336": ("awq", 8, 4096, 14336, 128, False),
+    "prep_c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128, False),
+    "prep_c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128, False),
 }
 
 
@@ -268,8 +275,18 @@ def pmc_child(args) -> int:
         g_idx = c2_g_idx(torch, dev, K, G) if act_order else None
         x = torch.randn((M, K), device=dev).half()
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        for i in range(PMC_WARM + PMC_MEASURED):
-            pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G, g_idx=g_idx, out=out)
+        if args.pmc_workload.startswith("prep_"):
+            prep = [pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
+                    for qw, sc, qz in sets]
+            del sets
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            for i in range(PMC_WARM + PMC_MEASURED):
+                pkg.gemm_prepared(x, prep[i % len(prep)], out=out)
+            sets = prep
+        else:
+            for i in range(PMC_WARM + PMC_MEASURED):
+                pkg.gemm(x, *sets[i % len(sets)], fmt=fmt, group_size=G, g_idx=g_idx, out=out)
         del sets
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -430,10 +447,11 @@ def extras(torch, pkg, dev, stream, args):
     for M in (1, 4, 8):
         gemm_case(f"c1_awq_m{M}_k14336_n4096", "awq", M, 14336, 4096, 128, 20, 1000)
     g_idx = c2_g_idx(torch, dev)
+    # 40 weight sets of 13.4 MB (537 MB, past the 256 MB Infinity Cache)
     for M in (16, 32, 64):
-        gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 20, 500,
+        gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 40, 500,
                   g_idx=g_idx)
-        gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 20, 500)
+        gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 40, 500)
 
     # config 2's act-order layer through the one-time group-order repack: gather + plain kernel
     def prepared_case(tag, M, n_sets, calls):
@@ -454,11 +472,51 @@ def extras(torch, pkg, dev, stream, args):
         del sets, prep
 
     for M in (16, 64):
-        prepared_case(f"c2_gptq_actorder_prepared_m{M}_k4096_n6144", M, 20, 500)
+        prepared_case(f"c2_gptq_actorder_prepared_m{M}_k4096_n6144", M, 40, 500)
     prepared_case("c2_gptq_actorder_prepared_m2048_k4096_n6144", 2048, 2, 200)
 
     gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
     gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
+
+    # the prepared layout (w4a16_prepare_layout once per weight set, then w4a16_gemm_prepared);
+    # the one-time prepare is timed on its own (one call, after a warm-up call)
+    def layout_case(tag, fmt, M, K, N, G, n_sets, calls):
+        sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
+        qw, sc, qz = sets[0]
+        pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
+        ev1.record()
+        torch.cuda.synchronize()
+        prep_us = ev0.elapsed_time(ev1) * 1e3
+        preps = []
+        for i in range(n_sets):
+            qw, sc, qz = sets[i]
+            preps.append(pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1))
+            sets[i] = None   # the checkpoint copy is not needed any more
+        torch.cuda.synchronize()
+        del sets
+        torch.cuda.empty_cache()
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+        def fn(i):
+            pkg.gemm_prepared(x, preps[i % n_sets], out=out)
+        ms = time_calls(torch, fn, GRAPH_CALLS, 10, stream, n_sets, batch_calls=calls)[1]
+        record(tag, fmt, M, K, N, G, ms, "prepared/" + ("gemv" if M <= 8 else "prefill"))
+        res[tag]["prepare_once_us"] = round(prep_us, 1)
+        res[tag]["prepared_bytes"] = pkg.prepared_bytes(K, N, G)
+        del preps
+        torch.cuda.empty_cache()
+
+    layout_case("prepared_c0_gptq_sym_m1_k4096_n4096", "gptq_sym", 1, 4096, 4096, 128, 60, 1000)
+    for M in (1, 4, 8):
+        layout_case(f"prepared_c1_awq_m{M}_k4096_n14336", "awq", M, 4096, 14336, 128, 20, 1000)
+        layout_case(f"prepared_c1_awq_m{M}_k14336_n4096", "awq", M, 14336, 4096, 128, 20, 1000)
+    layout_case("prepared_c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
+    layout_case("prepared_c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
 
     # one GPU's share of an 8-way tensor-parallel MLP at its real shape: gate/up split by
     # columns (N / 8 = 1792), down split by rows (K / 8 = 1792); 150 weight sets (> 512 MB)
