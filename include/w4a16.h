@@ -109,8 +109,9 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
  * results as w4a16_gemm, but the split-K scratch (counters, fixed-point hand-off slots,
  * fp32 partials) lives in a fixed device array of w4a16_gemm_noalloc_scratch_bytes() bytes
  * (8 MiB: at most 1024 split-K tiles and 6.9 MiB of partials), one per device, held until the
- * process ends; the call itself allocates nothing. Requests beyond those limits fail with
- * W4A16_ERR_UNSUPPORTED (a prefill whose K split would exceed them runs unsplit instead).
+ * process ends; the call itself allocates nothing. A call whose planned kernel would need
+ * more than that runs a kernel that needs no scratch instead (the prefill kernel without a K
+ * split, or the generic kernel), so its result may differ from w4a16_gemm's in the last bits.
  * All calls on one device share its array: calls that overlap in time on one device (other
  * streams or threads) race and must be serialised by the caller. The device's array is set
  * up by w4a16_init (recommended before capture) or by the first call on the device. */

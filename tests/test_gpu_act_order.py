@@ -92,3 +92,37 @@ def test_prepare_rejects_uneven_groups(torch_cuda):
     bad[5] = 4
     with pytest.raises(P.InvalidArgument, match="outside"):
         P.prepare_act_order(to_dev(p.qweight), to_dev(bad), group_size=128)
+
+
+@pytest.mark.parametrize("M,K", [(3, 1664), (5, 1152), (1, 4224)])
+def test_gather_uneven_share(torch_cuda, orc, M, K):
+    """A few rows and a K whose 8-column chunks do not divide evenly over the workgroups that
+    share a row (M=3, K=1664: 208 chunks, 6 workgroups of 35, the last one 33): every output
+    column still gathered once, product against the oracle's act-order GEMM."""
+    P = pkg()
+    p = Problem(GPTQ, M=M, K=K, N=256, G=128, seed=0x5EED4000 + K, act_order=True)
+    qout, perm = _prepare(P, p)
+    y = P.gemm_act_order(to_dev(p.x), qout, to_dev(p.scales), to_dev(p.qzeros), perm).cpu().numpy()
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, 256, 128, g_idx=p.g_idx,
+                         want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"act-order gather M={M} K={K}")
+
+
+def test_gather_fallback_kernel_with_unaligned_perm(torch_cuda, orc):
+    """perm at a 4-byte (not 16-byte) offset: the gather reads x's columns straight from global
+    memory (the kernel kept for unaligned buffers); same product as the staged gather."""
+    torch = torch_cuda
+    P = pkg()
+    M, K, N = 7, 2048, 384
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED4100, act_order=True)
+    qout, perm = _prepare(P, p)
+    buf = torch.empty(K + 1, dtype=torch.int32, device="cuda:0")
+    buf[1:] = perm
+    perm_u = buf[1:]
+    assert perm_u.data_ptr() % 16 != 0
+    y_u = P.gemm_act_order(to_dev(p.x), qout, to_dev(p.scales), to_dev(p.qzeros), perm_u).cpu().numpy()
+    y = P.gemm_act_order(to_dev(p.x), qout, to_dev(p.scales), to_dev(p.qzeros), perm).cpu().numpy()
+    assert np.array_equal(y_u.view(np.uint16), y.view(np.uint16))
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx,
+                         want_f32=True)[1]
+    assert_parity(y_u, ref.astype(np.float64), what="act-order fallback gather")

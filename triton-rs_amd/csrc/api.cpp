@@ -286,6 +286,23 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
                         "(M=%d N=%d K=%d)", partial_bytes, src.max_partial_bytes, M, N, K);
         return src.get(st, partial_bytes, sc);
     };
+    // A fixed scratch area (w4a16_gemm_noalloc) may be too small for the split-K partials of
+    // the planned GEMV or small-batch kernel (e.g. AWQ M = 8 on a 70B-class MLP: 7 MiB): such
+    // a call takes the prefill kernel without a K split instead, which needs no scratch.
+    auto scratch_fits = [&](size_t tiles, size_t partial_bytes) {
+        return tiles <= src.max_tiles && partial_bytes <= src.max_partial_bytes;
+    };
+    if (kernel == W4A16_KERNEL_SKINNY) {
+        const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd);
+        if (s.splits > 1 && !scratch_fits((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float)))
+            kernel = g_idx ? W4A16_KERNEL_STRIDED
+                           : prefill_shape(fmt, M, N, K, G, cus, 1).ok ? W4A16_KERNEL_PREFILL
+                                                                       : W4A16_KERNEL_STRIDED;
+    } else if (kernel == W4A16_KERNEL_GEMV) {
+        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd);
+        if (s.splits > 1 && !scratch_fits((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float)))
+            kernel = prefill_shape(fmt, M, N, K, G, cus, 1).ok ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
+    }
 
     if (kernel == W4A16_KERNEL_SKINNY) {
         const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd);

@@ -199,9 +199,11 @@ constexpr size_t prep_mfma_wave_lds() { return (size_t)BPW * (4 * PREP_SEG_BYTES
 template <int BPW>
 __global__ void __launch_bounds__(1024)
 gemv_prep_mfma_kernel(PrepParams p) {
-    constexpr int XC = BPW / 4;   // 16-byte chunks of x per lane: 16 per block
-    constexpr int EC = BPW / 4;   // (block, column) table entries per lane: 16 per block
-    static_assert(BPW % 4 == 0, "blocks per wave");
+    // 16-byte chunks of x per lane (16 per block) and (block, column) table entries per
+    // lane (16 per block); with BPW = 2 only lanes 0..31 load them
+    constexpr int XC = BPW >= 4 ? BPW / 4 : 1;
+    constexpr int EC = BPW >= 4 ? BPW / 4 : 1;
+    static_assert(BPW == 2 || BPW % 4 == 0, "blocks per wave");
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -224,12 +226,13 @@ gemv_prep_mfma_kernel(PrepParams p) {
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
         const int c = lane + 64 * i, kb = wave * BPW + (c >> 4);   // chunk c: block c / 16 of the wave
-        const uint32_t off = kb < blocks ? (uint32_t)(kb * 128 + (c & 15) * 8) * 2u : (uint32_t)p.K * 2u;
+        const uint32_t off = kb < blocks && c < 16 * BPW ? (uint32_t)(kb * 128 + (c & 15) * 8) * 2u
+                                                         : (uint32_t)p.K * 2u;
         xv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
     }
     {   // the wave's BPW x 16 entries are contiguous: EC consecutive ones per lane, one load
         // (streaming: with the default policy the same entries cost 0.3 us more per call)
-        const uint32_t off = (uint32_t)(wave * BPW * 16 + EC * lane) * 4u;
+        const uint32_t off = EC * lane < 16 * BPW ? (uint32_t)(wave * BPW * 16 + EC * lane) * 4u : tbytes;
         if constexpr (EC == 1) {
             ev[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(tr, off, 0, 2);
         } else if constexpr (EC == 2) {
@@ -257,12 +260,15 @@ gemv_prep_mfma_kernel(PrepParams p) {
         const half2_t a1 = as_h2(v.y) * s16, a3 = as_h2(v.w) * s16;
         const float sp = row16_sum(dot2(a0, one2, dot2(a1, one2, dot2(a2, one2, dot2(a3, one2, 0.f)))));
         const float sx = row16_sum(dot2(a0, one2, dot2(as_h2(v.y), one2, dot2(a2, one2, dot2(as_h2(v.w), one2, 0.f)))));
-        unsigned char* row = xs + (size_t)(c >> 2) * PREP_SEG_BYTES;
-        *reinterpret_cast<u32x4*>(row + (c & 3) * 16) = u32x4{as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)};
-        if ((c & 15) == 0) bsum[c >> 4] = make_float2(1024.0f * sp, sx);
+        if (c < 16 * BPW) {
+            unsigned char* row = xs + (size_t)(c >> 2) * PREP_SEG_BYTES;
+            *reinterpret_cast<u32x4*>(row + (c & 3) * 16) = u32x4{as_u32(a0), as_u32(a1), as_u32(a2), as_u32(a3)};
+            if ((c & 15) == 0) bsum[c >> 4] = make_float2(1024.0f * sp, sx);
+        }
     }
 #pragma unroll
-    for (int i = 0; i < EC; ++i) tab[EC * lane + i] = ev[i];
+    for (int i = 0; i < EC; ++i)
+        if (EC * lane + i < 16 * BPW) tab[EC * lane + i] = ev[i];
     // the region is this wave's alone: its LDS writes are ordered before its reads below
 
     // ---- blocks: four MFMAs each
