@@ -35,30 +35,37 @@ namespace w4a16 {
 
 // ------------------------------------------------------------------ one-time repack
 
-// One thread per prepared word: grid (N / 16 strips, K / 128 blocks), 256 threads = the
-// block's 64 lanes x 4 words, so the stores of a workgroup are one contiguous 1 KiB.
+// Grid (ceil(N / 256), K / 128): a workgroup writes block kb of 16 consecutive strips, thread
+// t word t of each (lane t / 4, word t % 4), so its stores are 16 contiguous KiB and it reads
+// whole 128-byte lines of the checkpoint (AWQ: 128 rows x 32 words; GPTQ: 16 packed rows x
+// 256 columns). With one workgroup per strip the 16 strips sharing a line ran on different
+// XCDs and each fetched it: the AWQ repack read 8.7x its input from HBM.
 template <int FMT>
 __global__ void __launch_bounds__(256)
 prep_weights_kernel(const uint32_t* __restrict__ qw, uint32_t* __restrict__ out, int K, int N,
                     uint32_t strip_words, uint32_t table_words) {
-    const int s = blockIdx.x, kb = blockIdx.y, t = threadIdx.x;
+    const int kb = blockIdx.y, t = threadIdx.x;
     const int l = t >> 2, w = t & 3;
-    const int n = 16 * s + (l & 15);
     const int k0 = 128 * kb + 32 * (l >> 4) + 8 * w;
-    uint32_t r = 0;
-    if constexpr (FMT == FMT_AWQ) {
-        const int NW = N >> 3, sl = awq_slot(n);
+    for (int si = 0; si < 16; ++si) {
+        const int s = 16 * blockIdx.x + si;
+        if (16 * s >= N) break;
+        const int n = 16 * s + (l & 15);
+        uint32_t r = 0;
+        if constexpr (FMT == FMT_AWQ) {
+            const int NW = N >> 3, sl = awq_slot(n);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t v = qw[(size_t)(k0 + i) * NW + (n >> 3)];
-            r |= ((v >> (4 * sl)) & 0xFu) << (4 * prep_slot(i));
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t v = qw[(size_t)(k0 + i) * NW + (n >> 3)];
+                r |= ((v >> (4 * sl)) & 0xFu) << (4 * prep_slot(i));
+            }
+        } else {
+            const uint32_t v = qw[(size_t)(k0 >> 3) * N + n];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r |= ((v >> (4 * i)) & 0xFu) << (4 * prep_slot(i));
         }
-    } else {
-        const uint32_t v = qw[(size_t)(k0 >> 3) * N + n];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r |= ((v >> (4 * i)) & 0xFu) << (4 * prep_slot(i));
+        out[(size_t)s * strip_words + table_words + (size_t)kb * 256 + t] = r;
     }
-    out[(size_t)s * strip_words + table_words + (size_t)kb * 256 + t] = r;
 }
 
 // One thread per table entry (block, row, column) of every strip; the same threads also
@@ -93,7 +100,7 @@ hipError_t launch_prepare_layout(int fmt, const uint32_t* qweight, const half_t*
     (void)hipGetLastError();
     const uint32_t sw = (uint32_t)(prep_strip_bytes(K, G) / 4), tw = prep_table_words(K, G);
     uint32_t* ow = static_cast<uint32_t*>(out);
-    const dim3 gw(N / 16, K / 128);
+    const dim3 gw((N + 255) / 256, K / 128);
     const int64_t metas = (int64_t)(N / 16) * tw;   // entries and padding
     const dim3 gm((unsigned)((metas + 255) / 256));
     if (fmt == FMT_AWQ) {
