@@ -86,6 +86,14 @@ extern "C" {
     fn w4a16_gemm_act_order(stream: *mut c_void, fmt: i32, x: u64, qweight: u64, scales: u64,
                             qzeros: u64, perm: u64, out: u64, m: i32, n: i32, k: i32,
                             group_size: i32, gptq_zero_offset: i32) -> i32;
+    fn w4a16_prepared_bytes(k: i32, n: i32, group_size: i32) -> usize;
+    fn w4a16_prepare_layout(stream: *mut c_void, fmt: i32, qweight: u64, scales: u64, qzeros: u64,
+                            k: i32, n: i32, group_size: i32, gptq_zero_offset: i32,
+                            prepared: u64, prepared_bytes: usize) -> i32;
+    fn w4a16_gemm_prepared(stream: *mut c_void, x: u64, prepared: u64, perm: u64, out: u64,
+                           m: i32, n: i32, k: i32, group_size: i32) -> i32;
+    fn w4a16_dequant_prepared(stream: *mut c_void, prepared: u64, out: u64, k: i32, n: i32,
+                              group_size: i32, transposed: i32) -> i32;
     fn w4a16_fused_moe_workspace_size(t: i32, e: i32, topk: i32, i: i32, k: i32,
                                       block_m: i32) -> usize;
     fn w4a16_fused_moe(stream: *mut c_void, fmt: i32, x: u64, router_logits: u64, t: i32, k: i32,
@@ -318,6 +326,44 @@ pub fn gemm_act_order(stream: &HipStream, fmt: Format, x: u64, w_prepared: &Quan
     check(unsafe {
         w4a16_gemm_act_order(stream.0, fmt as i32, x, w_prepared.qweight, w_prepared.scales,
                              w_prepared.qzeros, perm, out, m, n, k, group_size, gptq_zero_offset)
+    })
+}
+
+/// Bytes of the prepared layout of a K x N matrix (0: shape not supported: N % 16, K % 128,
+/// K <= 32768, group size 32, 64 or a multiple of 128).
+pub fn prepared_bytes(k: i32, n: i32, group_size: i32) -> usize {
+    // SAFETY: pure function of its arguments.
+    unsafe { w4a16_prepared_bytes(k, n, group_size) }
+}
+
+/// One-time rewrite of a checkpoint matrix into the prepared layout at `prepared` (256-byte
+/// aligned, `prepared_bytes` long, not overlapping the checkpoint). Asynchronous on `stream`.
+#[allow(clippy::too_many_arguments)]
+pub fn prepare_layout(stream: &HipStream, fmt: Format, w: &QuantWeights, k: i32, n: i32,
+                      group_size: i32, gptq_zero_offset: i32, prepared: u64,
+                      prepared_bytes: usize) -> Result<(), RuntimeError> {
+    // SAFETY: as for gemm.
+    check(unsafe {
+        w4a16_prepare_layout(stream.0, fmt as i32, w.qweight, w.scales, w.qzeros, k, n,
+                             group_size, gptq_zero_offset, prepared, prepared_bytes)
+    })
+}
+
+/// out[M, N] = x[M, K] @ W16 from prepared weights, any M; `perm` 0, or the permutation of an
+/// act-order checkpoint repacked by `prepare_act_order` before `prepare_layout`.
+#[allow(clippy::too_many_arguments)]
+pub fn gemm_prepared(stream: &HipStream, x: u64, prepared: u64, perm: u64, out: u64, m: i32,
+                     n: i32, k: i32, group_size: i32) -> Result<(), RuntimeError> {
+    // SAFETY: as for gemm.
+    check(unsafe { w4a16_gemm_prepared(stream.0, x, prepared, perm, out, m, n, k, group_size) })
+}
+
+/// The fp16 weights of a prepared matrix, [K, N] or (transposed) [N, K], bit-exact.
+pub fn dequant_prepared(stream: &HipStream, prepared: u64, out: u64, k: i32, n: i32,
+                        group_size: i32, transposed: bool) -> Result<(), RuntimeError> {
+    // SAFETY: as for gemm.
+    check(unsafe {
+        w4a16_dequant_prepared(stream.0, prepared, out, k, n, group_size, transposed as i32)
     })
 }
 
