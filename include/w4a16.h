@@ -146,13 +146,16 @@ W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const v
  * ferrum's loader ships qweight, scales and qzeros; awq_gemm_int4_typed.rs:26-31: the AWQ
  * packing), done once so that every later call streams the weights in the order the
  * kernels consume them.
- * Layout: strips of 16 columns, strip s one contiguous run of bytes: K/128 blocks of 1 KiB
- * (block kb: 64 lanes x 16 bytes, lane l = column 16 s + l % 16, rows 128 kb + 32 (l / 16)
- * + [0, 32) as four words of 8 rows; row i of a word in nibble slot (i >> 1) | ((i & 1) << 2)),
- * then the strip's scales (fp16 [K/G][16]) and full zero points (uint8 [K/G][16]: the GPTQ
- * nibble + gptq_zero_offset, 8 for GPTQ_SYM, the AWQ nibble), padded to 256 bytes. Any of the
- * three formats gives the same layout for the same weights W16 = RNE_f16((q - z) * s).
- * Shapes: N % 16 == 0, K % 128 == 0, group_size % 32 == 0, K % group_size == 0, K <= 32768.
+ * Layout: strips of 16 columns, strip s one contiguous run of bytes: first the strip's table,
+ * per block of 128 rows R = max(1, 128 / group_size) rows of 16 32-bit entries (entry c of a
+ * row: the group's fp16 scale for column 16 s + c in bits 0..15, its full zero point in bits
+ * 16..31: the GPTQ nibble + gptq_zero_offset, 8 for GPTQ_SYM, the AWQ nibble), padded to 256
+ * bytes; then K/128 blocks of 1 KiB (block kb: 64 lanes x 16 bytes, lane l = column
+ * 16 s + l % 16, rows 128 kb + 32 (l / 16) + [0, 32) as four words of 8 rows; row i of a word
+ * in nibble slot (i >> 1) | ((i & 1) << 2)). Any of the three formats gives the same layout
+ * for the same weights W16 = RNE_f16((q - z) * s).
+ * Shapes: N % 16 == 0, K % 128 == 0, group_size 32, 64 or a multiple of 128,
+ * K % group_size == 0, K <= 32768.
  *
  * w4a16_prepared_bytes: size of the prepared buffer (0 when the shape is not supported).
  * w4a16_prepare_layout: writes it (256-byte aligned `prepared`, not overlapping the inputs);
@@ -161,7 +164,10 @@ W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const v
  *   for an act-order checkpoint first repacked by w4a16_prepare_act_order, the permutation it
  *   returned; x's columns are then gathered by it first (as w4a16_gemm_act_order does, into a
  *   per-(device, stream) buffer the library keeps). M = 1 runs a GEMV with one workgroup per
- *   strip over all of K (no split-K, no scratch).
+ *   strip over all of K (no split-K, no scratch). With group_size a multiple of 128, 5..64 rows
+ *   (2..64 with perm) run a small-batch kernel, one workgroup per 1, 2 or 4 strips over all of
+ *   K (no split-K), after one pass that rewrites x (gathered by perm) into the kernel's
+ *   operand order in that same buffer.
  * w4a16_dequant_prepared: W16 as fp16 [K, N] (transposed = 0) or [N, K] (= 1), bit-exact. */
 W4A16_API size_t w4a16_prepared_bytes(int32_t K, int32_t N, int32_t group_size);
 W4A16_API int w4a16_prepare_layout(void* stream, int fmt, const void* qweight, const void* scales,

@@ -208,9 +208,10 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
 
 
 def test_prepared_kernels_isa(tmp_path):
-    """Prepared-layout kernels: the M = 1 and M = 2..8 GEMVs run their dot products on fp16
-    MFMA (one shift and four v_and_or_b32 per word feed them), the group-size-32/64 GEMV on
-    v_dot2 without MFMA; no split-K atomics anywhere in them."""
+    """Prepared-layout kernels: the M = 1 and M = 2..8 GEMVs and the small-batch kernel run
+    their dot products on fp16 MFMA (shifts and v_and_or_b32 per word feed them), the
+    group-size-32/64 GEMV on v_dot2 without MFMA; no split-K atomics anywhere in them, and no
+    scratch (spilled registers) in the small-batch kernels."""
     o = os.path.join(ROOT, "triton-rs_amd", "_build", "prepared.o")
     if not os.path.exists(o):
         pytest.skip("build objects not present (run build first)")
@@ -223,6 +224,11 @@ def test_prepared_kernels_isa(tmp_path):
         assert "atomic" not in b, n
     for n, b in va.items():
         assert "v_mfma" not in b and "v_dot2" in b and "atomic" not in b, n
+    fr = {n: b for n, b in k.items() if "gemm_prep_frag_kernel" in n}
+    assert len(fr) >= 20
+    for n, b in fr.items():
+        assert "v_mfma_f32_16x16x32_f16" in b and "v_and_or_b32" in b, n
+        assert "atomic" not in b and "scratch_" not in b and "buffer_store" not in b, n
 
 
 def test_bf16_flag_plans_generic_kernel_and_is_refused_elsewhere():

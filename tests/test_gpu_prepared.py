@@ -162,3 +162,68 @@ def test_gemm_prepared_prefill_exact_arithmetic(torch_cuda, orc):
         ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
                              zero_offset=p.zero_offset)
         assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), (NAME[fmt], M)
+
+
+# ------------------------------------------------- small batch (5..64 rows, G % 128 == 0)
+
+@pytest.mark.parametrize("fmt,M,K,N,G", [
+    (GPTQ, 16, 4096, 6144, 128), (GPTQ, 32, 4096, 6144, 128), (GPTQ, 64, 4096, 6144, 128),  # config 2's shape
+    (AWQ, 8, 4096, 14336, 128), (AWQ, 8, 14336, 4096, 128),      # config 1 at M = 8: 4 and 1 strips per workgroup
+    (AWQ, 17, 4096, 16 * 385, 128),     # 2 strips per workgroup, the last one holds one
+    (SYM, 33, 1024, 16 * 771, 128),     # 4 strips per workgroup (3 in the last), 3 row tiles
+    (GPTQ, 47, 128 * 33, 512, 128),     # 8 blocks per wave, the last wave 1 block
+    (AWQ, 63, 128 * 70, 256, 256),      # 16 blocks per wave, group of 2 blocks
+    (GPTQ, 5, 32768, 64, 128),          # 32 blocks per wave, 8 waves
+    (SYM, 12, 128, 16, 128),            # one block, one strip
+])
+def test_gemm_prepared_small_batch_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=0x5EED0005 + M + K + N)
+    w = _prep(P, p)
+    y = P.gemm_prepared(to_dev(p.x), w)
+    y2 = P.gemm_prepared(to_dev(p.x), w)
+    torch_cuda.cuda.synchronize()
+    y, y2 = y.cpu().numpy(), y2.cpu().numpy()
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), "repeated calls differ"
+    ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, G,
+                         zero_offset=p.zero_offset, want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"prepared small batch {NAME[fmt]} M={M} K={K} N={N} G={G}")
+
+
+@pytest.mark.parametrize("M", [2, 7, 16, 32, 64])
+def test_act_order_then_prepared_small_batch(torch_cuda, orc, M):
+    """Config 2 (GPTQ act-order, K=4096 -> N=6144) through the group-order repack and the
+    prepared layout: x is gathered straight into the small-batch kernel's operand order."""
+    P = pkg()
+    K, N = 4096, 6144
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED0002 + M, act_order=True)
+    qout, perm = P.prepare_act_order(to_dev(p.qweight), to_dev(p.g_idx), group_size=128)
+    w = P.prepare_layout(qout, to_dev(p.scales), to_dev(p.qzeros), fmt="gptq", group_size=128,
+                         zero_offset=1)
+    y = P.gemm_prepared(to_dev(p.x), w, perm=perm).cpu().numpy()
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx,
+                         want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"act-order prepared M={M}")
+
+
+def test_gemm_prepared_small_batch_exact_arithmetic(torch_cuda, orc):
+    """Exactly representable products and sums through the small-batch kernel (every row-tile
+    count, with and without act-order): the oracle's bits."""
+    P = pkg()
+    g = np.random.default_rng(81)
+    for fmt, M, K, N, G, act in ((AWQ, 16, 1024, 512, 128, False), (GPTQ, 29, 2048, 256, 256, False),
+                                 (SYM, 48, 512, 6160, 128, False), (GPTQ, 64, 2048, 192, 128, True),
+                                 (GPTQ, 3, 1024, 64, 128, True)):
+        p = Problem(fmt, M=M, K=K, N=N, G=G, seed=82 + M, act_order=act)
+        p.x = (g.integers(-8, 9, size=p.x.shape) / 4.0).astype(np.float16)
+        p.scales = (2.0 ** g.integers(-8, -4, size=p.scales.shape)).astype(np.float16)
+        if act:
+            qout, perm = P.prepare_act_order(to_dev(p.qweight), to_dev(p.g_idx), group_size=G)
+            w = P.prepare_layout(qout, to_dev(p.scales), to_dev(p.qzeros), fmt="gptq", group_size=G,
+                                 zero_offset=p.zero_offset)
+            y = P.gemm_prepared(to_dev(p.x), w, perm=perm).cpu().numpy()
+        else:
+            y = P.gemm_prepared(to_dev(p.x), _prep(P, p)).cpu().numpy()
+        ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
+                             g_idx=p.g_idx if act else None, zero_offset=p.zero_offset)
+        assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), (NAME[fmt], M, act)

@@ -520,6 +520,141 @@ gemv_prep_rows_kernel(PrepParams p) {
     }
 }
 
+// M <= 64 with the activations in MFMA fragment order (xfrag, written by launch_xfrag or by
+// the act-order gather): A operand st of 16-row tile tt of block kb is 1 KiB at
+// ((kb * MT + tt) * 4 + st) KiB, lane l's 16 bytes holding x at row 16 tt + l % 16 and rows
+// 128 kb + 32 (l / 16) + 8 st + [0, 8). A wave's A loads are then whole cache lines, and lanes
+// whose row is >= M load nothing (the tile's padding rows are never read or written).
+//
+// One workgroup owns S strips over the whole K range: wave w takes blocks w BPW .. w BPW +
+// BPW - 1 (so no split-K hand-off and no partial sums leave the CU); its table entries,
+// activations and weights run PD blocks ahead of its MFMAs. Per block and strip, B = word st
+// of the lane's 16 bytes as eight fp16 q - z: ((w >> 4 i) & 0x000F000F | 0x64006400) -
+// (1024 + z) is exact; one chain of four MFMAs per 16-row tile gives D = sum_k x_k (q_k - z)
+// over the block, and y += s D. The waves' sums meet in LDS and are added in wave order.
+// Requires G % 128 == 0 and fewer than 2^31 bytes of prepared weights.
+template <int MT, int S, int BPW, int PD>
+__global__ void __launch_bounds__(512)
+gemm_prep_frag_kernel(PrepFragParams p) {
+    static_assert(PD >= 1 && PD <= BPW, "prefetch depth");
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int W = blockDim.x >> 6;
+    const int col = lane & 15, h = lane >> 4;
+    const int NS = p.N >> 4, KB = p.K >> 7, M = p.M;
+    const int s0 = blockIdx.x * S;
+    const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
+    const uint32_t pbytes = (uint32_t)NS * p.strip_bytes;
+    const uint32_t xbytes = (uint32_t)KB * MT * 4096u;
+    const bufrsrc_t pr = make_rsrc(p.prep, pbytes);
+    const bufrsrc_t xr = make_rsrc(p.xfrag, xbytes);
+
+    uint32_t ev[BPW][S];
+    u32x4 av[BPW][MT][4], wv[BPW][S];
+    auto load = [&](const int j) __attribute__((always_inline)) {
+        const int kb = wave * BPW + j;
+        const bool kin = kb < KB;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int strip = s0 + s;
+            const uint32_t off = kin && strip < NS ? (uint32_t)strip * p.strip_bytes + (uint32_t)(kb * 16 + col) * 4u
+                                                   : pbytes;
+            ev[j][s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 2);
+        }
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t off = kin && 16 * tt + col < M ? (uint32_t)(((kb * MT + tt) * 4 + st) * 1024 + lane * 16)
+                                                              : xbytes;
+                av[j][tt][st] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+            }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int strip = s0 + s;
+            const uint32_t off = kin && strip < NS
+                                     ? (uint32_t)strip * p.strip_bytes + tbytes + (uint32_t)kb * 1024u + (uint32_t)lane * 16u
+                                     : pbytes;
+            wv[j][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 2));
+        }
+    };
+#pragma unroll
+    for (int j = 0; j < PD; ++j) load(j);
+
+    float acc[S][MT][4];
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[s][tt][i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+        if (j + PD < BPW) load(j + PD);
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const uint32_t e = ev[j][s];
+            // -(1024 + z) as an fp16 pair (z <= 31: exact, bit pattern)
+            const half2_t ze = as_h2(((0x6400u + (e >> 16)) * 0x10001u) | 0x80008000u);
+            half8_t B[4];
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t q = wv[j][s][st];
+                B[st] = __builtin_bit_cast(half8_t, u32x4{as_u32(nib_pair(q) + ze), as_u32(nib_pair(q >> 4) + ze),
+                                                          as_u32(nib_pair(q >> 8) + ze), as_u32(nib_pair(q >> 12) + ze)});
+            }
+            const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt) {
+                float4_t d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+                    d = mfma16x16x32(__builtin_bit_cast(half8_t, av[j][tt][st]), B[st], d);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[s][tt][i] = __builtin_fmaf(sc, d[i], acc[s][tt][i]);
+            }
+        }
+    }
+
+    // ---- the waves' sums, added in wave order; lane l of tile tt holds rows 16 tt + 4 (l / 16)
+    // + i of column l % 16
+    float4_t* red = reinterpret_cast<float4_t*>(lds);
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+            red[((wave * S + s) * MT + tt) * 64 + lane] = float4_t{acc[s][tt][0], acc[s][tt][1], acc[s][tt][2], acc[s][tt][3]};
+    __syncthreads();
+    const float* rf = reinterpret_cast<const float*>(lds);
+    for (int o = t; o < S * MT * 256; o += blockDim.x) {
+        const int i = o & 3, l = (o >> 2) & 63, rest = o >> 8, tt = rest % MT, s = rest / MT;
+        const int m = 16 * tt + 4 * (l >> 4) + i, strip = s0 + s;
+        if (m >= M || strip >= NS) continue;
+        float a = 0.f;
+        for (int w = 0; w < W; ++w) a += rf[w * S * MT * 256 + o];
+        p.out[(size_t)m * p.N + strip * 16 + (l & 15)] = (half_t)a;
+    }
+}
+
+// x [M, K] -> fragment order (see gemm_prep_frag_kernel): grid (K / 128, MT), 256 threads;
+// thread t writes lane t % 64 of step t / 64. Rows past M are left unwritten.
+__global__ void __launch_bounds__(256)
+xfrag_kernel(const half_t* __restrict__ x, half_t* __restrict__ xf, int M, int K) {
+    const int kb = blockIdx.x, tt = blockIdx.y, MT = gridDim.y;
+    const int t = threadIdx.x, lane = t & 63, st = t >> 6;
+    const int m = 16 * tt + (lane & 15);
+    if (m >= M) return;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + kb * 128 + 32 * (lane >> 4) + 8 * st);
+    *reinterpret_cast<u32x4*>(xf + ((size_t)((kb * MT + tt) * 4 + st) * 64 + lane) * 8) = v;
+}
+
+hipError_t launch_xfrag(const half_t* x, half_t* xf, int M, int K, hipStream_t st) {
+    (void)hipGetLastError();
+    hipLaunchKernelGGL(xfrag_kernel, dim3(K / 128, (M + 15) / 16), dim3(256), 0, st, x, xf, M, K);
+    return hipGetLastError();
+}
+
 PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
     PrepGemvShape s{};
     if (M < 1 || M > PREP_GEMV_MAX_M || N % 16 || K % 128 || !prep_group_ok(G) || K % G || K > PREP_MAX_K)
@@ -549,6 +684,68 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
     s.lds = (size_t)waves * wave_lds + (size_t)waves * 16 * 4;
     s.ok = waves <= 16 && s.lds <= 160 * 1024;
     return s;
+}
+
+// Shape of the fragment-order kernel: blocks per wave so that at most 8 waves cover K; S
+// strips per workgroup, the most (up to 4; up to 2 from 33 rows or 32 blocks per wave, where
+// the registers leave less room) that still gives 192 workgroups (K=4096 -> N=6144: S = 2, 192 workgroups,
+// 6.1 us at M = 16 against 7.5 with S = 1; N=14336: S = 4); loads in flight: the whole queue
+// at 16 rows when it is 4 blocks, else 2 blocks, then 1 (measured over PD = 1, 2, 4, BPW).
+PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
+    PrepFragShape s{};
+    if (M < 1 || M > PREP_FRAG_MAX_M || N % 16 || K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
+        return s;
+    if (prep_total_bytes(K, N, G) >= ((size_t)1 << 31)) return s;
+    const int NS = N / 16, KB = K / 128;
+    s.mt = (M + 15) / 16;
+    s.bpw = KB <= 32 ? 4 : KB <= 64 ? 8 : KB <= 128 ? 16 : 32;
+    s.waves = (KB + s.bpw - 1) / s.bpw;
+    s.s = 1;
+    for (int c = s.mt <= 2 && s.bpw <= 16 ? 4 : 2; c > 1; c /= 2)
+        if (NS / c >= 192) { s.s = c; break; }
+    s.pd = s.mt == 1 ? (s.bpw == 4 ? 4 : 2) : s.mt == 2 ? 2 : 1;
+    s.lds = (size_t)s.waves * s.s * s.mt * 1024;
+    s.ok = true;
+    return s;
+}
+
+template <int MT, int S>
+static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    constexpr int PD1 = MT == 1 ? 2 : MT == 2 ? 2 : 1;   // pd for 8 or more blocks per wave
+    const dim3 grid((p.N / 16 + S - 1) / S), block(64 * s.waves);
+    switch (s.bpw) {
+        case 4: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 4, MT == 1 ? 4 : PD1>), grid, block, s.lds, st, p); break;
+        case 8: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 8, PD1>), grid, block, s.lds, st, p); break;
+        case 16: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 16, PD1>), grid, block, s.lds, st, p); break;
+        case 32:   // 4 strips over 32 blocks would spill
+            if constexpr (S <= 2) { hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 32, PD1>), grid, block, s.lds, st, p); break; }
+            return hipErrorInvalidValue;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int MT>
+static hipError_t launch_prep_frag_m(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    switch (s.s) {
+        case 1: return launch_prep_frag_ms<MT, 1>(p, s, st);
+        case 2: return launch_prep_frag_ms<MT, 2>(p, s, st);
+        case 4: if constexpr (MT <= 2) return launch_prep_frag_ms<MT, 4>(p, s, st);
+                [[fallthrough]];
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    (void)hipGetLastError();
+    if (!s.ok || s.pd != (s.mt == 1 ? (s.bpw == 4 ? 4 : 2) : s.mt == 2 ? 2 : 1)) return hipErrorInvalidValue;
+    switch (s.mt) {
+        case 1: return launch_prep_frag_m<1>(p, s, st);
+        case 2: return launch_prep_frag_m<2>(p, s, st);
+        case 3: return launch_prep_frag_m<3>(p, s, st);
+        case 4: return launch_prep_frag_m<4>(p, s, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int BPW>
