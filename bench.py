@@ -529,23 +529,43 @@ def extras(torch, pkg, dev, stream, args):
     gemm_case("tp8_c3_awq_m2048_k4096_n1792", "awq", 2048, 4096, 1792, 128, 2, 300)
     gemm_case("tp8_c3_awq_m2048_k1792_n4096", "awq", 2048, 1792, 4096, 128, 2, 300)
 
-    # the reference-named typed entry point (its 19-parameter list, dense strides) at C1 / C3
-    def typed_case(tag, M, K, N, n_sets, calls):
+    # the reference-named typed entry point (its 19-parameter list, dense strides) at C1 / C3,
+    # called through the C ABI and launched by name through the DeviceRuntime backend
+    # (hiprt_launch of awq_gemm_int4_typed from w4a16_typed.hsaco, grid (cdiv(M,64),
+    # cdiv(N,64), 1) x 256 threads, the 19 arguments + 2 scratch pointers)
+    rt = pkg.HipRuntime(0)
+    hs_mod = rt.load_module(pkg.typed_module_bytes())
+    scratch = torch.empty(1, dtype=torch.uint8, device=dev)
+
+    def typed_case(tag, M, K, N, n_sets, calls, hiprt=False):
         G = 128
         sets = make_weight_sets(torch, "awq", K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
         x = torch.randn((M, K), device=dev, generator=gen).half()
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         st = [K, 1, N // 8, 1, N, 1, N // 8, 1, N, 1]
+        A = pkg.KernelArg
+        args = [[A.ptr(x), A.ptr(qw), A.ptr(sc), A.ptr(qz), A.ptr(out)] +
+                [A.i32(v) for v in (M, N, K, G, *st)] + [A.ptr(scratch), A.ptr(scratch)]
+                for qw, sc, qz in sets]
+        grid = (-(-M // 64), -(-N // 64), 1)
 
         def fn(i):
-            qw, sc, qz = sets[i % n_sets]
-            pkg.awq_gemm_int4_typed(x, qw, sc, qz, out, M, N, K, G, *st)
+            if hiprt:
+                rt.launch(hs_mod, "awq_gemm_int4_typed", grid, (256, 1, 1), 0, None, args[i % n_sets])
+            else:
+                qw, sc, qz = sets[i % n_sets]
+                pkg.awq_gemm_int4_typed(x, qw, sc, qz, out, M, N, K, G, *st)
         ms = time_calls(torch, fn, GRAPH_CALLS, 10, stream, n_sets, batch_calls=calls)[1]
-        record(tag, "awq", M, K, N, G, ms, "typed->" + pkg.typed_plan("awq", M, N, K, G, st))
-        del sets
+        record(tag, "awq", M, K, N, G, ms,
+               ("hiprt->" if hiprt else "typed->") + pkg.typed_plan("awq", M, N, K, G, st))
+        del sets, args
 
     typed_case("typed_awq_gemm_int4_m1_k4096_n14336", 1, 4096, 14336, 20, 1000)
     typed_case("typed_awq_gemm_int4_m2048_k4096_n14336", 2048, 4096, 14336, 2, 300)
+    typed_case("hiprt_awq_gemm_int4_typed_m1_k4096_n14336", 1, 4096, 14336, 20, 1000, hiprt=True)
+    typed_case("hiprt_awq_gemm_int4_typed_m2048_k4096_n14336", 2048, 4096, 14336, 2, 300, hiprt=True)
+    rt.unload_module(hs_mod)
+    rt.close()
 
     # config 4: fused MoE layer, T=512, 8 experts, top-2, K=4096, I=14336, GPTQ G=128
     L = moe_layer(torch, dev, gen)

@@ -490,6 +490,52 @@ def test_hip_runtime_module_launch(torch_cuda, orc):
     rt.close()
 
 
+def _hiprt_typed_args(P, p, a, qw, sc, qz, c, scratch):
+    A = P.KernelArg
+    M, K, N = p.M, p.K, p.N
+    return [A.ptr(a), A.ptr(qw), A.ptr(sc), A.ptr(qz), A.ptr(c), A.i32(M), A.i32(N), A.i32(K),
+            A.i32(p.G), A.i32(K), A.i32(1), A.i32(N // 8 if p.fmt == AWQ else N), A.i32(1), A.i32(N),
+            A.i32(1), A.i32(N // 8), A.i32(1), A.i32(N), A.i32(1), A.ptr(scratch), A.ptr(scratch)]
+
+
+@pytest.mark.parametrize("fmt,M,K,N", [(AWQ, 1, 4096, 14336), (AWQ, 8, 14336, 4096), (GPTQ, 16, 4096, 6144),
+                                       (AWQ, 2048, 4096, 14336)])
+def test_hip_runtime_launch_planned(torch_cuda, orc, fmt, M, K, N):
+    """DeviceRuntime::launch by name at the configs' shapes: a launch of the library's code
+    object that follows its contract runs the planned kernels (same results as the C-ABI typed
+    entry, bit for bit); a grid off the contract runs the module's own kernel (same function)."""
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=1510 + M)
+    rt = P.HipRuntime(0)
+    mod = rt.load_module(P.typed_module_bytes())
+    name = "awq_gemm_int4_typed" if fmt == AWQ else "w4a16_gptq_gemm_typed"
+    a, qw, sc, qz = (to_dev(v) for v in (p.x, p.qweight, p.scales, p.qzeros))
+    c = torch.empty((M, N), dtype=torch.float16, device="cuda:0")
+    scratch = torch.empty(1, dtype=torch.uint8, device="cuda:0")
+    args = _hiprt_typed_args(P, p, a, qw, sc, qz, c, scratch)
+    grid = (-(-M // 64), -(-N // 64), 1)
+    rt.launch(mod, name, grid, (256, 1, 1), 0, None, args)
+    torch.cuda.synchronize()
+    y = c.cpu().numpy()
+    fn = P.w4a16_gptq_gemm_typed if fmt == GPTQ else P.awq_gemm_int4_typed
+    c2 = torch.empty_like(c)
+    fn(a, qw, sc, qz, c2, M, N, K, p.G, K, 1, N // 8 if fmt == AWQ else N, 1, N, 1, N // 8, 1, N, 1)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.view(np.uint16), c2.cpu().numpy().view(np.uint16)), "hiprt route vs typed entry"
+    rows = np.arange(M) if M <= 64 else np.unique(np.r_[0, M - 1, np.random.default_rng(M).choice(M, 30)])
+    ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, p.G, rows.astype(np.int32),
+                              zero_offset=p.zero_offset)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"hiprt planned {name} M={M}")
+    if M <= 16:   # an extra grid row: off the contract, the module's kernel runs
+        c.zero_()
+        rt.launch(mod, name, (grid[0] + 1, grid[1], 1), (256, 1, 1), 0, None, args)
+        torch.cuda.synchronize()
+        assert_parity(c.cpu().numpy()[rows], ref.astype(np.float64), what=f"hiprt module kernel {name} M={M}")
+    rt.unload_module(mod)
+    rt.close()
+
+
 # ------------------------------------------------------------------ dequant (bit-exact)
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])

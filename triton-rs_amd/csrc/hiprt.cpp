@@ -27,6 +27,7 @@ struct hiprt_ctx {
 struct hiprt_module {
     hiprt_ctx* ctx;
     hipModule_t module;
+    bool planned;   // the library's typed code object (w4a16_typed_module_marker present)
     mutable std::mutex mu;
     mutable std::unordered_map<std::string, hipFunction_t> fns;
 };
@@ -80,6 +81,11 @@ W4A16_API int hiprt_module_load(hiprt_ctx* ctx, const void* binary, size_t size,
     hiprt_module* mod = new hiprt_module();
     mod->ctx = ctx;
     mod->module = m;
+    hipDeviceptr_t marker = nullptr;
+    size_t marker_size = 0;
+    mod->planned = hipModuleGetGlobal(&marker, &marker_size, m, "w4a16_typed_module_marker") == hipSuccess &&
+                   marker_size == sizeof(uint32_t);
+    (void)hipGetLastError();
     *out = mod;
     return W4A16_OK;
 }
@@ -92,6 +98,37 @@ W4A16_API int hiprt_module_unload(hiprt_module* module) {
 }
 
 static size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// A launch of w4a16_gptq_gemm_typed or awq_gemm_int4_typed from the library's own code object
+// that follows its launch contract (the reference's 19 arguments, optionally the two scratch
+// pointers, grid (cdiv(m, 64), cdiv(n, 64), 1), 256 threads, no dynamic LDS) computes the
+// same function as the C-ABI entry of the same name, which plans the kernel for the shape
+// (GEMV, small-batch, prefill; the generic kernel for other strides): that entry runs it, so
+// that DeviceRuntime::launch by name gets the planned kernels. Returns -1 when the launch does
+// not match (it then goes to the module's kernel as given).
+static int launch_planned(const char* name, const uint32_t grid[3], const uint32_t block[3],
+                          uint32_t shared_mem_bytes, void* stream, const hiprt_arg* args, size_t nargs) {
+    const bool gptq = std::strcmp(name, "w4a16_gptq_gemm_typed") == 0;
+    if (!gptq && std::strcmp(name, "awq_gemm_int4_typed") != 0) return -1;
+    if (nargs != 19 && nargs != 21) return -1;
+    for (size_t i = 0; i < nargs; ++i) {
+        const bool ptr = i < 5 || i >= 19;
+        if (ptr ? args[i].kind != HIPRT_ARG_DEVICE_PTR
+                : args[i].kind != HIPRT_ARG_I32 && args[i].kind != HIPRT_ARG_U32)
+            return -1;
+    }
+    int32_t v[14];
+    for (int i = 0; i < 14; ++i) v[i] = args[5 + i].kind == HIPRT_ARG_I32 ? args[5 + i].v.i32 : (int32_t)args[5 + i].v.u32;
+    const int64_t m = v[0], n = v[1];
+    if (m < 1 || n < 1 || grid[0] != (uint64_t)(m + 63) / 64 || grid[1] != (uint64_t)(n + 63) / 64 || grid[2] != 1 ||
+        block[0] != 256 || block[1] != 1 || block[2] != 1 || shared_mem_bytes != 0)
+        return -1;
+    const void* p[5];
+    for (int i = 0; i < 5; ++i) p[i] = reinterpret_cast<const void*>(args[i].v.device_ptr);
+    return (gptq ? w4a16_gptq_gemm_typed : awq_gemm_int4_typed)(
+        stream, p[0], p[1], p[2], p[3], const_cast<void*>(p[4]), v[0], v[1], v[2], v[3], v[4], v[5],
+        v[6], v[7], v[8], v[9], v[10], v[11], v[12], v[13]);
+}
 
 W4A16_API int hiprt_launch(hiprt_ctx* ctx, const hiprt_module* module, const char* kernel_name,
                            const uint32_t grid[3], const uint32_t block[3],
@@ -107,6 +144,12 @@ W4A16_API int hiprt_launch(hiprt_ctx* ctx, const hiprt_module* module, const cha
     if (shared_mem_bytes > 160 * 1024)
         return fail(W4A16_ERR_LAUNCH_CONFIG, "invalid launch config: %u bytes of LDS exceeds 160 KiB",
                     shared_mem_bytes);
+
+    if (module->planned) {
+        if (int rc = set_device(ctx)) return rc;
+        const int rc = launch_planned(kernel_name, grid, block, shared_mem_bytes, stream, args, nargs);
+        if (rc != -1) return rc;
+    }
 
     // pack KernelArg values at natural alignment
     std::vector<unsigned char> buf;
