@@ -455,6 +455,9 @@ def extras(torch, pkg, dev, stream, args):
         gemm_case(f"c2_gptq_actorder_m{M}_k4096_n6144", "gptq", M, 4096, 6144, 128, 40, 500,
                   g_idx=g_idx)
         gemm_case(f"c2_gptq_m{M}_k4096_n6144_no_gidx", "gptq", M, 4096, 6144, 128, 40, 500)
+    # the same act-order weights at prefill size through w4a16_gemm (group order computed on the
+    # device per call, rows repacked, x gathered, then the prefill kernel)
+    gemm_case("c2_gptq_actorder_m2048_k4096_n6144", "gptq", 2048, 4096, 6144, 128, 2, 200, g_idx=g_idx)
 
     # config 2's act-order layer through the one-time group-order repack: gather + plain kernel
     def prepared_case(tag, M, n_sets, calls):
@@ -477,6 +480,33 @@ def extras(torch, pkg, dev, stream, args):
     for M in (16, 64):
         prepared_case(f"c2_gptq_actorder_prepared_m{M}_k4096_n6144", M, 40, 500)
     prepared_case("c2_gptq_actorder_prepared_m2048_k4096_n6144", 2048, 2, 200)
+
+    # config 2's act-order layer in the prepared layout (group-order repack, then
+    # w4a16_prepare_layout, once): per call, x gathered by perm straight into the small-batch
+    # kernel's operand order, then the small-batch kernel (prefill kernel at M = 2048)
+    def preplayout_case(tag, M, n_sets, calls):
+        K, N, G = 4096, 6144, 128
+        sets = make_weight_sets(torch, "gptq", K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
+        preps = []
+        for qw, sc, qz in sets:
+            qp, pm = pkg.prepare_act_order(qw, g_idx, group_size=G)
+            preps.append((pkg.prepare_layout(qp, sc, qz, fmt="gptq", group_size=G, zero_offset=1), pm))
+        del sets
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+        def fn(i):
+            w, pm = preps[i % n_sets]
+            pkg.gemm_prepared(x, w, perm=pm, out=out)
+        ms = time_calls(torch, fn, GRAPH_CALLS, 10, stream, n_sets, batch_calls=calls,
+                        n_graphs=min(10, max(1, 1000 // GRAPH_CALLS)))[1]
+        record(tag, "gptq", M, K, N, G, ms, "gather+prepared/" + ("prefill" if M > 64 else "small-batch"),
+               act_order=True)
+        del preps
+
+    for M in (16, 32, 64):
+        preplayout_case(f"c2_gptq_actorder_preplayout_m{M}_k4096_n6144", M, 40, 500)
+    preplayout_case("c2_gptq_actorder_preplayout_m2048_k4096_n6144", 2048, 2, 200)
 
     gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
     gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)

@@ -413,18 +413,59 @@ def test_act_order_identity_gidx_equals_plain(torch_cuda, M, K, N, G):
     assert np.array_equal(plain.view(np.uint16), ident.view(np.uint16))
 
 
-def test_act_order_large_m_uses_strided(torch_cuda, orc):
-    p = Problem(GPTQ, M=100, K=512, N=256, G=128, seed=1330, act_order=True)
-    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) == "strided"
+@pytest.mark.parametrize("fmt,M,K,N,G", [(GPTQ, 100, 512, 256, 128), (SYM, 65, 1024, 384, 64),
+                                         (GPTQ, 300, 2048, 1024, 256), (GPTQ, 130, 4096, 224, 128)])
+def test_act_order_large_m_prefill(torch_cuda, orc, fmt, M, K, N, G):
+    """Act-order beyond 64 rows through w4a16_gemm: the group order is computed on the device,
+    then the prefill kernel runs on the repacked rows and the gathered x."""
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1330 + M, act_order=True)
+    assert pkg().plan(FMT_NAME[fmt], p.M, p.N, p.K, p.G, has_g_idx=True) == "prefill"
     y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
-    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what="act-order strided")
+    y2 = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), "repeated calls differ"
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"act-order prefill M={M}")
 
 
-def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc):
+def test_act_order_config2_prefill_size(torch_cuda, orc):
+    """Config 2's act-order weights at M = 2048 (K=4096 -> N=6144): 32 sampled rows."""
+    M, K, N = 2048, 4096, 6144
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED0002, act_order=True)
+    assert pkg().plan("gptq", M, N, K, 128, has_g_idx=True) == "prefill"
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(5).choice(M, 30)]).astype(np.int32)
+    ref = orc.w4a16_gemm_rows(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows,
+                              g_idx=p.g_idx)
+    assert_parity(y[rows], ref.astype(np.float64), what="act-order config 2 M=2048")
+
+
+def test_act_order_large_m_identity_equals_plain(torch_cuda):
+    """g_idx[k] = k / G beyond 64 rows: the group order is the identity, the prefill kernel
+    runs on a copy of the same rows and x, so the output is bit for bit the plain call's."""
+    p = Problem(GPTQ, M=200, K=1024, N=512, G=128, seed=1335)
+    assert pkg().plan("gptq", p.M, p.N, p.K, p.G) == "prefill"
+    plain = _run_gemm(torch_cuda, p)
+    ident = _run_gemm(torch_cuda, p, g_idx=(np.arange(p.K) // p.G).astype(np.int32))
+    assert np.array_equal(plain.view(np.uint16), ident.view(np.uint16))
+
+
+def test_act_order_large_m_unequal_groups_runs_generic(torch_cuda, orc):
+    """A g_idx whose groups do not each hold G rows cannot be put in group order for the
+    prefill kernel: the device-side check leaves the generic kernel to run, which reads g_idx
+    per row (same results as the oracle)."""
+    p = Problem(GPTQ, M=96, K=1024, N=256, G=128, seed=1336)
+    g_idx = np.random.default_rng(1336).integers(0, p.K // p.G, p.K).astype(np.int32)
+    g_idx[:5] = 0
+    y = _run_gemm(torch_cuda, p, g_idx=g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=g_idx), what="act-order unequal groups")
+
+
+@pytest.mark.parametrize("M", [16, 80])
+def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc, M):
     """The device cannot report a bad g_idx without a host round trip; entries outside
     [0, K/G) are clamped into the scale table (the oracle, which rejects them, is given the
-    clamped index)."""
-    p = Problem(GPTQ, M=16, K=1024, N=256, G=128, seed=1340, act_order=True)
+    clamped index). Beyond 64 rows the group-order check sees them and the generic kernel
+    runs."""
+    p = Problem(GPTQ, M=M, K=1024, N=256, G=128, seed=1340, act_order=True)
     bad = p.g_idx.copy()
     bad[3], bad[700] = 99, -5
     y = _run_gemm(torch_cuda, p, g_idx=bad)

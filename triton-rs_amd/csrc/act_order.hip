@@ -93,6 +93,76 @@ gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restric
     }
 }
 
+// Group order on the device, per call: perm[j] = the row of W at position j when the rows are
+// sorted by g_idx, stable in k (the order w4a16_prepare_act_order computes on the host), and
+// gate[0] = 1 when every group holds exactly G rows (group g then occupies rows [g G, g G + G)
+// of that order, as the prefill kernel assumes), else 0 with perm the identity (so that the
+// kernels reading it stay in bounds). One workgroup of 16 waves; wave w takes rows
+// [w P, w P + P), P = ceil(K / 16): it counts them per group, the counts become each wave's
+// starting position per group (wave order), then the wave places its rows 64 at a time, each
+// lane after the earlier lanes of its 64 with the same group. K <= 32768, K / G <= 1024.
+constexpr int ORDER_MAX_GROUPS = 1024;
+
+__global__ void __launch_bounds__(1024)
+act_order_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ perm,
+                      uint32_t* __restrict__ gate, int K, int G) {
+    __shared__ int pos[16][ORDER_MAX_GROUPS];   // counts, then next position, per (wave, group)
+    __shared__ int bad;
+    const int groups = K / G;
+    const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    for (int i = t; i < 16 * ORDER_MAX_GROUPS; i += 1024) (&pos[0][0])[i] = 0;
+    if (t == 0) bad = 0;
+    __syncthreads();
+    const int per = (K + 15) / 16;
+    const int k0 = min(K, w * per), k1 = min(K, k0 + per);
+    for (int k = k0 + lane; k < k1; k += 64) {
+        const int g = g_idx[k];
+        if ((unsigned)g >= (unsigned)groups) bad = 1;
+        else atomicAdd(&pos[w][g], 1);
+    }
+    __syncthreads();
+    for (int g = t; g < groups; g += 1024) {
+        int run = g * G, total = 0;
+        for (int v = 0; v < 16; ++v) {
+            const int c = pos[v][g];
+            pos[v][g] = run;
+            run += c;
+            total += c;
+        }
+        if (total != G) bad = 1;
+    }
+    __syncthreads();
+    if (bad) {   // uniform
+        for (int k = t; k < K; k += 1024) perm[k] = k;
+    } else {
+        for (int kc = k0; kc < k1; kc += 64) {
+            const int k = kc + lane;
+            const int g = k < k1 ? g_idx[k] : -1;
+            int rank = 0;
+#pragma unroll
+            for (int i = 0; i < 64; ++i) rank += (i < lane && __builtin_amdgcn_readlane(g, i) == g) ? 1 : 0;
+            const int base = g >= 0 ? pos[w][g] : 0;
+            // every lane has read its base (one LDS read of the wave) before any lane adds
+            __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
+            if (g >= 0) {
+                perm[base + rank] = k;
+                atomicAdd(&pos[w][g], 1);
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+        }
+    }
+    __syncthreads();
+    if (t == 0) gate[0] = bad ? 0u : 1u;
+}
+
+hipError_t launch_act_order_perm(const int32_t* g_idx, int32_t* perm, uint32_t* gate, int K, int G,
+                                 hipStream_t st) {
+    (void)hipGetLastError();
+    if (K < 1 || K > 32768 || G < 1 || K % G || K / G > ORDER_MAX_GROUPS) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(act_order_perm_kernel, dim3(1), dim3(1024), 0, st, g_idx, perm, gate, K, G);
+    return hipGetLastError();
+}
+
 hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
                                    int N, hipStream_t st) {
     (void)hipGetLastError();

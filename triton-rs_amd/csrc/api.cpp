@@ -101,6 +101,8 @@ static int get_workspace(hipStream_t st, size_t need, uint32_t** counters, float
 
 // Per-(device, stream) buffer for activations gathered into act-order group order.
 static std::map<std::pair<int, hipStream_t>, Workspace> g_gather;
+// act-order beyond 64 rows on w4a16_gemm: perm, the gate word and the repacked rows
+static std::map<std::pair<int, hipStream_t>, Workspace> g_actorder;
 
 // ------------------------------------------------------------------ validation
 
@@ -182,11 +184,18 @@ static bool xcd_placement_cached() {
     return xcd_placement(nullptr, /*probe=*/false);
 }
 
+// Act-order beyond the small-batch kernel: the per-call group order (act_order.hip) feeds the
+// prefill kernel; it needs K <= 32768 and at most 1024 groups.
+static bool act_order_prefill_ok(int fmt, int M, int N, int K, int G, int cus) {
+    return (fmt == W4A16_FMT_GPTQ || fmt == W4A16_FMT_GPTQ_SYM) && K <= 32768 && K % G == 0 &&
+           K / G <= 1024 && prefill_shape(fmt, M, N, K, G, cus).ok;
+}
+
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) {
         const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus, true);
-        return sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES ? W4A16_KERNEL_SKINNY
-                                                                : W4A16_KERNEL_STRIDED;
+        if (sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
+        return act_order_prefill_ok(fmt, M, N, K, G, cus) ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     }
     const GemvShape gv = gemv_shape(fmt, M, N, K, G, false);
     if (gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
@@ -257,7 +266,7 @@ static int alloc_scratch(hipStream_t st, size_t partial_bytes, Scratch* out) {
     return W4A16_OK;
 }
 
-ScratchSource alloc_scratch_source() { return ScratchSource{SIZE_MAX, SPLITK_MAX_TILES, true, alloc_scratch}; }
+ScratchSource alloc_scratch_source() { return ScratchSource{SIZE_MAX, SPLITK_MAX_TILES, true, true, alloc_scratch}; }
 
 int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const void* scales,
               const void* qzeros, const int32_t* g_idx, void* out, int32_t M, int32_t N,
@@ -274,6 +283,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     const int cus = device_cus();
     int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok || bf16) kernel = W4A16_KERNEL_STRIDED;   // bf16: the generic kernel only
+    if (g_idx && kernel == W4A16_KERNEL_PREFILL && !src.may_allocate) kernel = W4A16_KERNEL_STRIDED;
     // the placement probe allocates: sources that must not allocate use what is cached
     const bool xcd = src.may_probe ? xcd_placement(st) : xcd_placement_cached();
     auto scratch_for = [&](size_t tiles, size_t partial_bytes, Scratch* sc) -> int {
@@ -327,30 +337,58 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
         return W4A16_OK;
     }
 
-    if (kernel == W4A16_KERNEL_PREFILL) {
+    // the prefill kernel on (xp, qwp) with the call's scales and zeros; gate as PrefillParams
+    auto run_prefill = [&](const void* xp, const void* qwp, const uint32_t* gate) -> int {
         PrefillShape s = prefill_shape(fmt, M, N, K, G, cus);
         if (s.ksplit > 1 && ((size_t)s.ksplit * M * N * sizeof(float) > src.max_partial_bytes ||
                              (size_t)s.col_tiles * s.row_tiles > src.max_tiles))
             s = prefill_shape(fmt, M, N, K, G, cus, 1);   // no K split: no scratch at all
         PrefillParams p{};
-        p.x = static_cast<const half_t*>(x);
-        p.qweight = static_cast<const uint32_t*>(qweight);
+        p.x = static_cast<const half_t*>(xp);
+        p.qweight = static_cast<const uint32_t*>(qwp);
         p.scales = static_cast<const half_t*>(scales);
         p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G; p.zero_offset = zero_offset;
         p.ksplit = s.ksplit;
+        p.gate = gate;
+        p.gate_want = 1;
         if (s.ksplit > 1) {
             Scratch sc{};
-            rc = scratch_for((size_t)s.col_tiles * s.row_tiles,
-                             (size_t)s.ksplit * M * N * sizeof(float), &sc);
-            if (rc) return rc;
+            const int r = scratch_for((size_t)s.col_tiles * s.row_tiles,
+                                      (size_t)s.ksplit * M * N * sizeof(float), &sc);
+            if (r) return r;
             p.counters = sc.counters;
             p.ws = sc.partials;
         }
         hipError_t e = launch_prefill(fmt, p, s, st);
-        if (e != hipSuccess) return hip_fail(e, "prefill launch");
-        return W4A16_OK;
+        return e == hipSuccess ? W4A16_OK : hip_fail(e, "prefill launch");
+    };
+    if (kernel == W4A16_KERNEL_PREFILL && !g_idx) return run_prefill(x, qweight, nullptr);
+
+    // act-order beyond the small-batch kernel's rows: per call, the group order of the rows is
+    // computed on the device (perm, and a gate word that is 1 when every group holds exactly G
+    // rows), the packed rows are repacked into it and x's columns gathered by it, then the
+    // prefill kernel runs on them when the gate is 1 and the generic kernel on the checkpoint
+    // when it is 0 (each reads the gate and returns at once when it is not the one wanted).
+    // Without the per-stream buffers (allocation-free entry) the generic kernel alone runs.
+    const uint32_t* gate = nullptr;
+    if (kernel == W4A16_KERNEL_PREFILL) {
+        const size_t perm_bytes = ((size_t)K * 4 + 255) & ~(size_t)255;
+        void* ws = nullptr;
+        void* xg = nullptr;
+        rc = stream_buffer(g_actorder, st, perm_bytes + 256 + (size_t)K / 8 * N * 4, 0, "act-order repack buffer", &ws);
+        if (!rc) rc = stream_buffer(g_gather, st, (size_t)M * K * sizeof(half_t), 0, "act-order gather buffer", &xg);
+        if (rc) return rc;
+        int32_t* perm = static_cast<int32_t*>(ws);
+        uint32_t* gw = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + perm_bytes);
+        uint32_t* qout = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + perm_bytes + 256);
+        hipError_t e = launch_act_order_perm(g_idx, perm, gw, K, G, st);
+        if (e == hipSuccess) e = launch_gptq_repack_rows(static_cast<const uint32_t*>(qweight), perm, qout, K, N, st);
+        if (e == hipSuccess) e = launch_gather_columns(static_cast<const half_t*>(x), perm, static_cast<half_t*>(xg), M, K, st);
+        if (e != hipSuccess) return hip_fail(e, "act-order group order launch");
+        if ((rc = run_prefill(xg, qout, gw))) return rc;
+        gate = gw;
     }
 
     if (kernel == W4A16_KERNEL_GEMV) {
@@ -396,6 +434,8 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     p.stride_sk = N; p.stride_sn = 1;
     p.stride_qzk = N / 8; p.stride_qzn = 1;
     p.stride_cm = N; p.stride_cn = 1;
+    p.gate = gate;
+    p.gate_want = 0;
     hipError_t e = launch_strided_gemm(fmt, p, st, bf16);
     if (e != hipSuccess) return hip_fail(e, "strided gemm launch");
     return W4A16_OK;

@@ -42,6 +42,7 @@ __device__ __forceinline__ int bswz(int n, int kc) { return kc ^ ((n >> 3) & 7);
 
 template <int FMT, int BM, int D, bool MOE>
 __global__ void __launch_bounds__(256) prefill_kernel(PrefillParams p) {
+    if (p.gate && *p.gate != p.gate_want) return;   // uniform: the whole grid returns
     constexpr int WM = BM / 2;          // rows per wave
     constexpr int RB = WM / 16;         // row blocks per wave
     constexpr int CB = 8;               // column blocks per wave (128 columns)
@@ -314,6 +315,7 @@ constexpr int PF_THREADS = 512;   // 8 waves: 4 along M x 2 along N
 
 template <int FMT, int BM, int BN, bool MOE>
 __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p) {
+    if (p.gate && *p.gate != p.gate_want) return;   // uniform: the whole grid returns
     constexpr int WGM = 4, WGN = 2, NWV = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
     constexpr int RB = WM / 16, CB = WN / 16;

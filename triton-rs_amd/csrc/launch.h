@@ -96,6 +96,10 @@ struct PrefillParams {
     float* ws;
     uint32_t* counters;       // one per tile (FLAG_STRIDE apart), zero between calls
     int ksplit;
+    // gate (nullable): the kernel runs only when *gate == gate_want (a word an earlier kernel
+    // on the stream wrote); otherwise every workgroup returns at once
+    const uint32_t* gate;
+    uint32_t gate_want;
 };
 
 struct PrefillShape {
@@ -179,6 +183,8 @@ struct StridedParams {
     int stride_am, stride_ak, stride_qwk, stride_qwn, stride_sk, stride_sn;
     int stride_qzk, stride_qzn, stride_cm, stride_cn;
     int zero_offset;
+    const uint32_t* gate;     // nullable: run only when *gate == gate_want (as PrefillParams)
+    uint32_t gate_want;
 };
 // bf16: activations, scales and output are bfloat16 (same layouts)
 hipError_t launch_strided_gemm(int fmt, const StridedParams& p, hipStream_t st, bool bf16 = false);
@@ -203,6 +209,11 @@ hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st, bool 
 // kernel (xfrag_bytes(M, K) bytes).
 hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
                                    int N, hipStream_t st);
+// perm (K entries) of the rows in group order, computed on the device from g_idx, and gate[0] =
+// 1 when every group holds exactly G rows, else 0 (perm then the identity). K <= 32768,
+// K / G <= 1024.
+hipError_t launch_act_order_perm(const int32_t* g_idx, int32_t* perm, uint32_t* gate, int K, int G,
+                                 hipStream_t st);
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
                                  hipStream_t st, bool frag = false);
 
@@ -284,6 +295,7 @@ struct ScratchSource {
     size_t max_partial_bytes;
     size_t max_tiles;
     bool may_probe;   // may run the XCD placement probe (it allocates)
+    bool may_allocate;   // may take per-stream buffers (act-order repack beyond 64 rows)
     int (*get)(hipStream_t st, size_t partial_bytes, Scratch* out);
 };
 ScratchSource alloc_scratch_source();

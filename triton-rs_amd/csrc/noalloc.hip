@@ -85,7 +85,7 @@ static int noalloc_scratch(hipStream_t st, size_t partial_bytes, Scratch* out) {
     return W4A16_OK;
 }
 
-static const ScratchSource NOALLOC_SCRATCH = {NA_PARTIAL_BYTES, NA_MAX_TILES, false, noalloc_scratch};
+static const ScratchSource NOALLOC_SCRATCH = {NA_PARTIAL_BYTES, NA_MAX_TILES, false, false, noalloc_scratch};
 
 }  // namespace w4a16
 

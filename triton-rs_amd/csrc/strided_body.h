@@ -21,6 +21,7 @@ constexpr int STR_LDA = STR_BK + 8;  // halfs per LDS row (pad: 80-byte rows)
 
 template <int FMT, typename E = half_t>
 __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
+    if (p.gate && *p.gate != p.gate_want) return;   // uniform: the whole grid returns
     typedef typename vec8<E>::type e8_t;
     __shared__ __attribute__((aligned(16))) E As[STR_BM][STR_LDA];
     __shared__ __attribute__((aligned(16))) E Bs[STR_BN][STR_LDA];   // [n][k]

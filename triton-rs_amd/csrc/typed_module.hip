@@ -29,6 +29,7 @@ static __device__ __forceinline__ StridedParams make_params(TYPED_PARAMS, int ze
     p.stride_qwn = stride_qwn; p.stride_sk = stride_sk; p.stride_sn = stride_sn;
     p.stride_qzk = stride_qzk; p.stride_qzn = stride_qzn; p.stride_cm = stride_cm;
     p.stride_cn = stride_cn; p.zero_offset = zero_offset;
+    p.gate = nullptr; p.gate_want = 0;
     return p;
 }
 
