@@ -98,7 +98,11 @@ W4A16_API int w4a16_init(int32_t device);
  * captured call stays valid for the life of the process. Growing the workspace is not
  * possible under stream capture: make one call of the largest size before capturing, or
  * the call fails with W4A16_ERR_UNSUPPORTED. Concurrent calls on different streams are
- * safe. */
+ * safe. With g_idx beyond 64 rows (GPTQ formats, K <= 32768, K / group_size <= 1024) each
+ * call also computes the group order of the rows on the device, repacks the rows and gathers
+ * x into per-(device, stream) buffers (grown like the workspace) and runs the prefill
+ * kernel on them; when g_idx's groups do not each hold exactly group_size rows (or an entry
+ * is out of range) the generic kernel runs instead, decided on the device. */
 W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweight,
                          const void* scales, const void* qzeros, const int32_t* g_idx,
                          void* out, int32_t M, int32_t N, int32_t K, int32_t group_size,
@@ -111,7 +115,8 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
  * (8 MiB: at most 1024 split-K tiles and 6.9 MiB of partials), one per device, held until the
  * process ends; the call itself allocates nothing. A call whose planned kernel would need
  * more than that runs a kernel that needs no scratch instead (the prefill kernel without a K
- * split, or the generic kernel), so its result may differ from w4a16_gemm's in the last bits.
+ * split, or the generic kernel), and act-order beyond 64 rows runs the generic kernel (the
+ * repacked rows would not fit), so such results may differ from w4a16_gemm's in the last bits.
  * All calls on one device share its array: calls that overlap in time on one device (other
  * streams or threads) race and must be serialised by the caller. The device's array is set
  * up by w4a16_init (recommended before capture) or by the first call on the device. */
@@ -347,7 +352,12 @@ W4A16_API int hiprt_module_load(hiprt_ctx* ctx, const void* binary, size_t size,
                                 hiprt_module** out);
 W4A16_API int hiprt_module_unload(hiprt_module* module);
 
-/* DeviceRuntime::launch. Arguments are packed at their natural alignment. */
+/* DeviceRuntime::launch. Arguments are packed at their natural alignment. A launch of
+ * w4a16_gptq_gemm_typed or awq_gemm_int4_typed from the library's own w4a16_typed.hsaco
+ * (recognised at load by its marker symbol) that follows that module's contract (the 19
+ * arguments, optionally the two scratch pointers; grid (cdiv(m, 64), cdiv(n, 64), 1), block
+ * (256, 1, 1), no dynamic LDS) is run by the C-ABI entry of the same name, i.e. on the planned
+ * kernels; any other launch runs the named kernel of the module as given. */
 W4A16_API int hiprt_launch(hiprt_ctx* ctx, const hiprt_module* module, const char* kernel_name,
                            const uint32_t grid[3], const uint32_t block[3],
                            uint32_t shared_mem_bytes, void* stream, const hiprt_arg* args,
