@@ -227,6 +227,14 @@ PMC_WORKLOADS = {
     "prep_c1_m8_k4096_n14336": ("awq", 8, 4096, 14336, 128, False),
     "prep_c3_k4096_n14336": ("awq", 2048, 4096, 14336, 128, False),
     "prep_c3_k14336_n4096": ("awq", 2048, 14336, 4096, 128, False),
+    # the prepared small-batch kernel (x rewritten in fragment order first), plain and
+    # act-order (group-order repack, then the layout; x gathered by perm per call)
+    "prep_c2_plain_m16": ("gptq", 16, 4096, 6144, 128, False),
+    "prep_c2_plain_m64": ("gptq", 64, 4096, 6144, 128, False),
+    "prep_c2_m16": ("gptq", 16, 4096, 6144, 128, True),
+    "prep_c2_m64": ("gptq", 64, 4096, 6144, 128, True),
+    # act-order beyond 64 rows through w4a16_gemm (group order computed per call)
+    "c2_m2048": ("gptq", 2048, 4096, 6144, 128, True),
 }
 
 
@@ -279,13 +287,20 @@ def pmc_child(args) -> int:
         x = torch.randn((M, K), device=dev).half()
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
         if args.pmc_workload.startswith("prep_"):
-            prep = [pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
-                    for qw, sc, qz in sets]
+            perm = None
+            if act_order:   # group order once, then the layout of the repacked rows
+                prep = []
+                for qw, sc, qz in sets:
+                    qs, perm = pkg.prepare_act_order(qw, g_idx, group_size=G)
+                    prep.append(pkg.prepare_layout(qs, sc, qz, fmt=fmt, group_size=G, zero_offset=1))
+            else:
+                prep = [pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
+                        for qw, sc, qz in sets]
             del sets
             torch.cuda.synchronize()
             torch.cuda.empty_cache()
             for i in range(PMC_WARM + PMC_MEASURED):
-                pkg.gemm_prepared(x, prep[i % len(prep)], out=out)
+                pkg.gemm_prepared(x, prep[i % len(prep)], perm=perm, out=out)
             sets = prep
         else:
             for i in range(PMC_WARM + PMC_MEASURED):

@@ -98,10 +98,15 @@ gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restric
 // gate[0] = 1 when every group holds exactly G rows (group g then occupies rows [g G, g G + G)
 // of that order, as the prefill kernel assumes), else 0 with perm the identity (so that the
 // kernels reading it stay in bounds). One workgroup of 16 waves; wave w takes rows
-// [w P, w P + P), P = ceil(K / 16): it counts them per group, the counts become each wave's
-// starting position per group (wave order), then the wave places its rows 64 at a time, each
-// lane after the earlier lanes of its 64 with the same group. K <= 32768, K / G <= 1024.
+// [w P, w P + P), P = ceil(K / 16) <= 2048, lane l rows w P + l + 64 i (i < 32): it loads all
+// of its g_idx entries at once into registers, counts them per group (LDS atomics), the counts
+// become each wave's starting position per group (wave order), then the wave places its rows
+// 64 at a time, each lane after the earlier lanes of its 64 with the same group (found with one
+// ballot per bit of the group index; 64 lane-by-lane compares instead cost 16 us at K = 4096,
+// the 16 waves sharing one CU's four SIMDs).
+// K <= 32768, K / G <= 1024.
 constexpr int ORDER_MAX_GROUPS = 1024;
+constexpr int ORDER_PER_LANE = 32;   // 32768 rows / 16 waves / 64 lanes
 
 __global__ void __launch_bounds__(1024)
 act_order_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ perm,
@@ -110,15 +115,24 @@ act_order_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ p
     __shared__ int bad;
     const int groups = K / G;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+    const int per = (K + 15) / 16;
+    const int k0 = min(K, w * per), k1 = min(K, k0 + per);
+    int gv[ORDER_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < ORDER_PER_LANE; ++i) {
+        const int k = k0 + lane + 64 * i;
+        gv[i] = k < k1 ? g_idx[k] : -1;
+    }
     for (int i = t; i < 16 * ORDER_MAX_GROUPS; i += 1024) (&pos[0][0])[i] = 0;
     if (t == 0) bad = 0;
     __syncthreads();
-    const int per = (K + 15) / 16;
-    const int k0 = min(K, w * per), k1 = min(K, k0 + per);
-    for (int k = k0 + lane; k < k1; k += 64) {
-        const int g = g_idx[k];
-        if ((unsigned)g >= (unsigned)groups) bad = 1;
-        else atomicAdd(&pos[w][g], 1);
+#pragma unroll
+    for (int i = 0; i < ORDER_PER_LANE; ++i) {
+        const int k = k0 + lane + 64 * i;
+        if (k < k1) {
+            if ((unsigned)gv[i] >= (unsigned)groups) bad = 1;
+            else atomicAdd(&pos[w][gv[i]], 1);
+        }
     }
     __syncthreads();
     for (int g = t; g < groups; g += 1024) {
@@ -135,12 +149,20 @@ act_order_perm_kernel(const int32_t* __restrict__ g_idx, int32_t* __restrict__ p
     if (bad) {   // uniform
         for (int k = t; k < K; k += 1024) perm[k] = k;
     } else {
-        for (int kc = k0; kc < k1; kc += 64) {
-            const int k = kc + lane;
-            const int g = k < k1 ? g_idx[k] : -1;
-            int rank = 0;
 #pragma unroll
-            for (int i = 0; i < 64; ++i) rank += (i < lane && __builtin_amdgcn_readlane(g, i) == g) ? 1 : 0;
+        for (int i = 0; i < ORDER_PER_LANE; ++i) {
+            if (k0 + 64 * i >= k1) break;   // uniform in the wave
+            const int k = k0 + lane + 64 * i;
+            const int g = gv[i];            // -1 past the wave's rows
+            // lanes holding the same group: one ballot per bit of the group index, each lane
+            // keeping the lanes that agree with it on that bit; the rank counts those below it
+            uint64_t same = __ballot(g >= 0);
+            for (int j = 0; (1 << j) < groups; ++j) {   // uniform
+                const uint64_t b = __ballot((g >> j) & 1);
+                same &= ((g >> j) & 1) ? b : ~b;
+            }
+            const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(same >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)same, 0u));
             const int base = g >= 0 ? pos[w][g] : 0;
             // every lane has read its base (one LDS read of the wave) before any lane adds
             __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
