@@ -309,6 +309,23 @@ def test_prefill_narrow_tiles(torch_cuda, orc, fmt, M, K, N):
 
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
+@pytest.mark.parametrize("M,K,N", [(2048, 1024, 6144), (1024, 2048, 6144), (300, 640, 768)])
+def test_prefill_192_wide_tiles(torch_cuda, orc, fmt, M, K, N):
+    """256 x 192 tiles (widths 224 and 256 do not divide evenly into the CUs: N = 6144 gives
+    256 workgroups of 192 columns where 256-wide tiles give 192): unsplit, K split in two
+    (M = 1024), and a row tail (M = 300); repeated calls are bit-identical."""
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2450 + M + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, 128) == "prefill"
+    y = _run_gemm(torch_cuda, p)
+    y2 = _run_gemm(torch_cuda, p)
+    assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
+    rows = np.unique(np.r_[0, 255, M - 1, np.random.default_rng(7).choice(M, 16)]).astype(np.int32)
+    ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows)
+    assert_parity(y[rows], ref.astype(np.float64), what=f"prefill 192-wide fmt={fmt} M={M} N={N}")
+
+
+@pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
 @pytest.mark.parametrize("M,K,N,G", [(2000, 640, 14336, 128), (512, 64, 128, 64),
                                      (512, 192, 128, 64), (1000, 128, 14336, 64)])
 def test_prefill_256_row_tiles(torch_cuda, orc, fmt, M, K, N, G):

@@ -463,7 +463,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     const int ph = DQC == 4 ? (t >> 8) : ((t >> 7) & 1);
     const int pq = DQC == 4 ? 0 : (t >> 8);
     (void)pn; (void)ph; (void)pq;
-    static_assert(BN <= 128 || BN > 192, "tile width");
+    static_assert(BN <= 128 || BN >= 192, "tile width");
     (void)DQW;
 
     // The dequantisation comes in three parts, so that its VALU work can be placed between
@@ -734,14 +734,18 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int
         // 4096: 256 x 256 with 2 splits, 231 us against 258 us for 256 x 128 unsplit) and fixes
         // the grids that left CUs idle: one GPU's share of an 8-way tensor-parallel layer,
         // M=2048, 4096 -> 1792, took 128 x 224 tiles (128 workgroups) in ~75 us, 256 x 128 with
-        // 2 splits 53 us; 4096 -> 3584 128 x 224 ~85 us, 256 x 128 73 us. A split keeps at
-        // least 8 stages of K. Ties go to larger tiles and fewer splits.
+        // 2 splits 53 us; 4096 -> 3584 128 x 224 ~85 us, 256 x 128 73 us. 256 x 192 tiles
+        // (e = 1.2: a quarter of the dequantising lanes idle, narrower wave tiles) for widths
+        // that 224 does not divide: N = 6144, K = 4096, M = 1024 / 2048 / 4096: 78.9 / 113.7 /
+        // 229.6 us with 256 x 256 (2 splits / 1 / 1) against 68.0 / 102.4 / 203.1 us (the 192
+        // workgroups of 256 x 256 at M = 2048 leave 64 CUs idle). A split keeps at least 8
+        // stages of K. Ties go to larger tiles and fewer splits.
         double best = -1.0;
         for (int bm : {256, 128}) {
-            for (int bn : {256, 224, 128}) {
+            for (int bn : {256, 224, 192, 128}) {
                 if (N % bn) continue;
-                if (bn == 128 && bm != 256) continue;   // 128-wide tiles only with 256 rows
-                const double e = bm == 128 ? 1.35 : bn == 128 ? 1.15 : 1.0;
+                if ((bn == 128 || bn == 192) && bm != 256) continue;   // 128/192-wide tiles only with 256 rows
+                const double e = bm == 128 ? 1.35 : bn == 128 ? 1.15 : bn == 192 ? 1.2 : 1.0;
                 const long long tiles = (long long)(N / bn) * ((M + bm - 1) / bm);
                 for (int ks = 1; ks <= 4; ks *= 2) {
                     if (ks > 1 && (bm != 256 || ks > max_ksplit || (K / BK) % ks || K / BK / ks < 8))
@@ -808,6 +812,7 @@ static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, si
         else launch_dma_t<FMT, 256, 256, true>(p, grid, lds, st);
     } else {
         if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false>(p, grid, lds, st);
+        else if (bm == 256 && bn == 192) launch_dma_t<FMT, 256, 192, false>(p, grid, lds, st);
         else if (bm == 256 && bn == 128) launch_dma_t<FMT, 256, 128, false>(p, grid, lds, st);
         else if (bm == 256) launch_dma_t<FMT, 256, 256, false>(p, grid, lds, st);
         else if (bn == 224) launch_dma_t<FMT, 128, 224, false>(p, grid, lds, st);
