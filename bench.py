@@ -629,6 +629,20 @@ def extras(torch, pkg, dev, stream, args):
             "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
         progress(f"fused moe block_m={bm}: {ms:.3f} ms")
         del ws
+    # the same layer on the experts in the prepared layout (w4a16_prepare_layout per expert,
+    # once; timed: w4a16_fused_moe_prepared only)
+    w13p = pkg.prepare_layout_experts(*w13, fmt="gptq", group_size=L["G"], zero_offset=1)
+    w2p = pkg.prepare_layout_experts(*w2, fmt="gptq", group_size=L["G"], zero_offset=1)
+    ws = torch.empty(pkg.lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, 64),
+                     dtype=torch.uint8, device=dev)
+    ms = time_calls(torch, lambda i: pkg.fused_moe_prepared(x, logits, w13p, w2p, topk=topk, block_m=64,
+                                                            out=out, workspace=ws),
+                    10, 5, stream, 1, batch_calls=20, graph_calls=10, n_graphs=1)[1]
+    res["c4_fused_moe_prepared"] = {
+        "ms_per_layer": round(ms, 3), "TFLOPs": round(flops / (ms * 1e-3) / 1e12, 1),
+        "frac_mfma": round(flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS, 4)}
+    progress(f"fused moe on prepared experts: {ms:.3f} ms")
+    del ws, w13p, w2p
     del w13, w2, L
     torch.cuda.empty_cache()
     res["achievable"] = achievable_refs(torch, dev, stream)

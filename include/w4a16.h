@@ -311,6 +311,20 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
                               int32_t block_m, int32_t gptq_zero_offset, void* workspace,
                               size_t workspace_bytes, void* out);
 
+/* The same layer on expert weights in the prepared layout (no reference counterpart, like
+ * w4a16_prepare_layout): w13_prepared holds E consecutive w4a16_prepare_layout outputs of the
+ * experts' K -> 2I matrices, each w4a16_prepared_bytes(K, 2I, group_size) bytes (256-byte
+ * aligned), w2_prepared E of the I -> K matrices. Same routing, tiles and workspace as
+ * w4a16_fused_moe (w4a16_fused_moe_workspace_size); the grouped GEMMs read the prepared strips.
+ * Needs group_size % 64 == 0 and the shapes the expert-tile kernels take (else
+ * W4A16_ERR_UNSUPPORTED). */
+W4A16_API int w4a16_fused_moe_prepared(void* stream, const void* x, const float* router_logits,
+                                       int32_t T, int32_t K, int32_t I, int32_t E, int32_t topk,
+                                       int32_t renormalize, const void* w13_prepared,
+                                       const void* w2_prepared, int32_t group_size,
+                                       int32_t block_m, void* workspace, size_t workspace_bytes,
+                                       void* out);
+
 /* ------------------------------------------------------------------ runtime
  * A HIP backend for the reference's DeviceRuntime trait (crates/triton-runtime/src/
  * lib.rs:64-85): load a code object, launch a kernel by name with KernelArg-style

@@ -305,3 +305,92 @@ def test_fused_layer_random_shapes_equal_block_composition(torch_cuda, orc, case
     diff = np.argwhere(got != want)
     assert diff.size == 0, f"{len(diff)} of {got.size} outputs differ, first at {diff[0].tolist()}"
     _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, f"random layer {case}")
+
+
+# ------------------------------------------------- the layer on experts in the prepared layout
+
+def _prepared_layer(P, xd, ld, w13, w2, topk, fmt, G, bm):
+    w13p = P.prepare_layout_experts(*w13, fmt=FMT_NAME[fmt], group_size=G, zero_offset=1)
+    w2p = P.prepare_layout_experts(*w2, fmt=FMT_NAME[fmt], group_size=G, zero_offset=1)
+    return P.fused_moe_prepared(xd, ld, w13p, w2p, topk=topk, block_m=bm)
+
+
+@pytest.mark.parametrize("case", TILE_CASES, ids=[f"T{c[0]}_E{c[1]}_I{c[4]}_skew{c[5]}"
+                                                  for c in TILE_CASES])
+def test_fused_moe_prepared_tile_cases(torch_cuda, orc, case):
+    """w4a16_fused_moe_prepared over every expert-tile shape: within the GEMM tolerance of
+    the layer on the checkpoint (the same weights W16, another order of the k sums within a
+    stage), sampled tokens against the oracle, repeated calls bit-identical."""
+    T, E, topk, K, I, skew, fmt, bm = case
+    P = pkg()
+    g = np.random.default_rng(180 + T + I)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    if skew is not None:
+        logits[:, skew] += 4.0
+    G = 128
+    w13 = tuple(to_dev(a) for a in stacked_weights(fmt, E, K, 2 * I, G, 181))
+    w2 = tuple(to_dev(a) for a in stacked_weights(fmt, E, I, K, G, 182))
+    if fmt == SYM:
+        w13 = (w13[0], w13[1], None)
+        w2 = (w2[0], w2[1], None)
+    xd, ld = to_dev(x), to_dev(logits)
+    y = _prepared_layer(P, xd, ld, w13, w2, topk, fmt, G, bm)
+    y2 = _prepared_layer(P, xd, ld, w13, w2, topk, fmt, G, bm)
+    ck = P.fused_moe(xd, ld, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G, block_m=bm)
+    torch_cuda.cuda.synchronize()
+    a = y.cpu().numpy()
+    assert np.array_equal(a.view(np.uint16), y2.cpu().numpy().view(np.uint16))
+    assert np.all(np.isfinite(a))
+    assert_parity(a, ck.cpu().numpy().astype(np.float64), what=f"prepared vs checkpoint {case}")
+    _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, f"prepared tile case {case}")
+
+
+@pytest.mark.parametrize("fmt", [GPTQ, AWQ])
+def test_fused_moe_prepared_down_projection_split_k(torch_cuda, orc, fmt):
+    """I = 8192: the prepared down projection splits its K over two workgroups per tile."""
+    T, E, topk, K, I, G = 512, 4, 2, 256, 8192, 128
+    P = pkg()
+    g = np.random.default_rng(190 + fmt)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    w13 = tuple(to_dev(a) for a in stacked_weights(fmt, E, K, 2 * I, G, 191))
+    w2 = tuple(to_dev(a) for a in stacked_weights(fmt, E, I, K, G, 192))
+    xd, ld = to_dev(x), to_dev(logits)
+    y = _prepared_layer(P, xd, ld, w13, w2, topk, fmt, G, 64)
+    ck = P.fused_moe(xd, ld, w13, w2, topk=topk, fmt=FMT_NAME[fmt], group_size=G)
+    torch_cuda.cuda.synchronize()
+    assert_parity(y.cpu().numpy(), ck.cpu().numpy().astype(np.float64), what="prepared split-K down")
+    _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, fmt, G, g, "prepared split-K down")
+
+
+def test_fused_moe_prepared_config4(torch_cuda, orc):
+    """Config 4 at full size on prepared experts: every token within the GEMM tolerance of
+    the layer on the checkpoint, sampled tokens against the oracle."""
+    P = pkg()
+    T, E, topk, K, I, G = 512, 8, 2, 4096, 14336, 128
+    g = np.random.default_rng(0x5EED0004)
+    x = synth.rand_x(g, T, K)
+    logits = g.standard_normal((T, E)).astype(np.float32)
+    w13 = tuple(to_dev(a) for a in stacked_weights(GPTQ, E, K, 2 * I, G, 0x5EED0104))
+    w2 = tuple(to_dev(a) for a in stacked_weights(GPTQ, E, I, K, G, 0x5EED0204))
+    xd, ld = to_dev(x), to_dev(logits)
+    ck = P.fused_moe(xd, ld, w13, w2, topk=topk, fmt="gptq", group_size=G).cpu().numpy()
+    y = _prepared_layer(P, xd, ld, w13, w2, topk, GPTQ, G, 64)
+    torch_cuda.cuda.synchronize()
+    assert_parity(y.cpu().numpy(), ck.astype(np.float64), what="config 4 prepared vs checkpoint")
+    _check_sampled_tokens(orc, y, x, logits, w13, w2, topk, GPTQ, G, g, "config 4 prepared")
+
+
+def test_fused_moe_prepared_rejects_unsupported_groups(torch_cuda):
+    """Group size 32 has a prepared layout but no expert-tile B stage: Unsupported."""
+    P = pkg()
+    T, E, topk, K, I, G = 32, 4, 2, 256, 256, 32
+    g = np.random.default_rng(199)
+    w13 = tuple(to_dev(a) for a in stacked_weights(GPTQ, E, K, 2 * I, G, 198))
+    w2 = tuple(to_dev(a) for a in stacked_weights(GPTQ, E, I, K, G, 197))
+    w13p = P.prepare_layout_experts(*w13, fmt="gptq", group_size=G)
+    w2p = P.prepare_layout_experts(*w2, fmt="gptq", group_size=G)
+    with pytest.raises(P.Unsupported):
+        P.fused_moe_prepared(to_dev(synth.rand_x(g, T, K)), to_dev(g.standard_normal((T, E)).astype(np.float32)),
+                             w13p, w2p, topk=topk)

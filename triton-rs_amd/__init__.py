@@ -77,7 +77,7 @@ EXPORTED = (
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
     "w4a16_moe_gemm", "fused_silu_mul_interleaved_f16", "fused_silu_mul_interleaved_f32",
     "w4a16_moe_sum",
-    "w4a16_fused_moe_workspace_size", "w4a16_fused_moe",
+    "w4a16_fused_moe_workspace_size", "w4a16_fused_moe", "w4a16_fused_moe_prepared",
     "hiprt_create", "hiprt_destroy", "hiprt_module_load", "hiprt_module_unload", "hiprt_launch",
     "hiprt_stream_create", "hiprt_stream_destroy", "hiprt_stream_synchronize", "hiprt_malloc",
     "hiprt_free", "hiprt_memcpy_htod_async", "hiprt_memcpy_dtoh_async", "hiprt_memset_async",
@@ -131,6 +131,8 @@ def lib() -> ctypes.CDLL:
         L.w4a16_fused_moe_workspace_size.argtypes = [_I] * 6
         L.w4a16_fused_moe.argtypes = [_P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
                                       _P, _I, _I, _I, _P, _Z, _P]
+        L.w4a16_fused_moe_prepared.argtypes = [_P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _I, _I,
+                                               _P, _Z, _P]
         L.hiprt_create.argtypes = [_I, ctypes.POINTER(_P)]
         L.hiprt_destroy.argtypes = [_P]
         L.hiprt_module_load.argtypes = [_P, _P, _Z, ctypes.POINTER(_P)]
@@ -501,6 +503,50 @@ def fused_moe(x, router_logits, w13, w2, topk=2, fmt="gptq", group_size=128, blo
                                 E, topk, int(renormalize), _ptr(q13), _ptr(s13), _ptr(z13),
                                 _ptr(q2), _ptr(s2), _ptr(z2), group_size, block_m, zero_offset,
                                 _ptr(workspace), workspace.numel(), _ptr(out)))
+    return out
+
+
+def prepare_layout_experts(qweight, scales, qzeros, fmt="gptq", group_size: int = 128,
+                           zero_offset: int = 1) -> PreparedWeights:
+    """Stacked experts ([E] x checkpoint tensors) into one buffer of E consecutive prepared
+    matrices (w4a16_prepare_layout per expert), as w4a16_fused_moe_prepared takes them."""
+    E = qweight.shape[0]
+    f = _fmt(fmt)
+    if f == FMT_AWQ:
+        K, N = qweight.shape[1], qweight.shape[2] * 8
+    else:
+        K, N = qweight.shape[1] * 8, qweight.shape[2]
+    per = prepared_bytes(K, N, group_size)
+    if per == 0:
+        raise Unsupported(f"no prepared layout for K={K} N={N} group_size={group_size}")
+    buf = torch.empty(E * per, dtype=torch.uint8, device=qweight.device)
+    for e in range(E):
+        check(lib().w4a16_prepare_layout(_stream(qweight), f, _ptr(qweight[e]), _ptr(scales[e]),
+                                         None if qzeros is None else _ptr(qzeros[e]), K, N,
+                                         group_size, zero_offset, _ptr(buf[e * per:]), per))
+    return PreparedWeights(buf, K, N, group_size)
+
+
+def fused_moe_prepared(x, router_logits, w13: PreparedWeights, w2: PreparedWeights, topk=2,
+                       block_m=64, renormalize=True, out=None, workspace=None):
+    """Whole MoE layer through w4a16_fused_moe_prepared: w13 / w2 from prepare_layout_experts
+    (K -> 2I and I -> K per expert)."""
+    _require(x, "x", _HALF)
+    T, K = x.shape
+    E = router_logits.shape[1]
+    I = w2.K
+    if w13.K != K or w13.N != 2 * I or w2.N != K or w13.group_size != w2.group_size:
+        raise InvalidArgument("w13 must be K -> 2I and w2 I -> K with one group size")
+    G = w13.group_size
+    need = lib().w4a16_fused_moe_workspace_size(T, E, topk, I, K, block_m)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    if out is None:
+        out = torch.empty((T, K), dtype=torch.float16, device=x.device)
+    check(lib().w4a16_fused_moe_prepared(_stream(x), _ptr(x), _ptr(router_logits.contiguous()), T,
+                                         K, I, E, topk, int(renormalize), _ptr(w13.buffer),
+                                         _ptr(w2.buffer), G, block_m, _ptr(workspace),
+                                         workspace.numel(), _ptr(out)))
     return out
 
 

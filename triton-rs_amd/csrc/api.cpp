@@ -1006,6 +1006,110 @@ W4A16_API size_t w4a16_fused_moe_workspace_size(int32_t T, int32_t E, int32_t to
     return moe_layout(T, E, topk, I, K, block_m).total;
 }
 
+// The expert-tile layer after routing: align into expert tiles, gate/up GEMM, silu * mul,
+// down GEMM (K split as moe_tiles chose), weighted sum. Weights in a checkpoint format or in
+// the prepared layout (fmt FMT_PREP: the q pointers are stacked prepared buffers, the scale and
+// zero pointers unused).
+struct MoeWeights {
+    int fmt;
+    const void *w13q, *w13s, *w13z, *w2q, *w2s, *w2z;
+    int64_t q13, s13, z13, q2, s2, z2;   // per-expert strides in elements
+    int32_t zero_offset;
+};
+static int fused_moe_tiles(void* stream, const MoeWeights& W, const void* x, int32_t T, int32_t K,
+                           int32_t I, int32_t E, int32_t topk, int32_t G, int32_t block_m,
+                           const MoeLayout& L, const MoeTiles& mt, char* ws, void* out) {
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto* ids = reinterpret_cast<int32_t*>(ws + L.ids);
+    auto* wts = reinterpret_cast<float*>(ws + L.weights);
+    auto* sorted = reinterpret_cast<int32_t*>(ws + L.sorted);
+    auto* experts = reinterpret_cast<int32_t*>(ws + L.experts);
+    auto* npp = reinterpret_cast<int32_t*>(ws + L.npp);
+    auto* tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
+    auto* ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
+    auto* ctr = reinterpret_cast<uint32_t*>(ws + L.ctr);
+    void* h = ws + L.h;
+    void* a = ws + L.a;
+    void* yp = ws + L.yp;
+    const int32_t P = T * topk;
+    const int64_t n13 = 2 * (int64_t)I;
+    hipError_t e = launch_moe_align(ids, P, E, block_m, L.capacity, sorted, experts, npp, st,
+                                    mt.bm, tiles, ntiles, ctr, mt.ks2 > 1 ? L.n_ctr : 0);
+    if (e != hipSuccess) return hip_fail(e, "moe align launch");
+    const int max_tiles = moe_max_tiles(P, E, mt.bm);
+    PrefillParams p{};
+    p.sorted_ids = sorted; p.expert_ids = experts; p.num_post_padded = npp;
+    p.tiles = tiles; p.num_tiles = ntiles;
+    p.num_pairs = P; p.G = G; p.zero_offset = W.zero_offset; p.M = L.capacity; p.num_experts = E;
+    // gate/up: h[p] = x[p / topk] @ W13[e]
+    p.x = static_cast<const half_t*>(x);
+    p.qweight = static_cast<const uint32_t*>(W.w13q);
+    p.scales = static_cast<const half_t*>(W.w13s);
+    p.qzeros = static_cast<const uint32_t*>(W.w13z);
+    p.out = static_cast<half_t*>(h);
+    p.N = (int)n13; p.K = K; p.a_div = topk;
+    p.qweight_stride = W.q13; p.scales_stride = W.s13; p.qzeros_stride = W.z13;
+    e = launch_moe_gemm_tiles(W.fmt, p, mt.bm, mt.bn13, max_tiles, st);
+    if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
+    int rc = fused_silu_mul_interleaved_f16(stream, h, a, I, P * I);
+    if (rc) return rc;
+    // down: yp[p] = a[p] @ W2[e]
+    p.x = static_cast<const half_t*>(a);
+    p.qweight = static_cast<const uint32_t*>(W.w2q);
+    p.scales = static_cast<const half_t*>(W.w2s);
+    p.qzeros = static_cast<const uint32_t*>(W.w2z);
+    p.out = static_cast<half_t*>(yp);
+    p.N = K; p.K = I; p.a_div = 1;
+    p.qweight_stride = W.q2; p.scales_stride = W.s2; p.qzeros_stride = W.z2;
+    if (mt.ks2 > 1) {
+        p.ksplit = mt.ks2;
+        p.ws = reinterpret_cast<float*>(ws + L.part);
+        p.counters = ctr;
+    }
+    e = launch_moe_gemm_tiles(W.fmt, p, mt.bm, mt.bn2, max_tiles, st);
+    if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
+    return w4a16_moe_sum(stream, yp, wts, out, T, topk, K);
+}
+
+W4A16_API int w4a16_fused_moe_prepared(void* stream, const void* x, const float* router_logits,
+                                       int32_t T, int32_t K, int32_t I, int32_t E, int32_t topk,
+                                       int32_t renormalize, const void* w13_prepared,
+                                       const void* w2_prepared, int32_t G, int32_t block_m,
+                                       void* workspace, size_t workspace_bytes, void* out) {
+    if (!x || !router_logits || !w13_prepared || !w2_prepared || !workspace || !out)
+        return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (int rc = check_moe_dims(T, E, topk)) return rc;
+    if (I < 1 || K < 1 || block_m < 1 || G < 1)
+        return fail(W4A16_ERR_INVALID_ARG, "bad sizes (K=%d I=%d block_m=%d group_size=%d)", K, I, block_m, G);
+    if (int rc = check_prep_shape(K, 2 * I, G)) return rc;
+    if (int rc = check_prep_shape(I, K, G)) return rc;
+    const MoeLayout L = moe_layout(T, E, topk, I, K, block_m);
+    if (workspace_bytes < L.total)
+        return fail(W4A16_ERR_INVALID_ARG, "workspace too small (%zu < %zu bytes)", workspace_bytes,
+                    L.total);
+    if (!aligned(workspace, 256) || !aligned(w13_prepared, 256) || !aligned(w2_prepared, 256) || !aligned(x, 16))
+        return fail(W4A16_ERR_INVALID_ARG,
+                    "workspace and prepared buffers must be 256-byte aligned, x 16-byte aligned");
+    const int32_t P = T * topk;
+    const MoeTiles mt = moe_tiles(P, E, K, I, device_cus());
+    const size_t b13 = prep_total_bytes(K, 2 * I, G), b2 = prep_total_bytes(I, K, G);
+    if (G % 64 || !mt.bn13 || !mt.bn2 || !moe_tiles_supported(2 * I, K, G, T, mt.bn13) ||
+        !moe_tiles_supported(K, I, G, P, mt.bn2) || b13 >= ((size_t)1 << 31) || b2 >= ((size_t)1 << 31))
+        return fail(W4A16_ERR_UNSUPPORTED,
+                    "prepared fused MoE needs the expert-tile kernels: group_size %% 64 == 0, 2I and K "
+                    "multiples of the tile widths, each expert's prepared matrix under 2 GiB "
+                    "(K=%d I=%d group_size=%d)", K, I, G);
+    int rc = w4a16_moe_route(stream, router_logits, T, E, topk, renormalize,
+                             reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + L.ids),
+                             reinterpret_cast<float*>(static_cast<char*>(workspace) + L.weights));
+    if (rc) return rc;
+    MoeWeights W{};
+    W.fmt = FMT_PREP;
+    W.w13q = w13_prepared; W.w2q = w2_prepared;
+    W.q13 = (int64_t)(b13 / 4); W.q2 = (int64_t)(b2 / 4);
+    return fused_moe_tiles(stream, W, x, T, K, I, E, topk, G, block_m, L, mt, static_cast<char*>(workspace), out);
+}
+
 W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float* router_logits,
                               int32_t T, int32_t K, int32_t I, int32_t E, int32_t topk,
                               int32_t renormalize, const void* w13_qweight, const void* w13_scales,
@@ -1033,7 +1137,6 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
     void* a = ws + L.a;
     void* yp = ws + L.yp;
     const int32_t P = T * topk;
-    hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = w4a16_moe_route(stream, router_logits, T, E, topk, renormalize, ids, wts);
     if (rc) return rc;
     // Expert tiles (one tile per expert's rows, whatever block_m padded them to) when both
@@ -1050,47 +1153,15 @@ W4A16_API int w4a16_fused_moe(void* stream, int fmt, const void* x, const float*
         if (!aligned(x, 16) || !aligned(w13_qweight, 16) || !aligned(w13_scales, 16) ||
             !aligned(w2_qweight, 16) || !aligned(w2_scales, 16))
             return fail(W4A16_ERR_INVALID_ARG, "tensors must be 16-byte aligned");
-        auto* tiles = reinterpret_cast<int32_t*>(ws + L.tiles);
-        auto* ntiles = reinterpret_cast<int32_t*>(ws + L.ntiles);
-        auto* ctr = reinterpret_cast<uint32_t*>(ws + L.ctr);
-        hipError_t e = launch_moe_align(ids, P, E, block_m, L.capacity, sorted, experts, npp, st,
-                                        mt.bm, tiles, ntiles, ctr, mt.ks2 > 1 ? L.n_ctr : 0);
-        if (e != hipSuccess) return hip_fail(e, "moe align launch");
-        const int max_tiles = moe_max_tiles(P, E, mt.bm);
-        PrefillParams p{};
-        p.sorted_ids = sorted; p.expert_ids = experts; p.num_post_padded = npp;
-        p.tiles = tiles; p.num_tiles = ntiles;
-        p.num_pairs = P; p.G = G; p.zero_offset = zero_offset; p.M = L.capacity; p.num_experts = E;
-        // gate/up: h[p] = x[p / topk] @ W13[e]
-        p.x = static_cast<const half_t*>(x);
-        p.qweight = static_cast<const uint32_t*>(w13_qweight);
-        p.scales = static_cast<const half_t*>(w13_scales);
-        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(w13_qzeros);
-        p.out = static_cast<half_t*>(h);
-        p.N = (int)n13; p.K = K; p.a_div = topk;
-        p.qweight_stride = (int64_t)K * n13 / 8; p.scales_stride = (int64_t)(K / G) * n13;
-        p.qzeros_stride = (int64_t)(K / G) * n13 / 8;
-        e = launch_moe_gemm_tiles(fmt, p, mt.bm, mt.bn13, max_tiles, st);
-        if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
-        rc = fused_silu_mul_interleaved_f16(stream, h, a, I, P * I);
-        if (rc) return rc;
-        // down: yp[p] = a[p] @ W2[e]
-        p.x = static_cast<const half_t*>(a);
-        p.qweight = static_cast<const uint32_t*>(w2_qweight);
-        p.scales = static_cast<const half_t*>(w2_scales);
-        p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(w2_qzeros);
-        p.out = static_cast<half_t*>(yp);
-        p.N = K; p.K = I; p.a_div = 1;
-        p.qweight_stride = (int64_t)I * K / 8; p.scales_stride = (int64_t)(I / G) * K;
-        p.qzeros_stride = (int64_t)(I / G) * K / 8;
-        if (mt.ks2 > 1) {
-            p.ksplit = mt.ks2;
-            p.ws = reinterpret_cast<float*>(ws + L.part);
-            p.counters = ctr;
-        }
-        e = launch_moe_gemm_tiles(fmt, p, mt.bm, mt.bn2, max_tiles, st);
-        if (e != hipSuccess) return hip_fail(e, "moe gemm launch");
-        return w4a16_moe_sum(stream, yp, wts, out, T, topk, K);
+        MoeWeights W{};
+        W.fmt = fmt;
+        W.w13q = w13_qweight; W.w13s = w13_scales;
+        W.w13z = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : w13_qzeros;
+        W.w2q = w2_qweight; W.w2s = w2_scales; W.w2z = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : w2_qzeros;
+        W.q13 = (int64_t)K * n13 / 8; W.s13 = (int64_t)(K / G) * n13; W.z13 = (int64_t)(K / G) * n13 / 8;
+        W.q2 = (int64_t)I * K / 8; W.s2 = (int64_t)(I / G) * K; W.z2 = (int64_t)(I / G) * K / 8;
+        W.zero_offset = zero_offset;
+        return fused_moe_tiles(stream, W, x, T, K, I, E, topk, G, block_m, L, mt, ws, out);
     }
     rc = w4a16_moe_align(stream, ids, P, E, block_m, L.capacity, sorted, experts, npp);
     if (!rc) {

@@ -827,7 +827,7 @@ static hipError_t launch_dma_any(int fmt, const PrefillParams& p, int bm, int bn
     if (fmt == FMT_AWQ) launch_dma_fmt<FMT_AWQ, MOE>(p, bm, bn, grid, lds, st);
     else if (fmt == FMT_GPTQ) launch_dma_fmt<FMT_GPTQ, MOE>(p, bm, bn, grid, lds, st);
     else if (fmt == FMT_GPTQ_SYM) launch_dma_fmt<FMT_GPTQ_SYM, MOE>(p, bm, bn, grid, lds, st);
-    else if constexpr (!MOE) launch_dma_fmt<FMT_PREP, false>(p, bm, bn, grid, lds, st);
+    else if (fmt == FMT_PREP) launch_dma_fmt<FMT_PREP, MOE>(p, bm, bn, grid, lds, st);
     else return hipErrorInvalidValue;
     return hipGetLastError();
 }
