@@ -70,6 +70,8 @@ def test_dequant_prepared_bit_exact(torch_cuda, orc, fmt, K, N, G, transposed):
     (AWQ, 8, 14336, 4096, 128), (GPTQ, 2, 1024, 512, 128), (GPTQ, 3, 1024, 512, 128),
     (SYM, 5, 2048, 256, 128), (AWQ, 6, 1536, 64, 256), (GPTQ, 7, 512, 32, 128),
     (AWQ, 2, 128, 16, 128), (AWQ, 8, 16384, 128, 128),
+    # 3..4 rows, two strips per workgroup: an odd strip count, 16 waves of 4 blocks
+    (SYM, 4, 1024, 16 * 33, 128), (AWQ, 3, 8192, 272, 128),
 ])
 def test_gemm_prepared_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
     P = pkg()

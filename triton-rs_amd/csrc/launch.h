@@ -244,6 +244,7 @@ struct PrepGemvShape {
     int waves;    // waves per workgroup (one workgroup per strip)
     bool mfma;    // matrix-core dot products (group_size % 128 == 0), else VALU dot2
     int mp;       // M > 1: rows per block slot of the A operand (2, 4 or 8)
+    int spw;      // M > 1: strips per workgroup
     size_t lds;   // dynamic LDS bytes
 };
 constexpr int PREP_GEMV_MAX_M = 8;

@@ -408,43 +408,50 @@ gemv_prep_valu_kernel(PrepParams p) {
     }
 }
 
-// M = 2..8: the same strips, waves and blocks, with the activations as MFMA A operands read
-// straight from global memory (x is a few hundred KiB at most and stays in the caches). An
-// A operand has 16 rows and M <= MP rows are needed, so one A register set carries P = 16 / MP
+// M = 2..4: SPW strips per workgroup over all of K, wave w taking blocks w BPW .. w BPW + BPW
+// - 1 of each, with the activations as MFMA A operands read straight from global memory (x is
+// a few hundred KiB at most and stays in the caches; SPW strips share each A load). An A
+// operand has 16 rows and M <= MP rows are needed, so one A register set carries P = 16 / MP
 // blocks: rows [b MP, b MP + MP) hold block b's activations (rows past M repeat row M - 1),
 // and the MFMA of block b leaves its result in those rows of D. The zero point is taken out
 // of the B operand exactly, (1024 + c q) - (1024 + c z) = c (q - z), c = 1 or 16 as in the
 // M = 1 kernel (A carries x / c), so D = sum_k x_k (q_k - z) per block, and y += s D per
-// block and row slot. VALU per 8 weights: one shift, four v_and_or_b32, four v_pk_add_f16.
-// Requires G % 128 == 0 (a block in one group) and blocks per wave BPW = 8.
-template <int MP>
+// block, strip and row slot; the (wave, slot) sums meet in LDS. VALU per 8 weights: one
+// shift, four v_and_or_b32, four v_pk_add_f16. Requires G % 128 == 0 (a block in one group).
+template <int MP, int BPW, int SPW>
 __global__ void __launch_bounds__(1024)
 gemv_prep_rows_kernel(PrepParams p) {
-    constexpr int BPW = 8, P = 16 / MP, S = BPW / P;   // blocks per A set, A sets per wave
-    constexpr int EC = BPW / 4;
+    constexpr int P = 16 / MP, S = BPW / P;
+    static_assert(BPW % P == 0 && (BPW == 4 || BPW == 8), "blocks per wave");
+    constexpr int EC = BPW / 4;   // table entries per lane per strip (one 32- or 64-bit load)
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int W = blockDim.x >> 6;
-    const int s = blockIdx.x;
-    const int M = p.M, blocks = p.K >> 7;
+    const int s0 = blockIdx.x * SPW;
+    const int M = p.M, blocks = p.K >> 7, NS = p.N >> 4;
     const int col = lane & 15, h = lane >> 4;
-    const unsigned char* strip = p.prep + (size_t)s * p.strip_bytes;
     const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
-    uint32_t* tab = reinterpret_cast<uint32_t*>(lds) + (size_t)wave * BPW * 16;   // BPW x 16
-    float* red = reinterpret_cast<float*>(lds + (size_t)W * BPW * 16 * 4);          // W x P x M x 16
-
-    // ---- loads: table entries, the A sets, then the blocks
+    const uint32_t pbytes = (uint32_t)NS * p.strip_bytes;
+    uint32_t* tab = reinterpret_cast<uint32_t*>(lds) + (size_t)wave * SPW * BPW * 16;
+    float* red = reinterpret_cast<float*>(lds + (size_t)W * SPW * BPW * 16 * 4);   // W x P x SPW x M x 16
     const bufrsrc_t xr = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
-    const bufrsrc_t tr = make_rsrc(strip, tbytes);
-    const bufrsrc_t wr = make_rsrc(strip + tbytes, (uint32_t)p.K * 8u);
-    uint32_t ev[EC];
-    {
-        const uint32_t off = (uint32_t)(wave * BPW * 16 + EC * lane) * 4u;
-        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(tr, off, 0, 2));
-        ev[0] = v.x; ev[1] = v.y;
+    const bufrsrc_t pr = make_rsrc(p.prep, pbytes);
+    uint32_t ev[SPW][EC];
+#pragma unroll
+    for (int sp = 0; sp < SPW; ++sp) {
+        // entries of blocks past K read zero (scale 0, zero point 0): their A and B operands
+        // are zero too, and 0 x scale must not meet weight bytes read as a scale
+        const int s = s0 + sp, e0 = wave * BPW * 16 + EC * lane;
+        const uint32_t off = s < NS && e0 / 16 < blocks ? (uint32_t)s * p.strip_bytes + (uint32_t)e0 * 4u : pbytes;
+        if constexpr (EC == 1) {
+            ev[sp][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 2);
+        } else {
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(pr, off, 0, 2));
+            ev[sp][0] = v.x; ev[sp][1] = v.y;
+        }
     }
-    u32x4 av[S][4], wv[BPW];
+    u32x4 av[S][4], wv[SPW][BPW];
     {
         const int slot = col / MP, r = min(col % MP, M - 1);
 #pragma unroll
@@ -458,23 +465,32 @@ gemv_prep_rows_kernel(PrepParams p) {
         }
     }
 #pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-        const uint32_t off = (uint32_t)(wave * BPW + j) * 1024u + (uint32_t)lane * 16u;
-        wv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, 2));
-    }
+    for (int j = 0; j < BPW; ++j)
 #pragma unroll
-    for (int i = 0; i < EC; ++i) tab[EC * lane + i] = ev[i];
+        for (int sp = 0; sp < SPW; ++sp) {
+            const int s = s0 + sp, kb = wave * BPW + j;
+            const uint32_t off = s < NS && kb < blocks
+                                     ? (uint32_t)s * p.strip_bytes + tbytes + (uint32_t)kb * 1024u + (uint32_t)lane * 16u
+                                     : pbytes;
+            wv[sp][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 2));
+        }
+#pragma unroll
+    for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+        for (int i = 0; i < EC; ++i) tab[sp * BPW * 16 + EC * lane + i] = ev[sp][i];
 
-    float y[P][4];
+    float y[SPW][P][4];
 #pragma unroll
-    for (int b = 0; b < P; ++b)
+    for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) y[b][i] = 0.f;
+        for (int b = 0; b < P; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) y[sp][b][i] = 0.f;
 #pragma unroll
     for (int a = 0; a < S; ++a) {
         half8_t A[4];
 #pragma unroll
-        for (int st = 0; st < 4; ++st) {   // x' = x with the rows of the 16 q pairs / 16
+        for (int st = 0; st < 4; ++st) {
             const u32x4 v = av[a][st];
             const half2_t h1 = as_h2(v.y) * (half2_t){(half_t)(1.0f / 16.0f), (half_t)(1.0f / 16.0f)};
             const half2_t h3 = as_h2(v.w) * (half2_t){(half_t)(1.0f / 16.0f), (half_t)(1.0f / 16.0f)};
@@ -483,40 +499,43 @@ gemv_prep_rows_kernel(PrepParams p) {
 #pragma unroll
         for (int b = 0; b < P; ++b) {
             const int j = a * P + b;
-            const uint32_t e = tab[j * 16 + col];
-            const uint32_t z = e >> 16;
-            // -(1024 + z) and -(1024 + 16 z) as fp16 pairs (z <= 31: exact, bit patterns)
-            const uint32_t ze = ((0x6400u + z) * 0x10001u) | 0x80008000u;
-            const uint32_t zo = ((0x6400u + 16u * z) * 0x10001u) | 0x80008000u;
-            float4_t d = {0.f, 0.f, 0.f, 0.f};
-            const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const uint32_t q = wd[st], q8 = q >> 8;
-                const u32x4 bw = {as_u32(nib_pair(q) + as_h2(ze)), as_u32(nib_pair16(q) + as_h2(zo)),
-                                  as_u32(nib_pair(q8) + as_h2(ze)), as_u32(nib_pair16(q8) + as_h2(zo))};
-                d = mfma16x16x32(A[st], __builtin_bit_cast(half8_t, bw), d);
+            for (int sp = 0; sp < SPW; ++sp) {
+                const uint32_t e = tab[sp * BPW * 16 + j * 16 + col];
+                const uint32_t z = e >> 16;
+                const uint32_t ze = ((0x6400u + z) * 0x10001u) | 0x80008000u;
+                const uint32_t zo = ((0x6400u + 16u * z) * 0x10001u) | 0x80008000u;
+                float4_t d = {0.f, 0.f, 0.f, 0.f};
+                const uint32_t wd[4] = {wv[sp][j].x, wv[sp][j].y, wv[sp][j].z, wv[sp][j].w};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const uint32_t q = wd[st], q8 = q >> 8;
+                    const u32x4 bw = {as_u32(nib_pair(q) + as_h2(ze)), as_u32(nib_pair16(q) + as_h2(zo)),
+                                      as_u32(nib_pair(q8) + as_h2(ze)), as_u32(nib_pair16(q8) + as_h2(zo))};
+                    d = mfma16x16x32(A[st], __builtin_bit_cast(half8_t, bw), d);
+                }
+                const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y[sp][b][i] = __builtin_fmaf(sc, d[i], y[sp][b][i]);
             }
-            const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) y[b][i] = __builtin_fmaf(sc, d[i], y[b][i]);
         }
     }
-
-    // ---- reduce over the waves and the slots: row 4 h + i of slot b is output row
-    // 4 h + i - b MP (each slot holds the sums of its own blocks)
 #pragma unroll
-    for (int b = 0; b < P; ++b)
+    for (int sp = 0; sp < SPW; ++sp)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = 4 * h + i - b * MP;
-            if (m >= 0 && m < MP && m < M) red[((wave * P + b) * M + m) * 16 + col] = y[b][i];
-        }
+        for (int b = 0; b < P; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = 4 * h + i - b * MP;
+                if (m >= 0 && m < MP && m < M) red[(((wave * P + b) * SPW + sp) * M + m) * 16 + col] = y[sp][b][i];
+            }
     __syncthreads();
-    for (int o = t; o < M * 16; o += blockDim.x) {
+    for (int o = t; o < SPW * M * 16; o += blockDim.x) {
+        const int sp = o / (M * 16), rem = o - sp * M * 16;
+        if (s0 + sp >= NS) continue;
         float acc = 0.f;
-        for (int wb = 0; wb < W * P; ++wb) acc += red[wb * M * 16 + o];
-        p.out[(size_t)(o >> 4) * p.N + (size_t)s * 16 + (o & 15)] = (half_t)acc;
+        for (int wb = 0; wb < W * P; ++wb) acc += red[(wb * SPW + sp) * M * 16 + rem];
+        p.out[(size_t)(rem >> 4) * p.N + (size_t)(s0 + sp) * 16 + (rem & 15)] = (half_t)acc;
     }
 }
 
@@ -661,12 +680,17 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
         return s;
     const int blocks = K / 128;
     s.mfma = G % 128 == 0;
-    if (M > 1) {   // rows kernel: 8 blocks per wave, up to 16 waves
+    if (M > 1) {   // rows kernel: up to 16 waves
         if (!s.mfma || blocks > 8 * 16) return s;
-        s.bpw = 8;
-        s.waves = (blocks + 7) / 8;
         s.mp = M <= 2 ? 2 : M <= 4 ? 4 : 8;
-        s.lds = (size_t)s.waves * 8 * 16 * 4 + (size_t)s.waves * (16 / s.mp) * M * 16 * 4;
+        // 3..4 rows: 2 strips per workgroup (x read once for both) with 4 blocks per wave where
+        // 16 waves cover K: AWQ 4096 -> 14336 M = 3 / 4 8.73 / 9.52 -> 8.48 / 8.92 us; at 2 rows
+        // and over longer K it measured no better or slower
+        const bool two = s.mp == 4 && blocks <= 4 * 16;
+        s.bpw = two ? 4 : 8;
+        s.spw = two ? 2 : 1;
+        s.waves = (blocks + s.bpw - 1) / s.bpw;
+        s.lds = (size_t)s.waves * s.spw * s.bpw * 16 * 4 + (size_t)s.waves * (16 / s.mp) * s.spw * M * 16 * 4;
         s.ok = true;
         return s;
     }
@@ -758,10 +782,11 @@ static void launch_prep_m1_b(const PrepParams& p, const PrepGemvShape& s, hipStr
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st) {
     (void)hipGetLastError();
     if (p.M > 1) {
-        const dim3 grid(p.N / 16), block(64 * s.waves);
-        if (s.mp == 2) hipLaunchKernelGGL(gemv_prep_rows_kernel<2>, grid, block, s.lds, st, p);
-        else if (s.mp == 4) hipLaunchKernelGGL(gemv_prep_rows_kernel<4>, grid, block, s.lds, st, p);
-        else hipLaunchKernelGGL(gemv_prep_rows_kernel<8>, grid, block, s.lds, st, p);
+        const dim3 grid((p.N / 16 + s.spw - 1) / s.spw), block(64 * s.waves);
+        if (s.mp == 2) hipLaunchKernelGGL((gemv_prep_rows_kernel<2, 8, 1>), grid, block, s.lds, st, p);
+        else if (s.mp == 4 && s.spw == 2) hipLaunchKernelGGL((gemv_prep_rows_kernel<4, 4, 2>), grid, block, s.lds, st, p);
+        else if (s.mp == 4) hipLaunchKernelGGL((gemv_prep_rows_kernel<4, 8, 1>), grid, block, s.lds, st, p);
+        else hipLaunchKernelGGL((gemv_prep_rows_kernel<8, 8, 1>), grid, block, s.lds, st, p);
         return hipGetLastError();
     }
     switch (s.bpw) {
