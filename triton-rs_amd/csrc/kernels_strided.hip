@@ -10,9 +10,17 @@ __global__ void __launch_bounds__(256) strided_gemm_kernel(StridedParams p) {
     strided_gemm_body<FMT, E>(p);
 }
 
+// A gated launch is a fallback that usually exits at once (the act-order route runs it
+// behind the tiled prefill, for a g_idx that route cannot take): launching one workgroup per
+// tile would cost about 4 us of empty workgroups at M = 2048, N = 6144, so it gets at most
+// STR_GATED_GRID workgroups that walk the tiles.
+constexpr int STR_GATED_GRID = 512;
+
 template <typename E>
 static void launch_strided_e(int fmt, const StridedParams& p, hipStream_t st) {
-    const dim3 grid((p.m + STR_BM - 1) / STR_BM, (p.n + STR_BN - 1) / STR_BN), block(256);
+    const int tm = (p.m + STR_BM - 1) / STR_BM, tn = (p.n + STR_BN - 1) / STR_BN;
+    const dim3 grid = p.gate && (int64_t)tm * tn > STR_GATED_GRID ? dim3(STR_GATED_GRID) : dim3(tm, tn);
+    const dim3 block(256);
     if (fmt == FMT_AWQ) hipLaunchKernelGGL((strided_gemm_kernel<FMT_AWQ, E>), grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ) hipLaunchKernelGGL((strided_gemm_kernel<FMT_GPTQ, E>), grid, block, 0, st, p);
     else if (fmt == FMT_GPTQ_SYM) hipLaunchKernelGGL((strided_gemm_kernel<FMT_GPTQ_SYM, E>), grid, block, 0, st, p);
