@@ -231,22 +231,56 @@ def test_prepared_kernels_isa(tmp_path):
         assert "atomic" not in b and "scratch_" not in b and "buffer_store" not in b, n
 
 
-def test_bf16_flag_plans_generic_kernel_and_is_refused_elsewhere():
-    """W4A16_BF16 selects the generic kernel for every shape; entry points without a
-    bfloat16 instantiation report the flagged value as an unknown format (no GPU call)."""
+def test_bf16_flag_plans_and_is_refused_elsewhere():
+    """W4A16_BF16 plans the small-batch kernel up to 64 rows and the pipelined prefill beyond
+    (plain group order, the shapes they take), the generic kernel for act-order and other
+    shapes; entry points without a bfloat16 instantiation report the flagged value as an
+    unknown format (no GPU call)."""
     P = pkg()
     L = P.lib()
     k = ctypes.c_int(0)
-    for M, N, K in ((1, 14336, 4096), (16, 6144, 4096), (2048, 4096, 14336)):
-        assert L.w4a16_gemm_plan(P.FMT_AWQ | P.BF16, M, N, K, 128, 0, ctypes.byref(k)) == P.OK
-        assert P.KERNELS[k.value] == "strided"
-        assert L.w4a16_gemm_plan(P.FMT_AWQ, M, N, K, 128, 0, ctypes.byref(k)) == P.OK
-        assert P.KERNELS[k.value] != "strided"
+
+    def plan(fmt, M, N, K, gidx=0):
+        assert L.w4a16_gemm_plan(fmt, M, N, K, 128, gidx, ctypes.byref(k)) == P.OK
+        return P.KERNELS[k.value]
+    for M, N, K, want in ((1, 14336, 4096, "skinny"), (8, 4096, 14336, "skinny"),
+                          (16, 6144, 4096, "skinny"), (64, 6144, 4096, "skinny"),
+                          (65, 6144, 4096, "prefill"), (2048, 4096, 14336, "prefill"),
+                          (33, 136, 384, "strided")):
+        assert plan(P.FMT_AWQ | P.BF16, M, N, K) == want, (M, N, K)
+        assert plan(P.FMT_GPTQ | P.BF16, M, N, K) == want, (M, N, K)
+    assert plan(P.FMT_GPTQ | P.BF16, 16, 6144, 4096, gidx=1) == "strided"
+    assert plan(P.FMT_GPTQ | P.BF16, 2048, 6144, 4096, gidx=1) == "strided"
+    assert plan(P.FMT_AWQ, 1, 14336, 4096) == "gemv"
     assert L.w4a16_gemm_plan(P.FMT_AWQ | 0x200, 1, 512, 512, 128, 0, ctypes.byref(k)) == \
         P.ERR_INVALID_ARG
     assert L.w4a16_prepare_act_order(None, P.FMT_GPTQ | P.BF16, None, None, 1024, 256, 128,
                                      None, None) == P.ERR_INVALID_ARG
     assert "fmt" in L.w4a16_last_error().decode()
+
+
+def test_bf16_fast_kernels_isa(tmp_path):
+    """The bfloat16 instances of the small-batch and prefill kernels run bf16 MFMA on weights
+    rounded with v_cvt_pk_bf16_f32 (from v_cvt_f32_ubyte nibble conversions), and none spills;
+    their fp16 twins have neither."""
+    bdir = os.path.join(ROOT, "triton-rs_amd", "_build")
+    objs = [os.path.join(bdir, f) for f in ("kernels_skinny.o", "kernels_prefill.o")]
+    if not all(os.path.exists(o) for o in objs):
+        pytest.skip("build objects not present (run build first)")
+    seen = 0
+    for o, name in zip(objs, ("skinny_kernel", "prefill_dma_kernel")):
+        ks = {n: b for n, b in _disassemble_tu(o, tmp_path).items() if name in n}
+        bf = {n: b for n, b in ks.items() if "DF16b" in n}
+        assert len(bf) >= (48 if name == "skinny_kernel" else 18), (name, len(bf))
+        for n, b in bf.items():
+            assert "v_mfma_f32_16x16x32_bf16" in b and "v_mfma_f32_16x16x32_f16" not in b, n
+            assert "v_cvt_pk_bf16_f32" in b and "v_cvt_f32_ubyte" in b, n
+            assert "scratch_" not in b, n
+            seen += 1
+        for n, b in ks.items():
+            if "DF16b" not in n:
+                assert "v_mfma_f32_16x16x32_bf16" not in b and "v_cvt_pk_bf16_f32" not in b, n
+    assert seen >= 66
 
 
 def test_moe_argument_errors():

@@ -1,8 +1,9 @@
 """GPU parity of the bfloat16 instantiation (W4A16_BF16 flag): dequantised weights bit-exact
 against the oracle, GEMM outputs within the path's 1e-2 bar of the oracle's float64
-accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32.
-The reference kernels are generic over the element type and name bf16
-(w4a16_gptq_gemm_typed.rs:65-67)."""
+accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32,
+on each kernel bf16 runs (small-batch up to 64 rows, pipelined prefill beyond, the generic
+kernel for act-order and other shapes). The reference kernels are generic over the element
+type and name bf16 (w4a16_gptq_gemm_typed.rs:65-67)."""
 import numpy as np
 import pytest
 
@@ -64,13 +65,14 @@ def test_dequant_bf16_act_order_bit_exact(torch_cuda, orc):
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
-@pytest.mark.parametrize("M,K,N", [(1, 1024, 512), (7, 512, 256), (64, 2048, 768),
-                                   (200, 1024, 512), (33, 384, 136)])
-def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N):
+@pytest.mark.parametrize("M,K,N,kernel", [(1, 1024, 512, "skinny"), (7, 512, 256, "skinny"),
+                                          (64, 2048, 768, "skinny"), (200, 1024, 512, "prefill"),
+                                          (33, 384, 136, "strided")])
+def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N, kernel):
     torch = torch_cuda
     P = pkg()
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=720 + M + fmt)
-    assert P.plan(FMT_NAME[fmt], M, N, K, p.G, bf16=True) == "strided"
+    assert P.plan(FMT_NAME[fmt], M, N, K, p.G, bf16=True) == kernel
     x_bits = bf16_bits(torch, p.x.astype(np.float32))
     s_bits = bf16_bits(torch, p.scales.astype(np.float32))
     y = P.gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
@@ -79,6 +81,41 @@ def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N):
     assert y.dtype == torch.bfloat16
     _, ref = orc.w4a16_gemm_bf16(fmt, x_bits, p.qweight, s_bits, p.qzeros, K, N, p.G)
     assert_parity(y.float().cpu().numpy(), ref, what=f"bf16 fmt={fmt} M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N,kernel", [
+    (AWQ, 1, 4096, 14336, "skinny"),      # config 1's shapes in bf16
+    (AWQ, 8, 14336, 4096, "skinny"),
+    (GPTQ, 16, 4096, 6144, "skinny"),     # config 2's shape, plain group order
+    (GPTQ, 64, 4096, 6144, "skinny"),
+    (SYM, 256, 8192, 1024, "prefill"),    # prefill with its K split across workgroups
+    (AWQ, 2048, 4096, 14336, "prefill"),  # config 3
+])
+def test_gemm_bf16_fast_paths_full_size(torch_cuda, orc, fmt, M, K, N, kernel):
+    """The bf16 small-batch and prefill kernels at the benchmark shapes: every row up to 16
+    rows, else 16 sampled rows (the first and last among them), against the oracle's bf16
+    GEMM; a second call is bit-identical (fixed-order split-K sums)."""
+    torch = torch_cuda
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=0xBF160000 + M + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, p.G, bf16=True) == kernel
+    x_bits = bf16_bits(torch, p.x.astype(np.float32))
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    args = (bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
+            None if p.qzeros is None else to_dev(p.qzeros))
+    y = P.gemm(*args, fmt=FMT_NAME[fmt], group_size=p.G)
+    y2 = P.gemm(*args, fmt=FMT_NAME[fmt], group_size=p.G)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev_bits(y), dev_bits(y2))
+    if M <= 16:
+        rows = np.arange(M)
+    else:
+        rows = np.random.default_rng(M).choice(M, 16, replace=False)
+        rows[:2] = [0, M - 1]
+    _, ref = orc.w4a16_gemm_bf16(fmt, x_bits[rows], p.qweight, s_bits, p.qzeros, K, N, p.G)
+    got = y.float().cpu().numpy()[rows]
+    assert np.all(np.isfinite(got))
+    assert_parity(got, ref, what=f"bf16 {kernel} fmt={fmt} M={M} K={K} N={N}")
 
 
 def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
@@ -95,11 +132,14 @@ def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
-def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt):
+@pytest.mark.parametrize("M,K,N,G", [(9, 256, 128, 64), (1, 4096, 512, 128), (40, 4096, 768, 128),
+                                     (256, 8192, 1024, 128)])
+def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt, M, K, N, G):
     """x in multiples of 1/2 up to 2, scales 2^-7: every product and partial sum is exact in
-    fp32, so the output is the exact sum rounded once to bf16, identical to the oracle."""
+    fp32, so the output is the exact sum rounded once to bf16, identical to the oracle, on
+    the small-batch kernel (with and without a K split across workgroups) and the prefill
+    kernel (256 rows: K split in 4)."""
     torch = torch_cuda
-    M, K, N, G = 9, 256, 128, 64
     g = np.random.default_rng(740 + fmt)
     q = g.integers(0, 16, size=(K, N), dtype=np.int32)
     zq = g.integers(0, 16, size=(K // G, N), dtype=np.int32)

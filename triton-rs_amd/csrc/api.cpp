@@ -206,6 +206,17 @@ static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DE
     return W4A16_KERNEL_STRIDED;
 }
 
+// bfloat16 elements (W4A16_BF16): the small-batch kernel up to 64 rows and the pipelined
+// prefill beyond, both in plain group order on the checkpoint layouts; act-order and the
+// shapes those kernels reject run the generic kernel.
+static int plan_bf16(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
+    if (has_gidx) return W4A16_KERNEL_STRIDED;
+    const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);
+    if (M <= 64 && sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
+    const PrefillShape ps = prefill_shape(fmt, M, N, K, G, cus);
+    return ps.ok && ps.dma ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
+}
+
 }  // namespace w4a16
 
 using namespace w4a16;
@@ -246,7 +257,7 @@ W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t 
     int rc = check_gemm_args(fmt, (void*)1, (void*)1, (void*)1, (void*)1, (void*)1, M, N, K, G);
     if (rc) return rc;
     if (!kernel) return fail(W4A16_ERR_INVALID_ARG, "kernel out-pointer is null");
-    *kernel = bf16 ? W4A16_KERNEL_STRIDED : plan(fmt, M, N, K, G, has_g_idx != 0);
+    *kernel = bf16 ? plan_bf16(fmt, M, N, K, G, has_g_idx != 0) : plan(fmt, M, N, K, G, has_g_idx != 0);
     return W4A16_OK;
 }
 
@@ -281,8 +292,9 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
                         aligned(out, 16) && (!qzeros || aligned(qzeros, 16)) &&
                         (!g_idx || aligned(g_idx, 16));
     const int cus = device_cus();
-    int kernel = plan(fmt, M, N, K, G, g_idx != nullptr, cus);
-    if (!vec_ok || bf16) kernel = W4A16_KERNEL_STRIDED;   // bf16: the generic kernel only
+    int kernel = bf16 ? plan_bf16(fmt, M, N, K, G, g_idx != nullptr, cus)
+                      : plan(fmt, M, N, K, G, g_idx != nullptr, cus);
+    if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
     if (g_idx && kernel == W4A16_KERNEL_PREFILL && !src.may_allocate) kernel = W4A16_KERNEL_STRIDED;
     // the placement probe allocates: sources that must not allocate use what is cached
     const bool xcd = src.may_probe ? xcd_placement(st) : xcd_placement_cached();
@@ -302,16 +314,19 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     auto scratch_fits = [&](size_t tiles, size_t partial_bytes) {
         return tiles <= src.max_tiles && partial_bytes <= src.max_partial_bytes;
     };
+    auto unsplit_prefill_ok = [&]() {   // bf16 runs the pipelined prefill only
+        const PrefillShape q = prefill_shape(fmt, M, N, K, G, cus, 1);
+        return q.ok && (!bf16 || q.dma);
+    };
     if (kernel == W4A16_KERNEL_SKINNY) {
         const SkinnyShape s = skinny_shape(fmt, M, N, K, G, cus, g_idx != nullptr, xcd);
         if (s.splits > 1 && !scratch_fits((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float)))
             kernel = g_idx ? W4A16_KERNEL_STRIDED
-                           : prefill_shape(fmt, M, N, K, G, cus, 1).ok ? W4A16_KERNEL_PREFILL
-                                                                       : W4A16_KERNEL_STRIDED;
+                           : unsplit_prefill_ok() ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     } else if (kernel == W4A16_KERNEL_GEMV) {
         const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd);
         if (s.splits > 1 && !scratch_fits((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float)))
-            kernel = prefill_shape(fmt, M, N, K, G, cus, 1).ok ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
+            kernel = unsplit_prefill_ok() ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     }
 
     if (kernel == W4A16_KERNEL_SKINNY) {
@@ -332,7 +347,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
             p.flags = sc.counters;
             p.ws = sc.partials;
         }
-        hipError_t e = launch_skinny(fmt, p, s, st);
+        hipError_t e = launch_skinny(fmt, p, s, st, bf16);
         if (e != hipSuccess) return hip_fail(e, "skinny launch");
         return W4A16_OK;
     }
@@ -361,7 +376,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
             p.counters = sc.counters;
             p.ws = sc.partials;
         }
-        hipError_t e = launch_prefill(fmt, p, s, st);
+        hipError_t e = launch_prefill(fmt, p, s, st, bf16);
         return e == hipSuccess ? W4A16_OK : hip_fail(e, "prefill launch");
     };
     if (kernel == W4A16_KERNEL_PREFILL && !g_idx) return run_prefill(x, qweight, nullptr);

@@ -18,6 +18,7 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float float16_t __attribute__((ext_vector_type(16)));
 
@@ -101,6 +102,27 @@ __device__ __forceinline__ half_t dequant1(int q, int z, half_t s) {
 __device__ __forceinline__ bf16_t dequant1(int q, int z, bf16_t s) {
     return (bf16_t)((float)(q - z) * (float)s);
 }
+
+// Two fp32 values as a packed element pair (low half first), each rounded to nearest even.
+__device__ __forceinline__ uint32_t pack2(half_t, float a, float b) {
+    return as_u32(half2_t{(half_t)a, (half_t)b});
+}
+__device__ __forceinline__ uint32_t pack2(bf16_t, float a, float b) {
+    return __builtin_bit_cast(uint32_t, bf16x2_t{(bf16_t)a, (bf16_t)b});
+}
+
+// The bf16 pair RNE_bf16((q - z) * s) for the nibbles at bits 0 and 16 of v, given s and
+// nzs = -z * s in fp32. q * s and z * s are exact in fp32 (a 5-bit integer times an 8-bit
+// significand), so the fma returns (q - z) * s exactly and the pack rounds once: the same
+// bits as dequant1 above. The byte conversions are v_cvt_f32_ubyte0 / ubyte2.
+__device__ __forceinline__ uint32_t deq2_bf16(uint32_t v, float s, float nzs) {
+    const uint32_t x = v & 0x000F000Fu;
+    return pack2(bf16_t{}, __builtin_fmaf((float)(x & 0xFFu), s, nzs),
+                 __builtin_fmaf((float)(x >> 16), s, nzs));
+}
+
+// bf16 bits (low 16 bits of b) as fp32: exact
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
 // v_mfma_f32_16x16x32 for either element type
 __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {

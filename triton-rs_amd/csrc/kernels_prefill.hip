@@ -313,8 +313,13 @@ size_t prefill_dma_lds(int bm, int bn) {
 
 constexpr int PF_THREADS = 512;   // 8 waves: 4 along M x 2 along N
 
-template <int FMT, int BM, int BN, bool MOE>
+// E: the element type of x, the scales and the output. With bf16 (dense checkpoint layouts)
+// a weight is RNE_bf16((q - z) * s) (deq2_bf16) and the MFMA is the bf16 one.
+template <int FMT, int BM, int BN, bool MOE, typename E = half_t>
 __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p) {
+    constexpr bool BF = std::is_same<E, bf16_t>::value;
+    typedef typename vec8<E>::type v8_t;
+    static_assert(!BF || (!MOE && FMT != FMT_PREP), "bf16: dense checkpoint layouts");
     if (p.gate && *p.gate != p.gate_want) return;   // uniform: the whole grid returns
     constexpr int WGM = 4, WGN = 2, NWV = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;     // wave tile
@@ -520,6 +525,30 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
                          deq2(nib_pair(w >> 8), hz, hs), deq2(nib_pair(w >> 12), hz, hs));
         }
         const uint32_t sw = DQC == 4 ? d.sv[c >> 1] : d.sv[0];
+        if constexpr (BF) {
+            // the same words and pairs as below, each pair RNE_bf16((q - z) * s)
+            const float sf = bf16_bits_to_f32((c & 1) ? sw >> 16 : sw & 0xFFFFu);
+            if constexpr (FMT == FMT_AWQ) {
+                const int slot = awq_slot(cc);
+                const float nzs = -(float)nib(d.zw, slot) * sf;
+                uint32_t pr[4];
+#pragma unroll
+                for (int rp = 0; rp < 4; ++rp) {
+                    const uint32_t a = d.w[2 * rp], b = d.w[2 * rp + 1];
+                    const uint32_t pp = perm(b, a, (slot & 4) ? 0x07060302u : 0x05040100u);
+                    pr[rp] = deq2_bf16(pp >> (4 * (slot & 3)), sf, nzs);
+                }
+                return u32x4{pr[0], pr[1], pr[2], pr[3]};
+            } else {
+                const int z = FMT == FMT_GPTQ_SYM ? 8 : nib(d.zw, cc) + p.zero_offset;
+                const float nzs = -(float)z * sf;
+                const uint32_t w = d.w[c];
+                const uint32_t q0 = deq2_bf16(w, sf, nzs), q1 = deq2_bf16(w >> 4, sf, nzs);
+                const uint32_t q2 = deq2_bf16(w >> 8, sf, nzs), q3 = deq2_bf16(w >> 12, sf, nzs);
+                return u32x4{perm(q1, q0, 0x05040100u), perm(q3, q2, 0x05040100u),
+                             perm(q1, q0, 0x07060302u), perm(q3, q2, 0x07060302u)};
+            }
+        }
         const half2_t hs = as_h2(perm(sw, sw, (c & 1) ? 0x07060706u : 0x05040504u));
         if constexpr (FMT == FMT_AWQ) {
             const int slot = awq_slot(cc);
@@ -599,18 +628,17 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const int kc = 4 * ks + kb;
-            half8_t af[RV > 0 ? RV : 1], bf[CB];
+            v8_t af[RV > 0 ? RV : 1], bf[CB];
 #pragma unroll
             for (int r = 0; r < RV; ++r)
-                af[r] = *reinterpret_cast<const half8_t*>(A + RSTEP * r * BK + 8 * (kc ^ (j & 7)));
+                af[r] = *reinterpret_cast<const v8_t*>(A + RSTEP * r * BK + 8 * (kc ^ (j & 7)));
 #pragma unroll
             for (int c = 0; c < CB; ++c)
-                if (RV > 0) bf[c] = *reinterpret_cast<const half8_t*>(B + boff[c] + ks * 4 * 256 * 8);
+                if (RV > 0) bf[c] = *reinterpret_cast<const v8_t*>(B + boff[c] + ks * 4 * 256 * 8);
 #pragma unroll
             for (int r = 0; r < RV; ++r)
 #pragma unroll
-                for (int c = 0; c < CB; ++c)
-                    acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[r], bf[c], acc[r][c], 0, 0, 0);
+                for (int c = 0; c < CB; ++c) acc[r][c] = mfma16x16x32(af[r], bf[c], acc[r][c]);
 #pragma unroll
             for (int c = ks * DQC / 2; c < (ks + 1) * DQC / 2; ++c) col[c] = dq_col(d, c);
             // place the dequantisation arithmetic between the MFMAs: 1 MFMA, 2 VALU
@@ -692,8 +720,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
             const size_t off = (size_t)m * p.N + n0 + c;
             float4_t v = ld_partial4<SCOPE_DEVICE>(p.ws + off);
             for (int sp = 1; sp < ksp; ++sp) v += ld_partial4<SCOPE_DEVICE>(p.ws + sp * MN + off);
-            const half2_t lo = {(half_t)v.x, (half_t)v.y}, hi = {(half_t)v.z, (half_t)v.w};
-            *reinterpret_cast<u32x2*>(p.out + off) = u32x2{as_u32(lo), as_u32(hi)};
+            *reinterpret_cast<u32x2*>(p.out + off) = u32x2{pack2(E{}, v.x, v.y), pack2(E{}, v.z, v.w)};
         }
         return;
     }
@@ -703,9 +730,9 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         for (int i = 0; i < 4; ++i) {
             const int m = dst_row(row0 + RSTEP * r + 4 * kb + i);
             if (m < 0) continue;
-            half_t* dst = p.out + (size_t)m * p.N + n0 + wn * WN + j;
+            E* dst = reinterpret_cast<E*>(p.out) + (size_t)m * p.N + n0 + wn * WN + j;
 #pragma unroll
-            for (int c = 0; c < CB; ++c) dst[16 * c] = (half_t)acc[r][c][i];
+            for (int c = 0; c < CB; ++c) dst[16 * c] = (E)acc[r][c][i];
         }
 }
 
@@ -790,13 +817,13 @@ static void allow_lds(F* kernel, size_t lds) {
 
 // The dynamic-LDS allowance is set on every launch (a host-side attribute, cheap beside these
 // kernels): once per process would miss other devices and race between host threads.
-template <int FMT, int BM, int BN2, bool MOE>
+template <int FMT, int BM, int BN2, bool MOE, typename E = half_t>
 static void launch_dma_t(const PrefillParams& p, dim3 grid, size_t lds, hipStream_t st) {
-    allow_lds(&prefill_dma_kernel<FMT, BM, BN2, MOE>, prefill_dma_lds(BM, BN2));
-    hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, MOE>), grid, dim3(PF_THREADS), lds, st, p);
+    allow_lds(&prefill_dma_kernel<FMT, BM, BN2, MOE, E>, prefill_dma_lds(BM, BN2));
+    hipLaunchKernelGGL((prefill_dma_kernel<FMT, BM, BN2, MOE, E>), grid, dim3(PF_THREADS), lds, st, p);
 }
 
-template <int FMT, bool MOE>
+template <int FMT, bool MOE, typename E = half_t>
 static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, size_t lds,
                            hipStream_t st) {
     if constexpr (MOE) {
@@ -811,12 +838,12 @@ static void launch_dma_fmt(const PrefillParams& p, int bm, int bn, dim3 grid, si
         else if (bn == 128) launch_dma_t<FMT, 256, 128, true>(p, grid, lds, st);
         else launch_dma_t<FMT, 256, 256, true>(p, grid, lds, st);
     } else {
-        if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false>(p, grid, lds, st);
-        else if (bm == 256 && bn == 192) launch_dma_t<FMT, 256, 192, false>(p, grid, lds, st);
-        else if (bm == 256 && bn == 128) launch_dma_t<FMT, 256, 128, false>(p, grid, lds, st);
-        else if (bm == 256) launch_dma_t<FMT, 256, 256, false>(p, grid, lds, st);
-        else if (bn == 224) launch_dma_t<FMT, 128, 224, false>(p, grid, lds, st);
-        else launch_dma_t<FMT, 128, 256, false>(p, grid, lds, st);
+        if (bm == 256 && bn == 224) launch_dma_t<FMT, 256, 224, false, E>(p, grid, lds, st);
+        else if (bm == 256 && bn == 192) launch_dma_t<FMT, 256, 192, false, E>(p, grid, lds, st);
+        else if (bm == 256 && bn == 128) launch_dma_t<FMT, 256, 128, false, E>(p, grid, lds, st);
+        else if (bm == 256) launch_dma_t<FMT, 256, 256, false, E>(p, grid, lds, st);
+        else if (bn == 224) launch_dma_t<FMT, 128, 224, false, E>(p, grid, lds, st);
+        else launch_dma_t<FMT, 128, 256, false, E>(p, grid, lds, st);
     }
 }
 
@@ -862,7 +889,18 @@ static hipError_t launch_any(int fmt, const PrefillParams& p, int bm, dim3 grid,
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st) {
+hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st,
+                          bool bf16) {
+    if (bf16) {   // the pipelined kernel on the dense checkpoint layouts only
+        (void)hipGetLastError();
+        if (!s.dma) return hipErrorInvalidValue;
+        const dim3 grid(s.col_tiles, s.row_tiles, s.ksplit);
+        if (fmt == FMT_AWQ) launch_dma_fmt<FMT_AWQ, false, bf16_t>(p, s.bm, s.bn, grid, s.lds, st);
+        else if (fmt == FMT_GPTQ) launch_dma_fmt<FMT_GPTQ, false, bf16_t>(p, s.bm, s.bn, grid, s.lds, st);
+        else if (fmt == FMT_GPTQ_SYM) launch_dma_fmt<FMT_GPTQ_SYM, false, bf16_t>(p, s.bm, s.bn, grid, s.lds, st);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     if (s.dma)
         return launch_dma_any<false>(fmt, p, s.bm, s.bn, dim3(s.col_tiles, s.row_tiles, s.ksplit),
                                      s.lds, st);

@@ -27,6 +27,8 @@
 // load per thread instead of two 32-byte loads per lane and k32 step, which the 16 lanes of
 // a k block all repeat, and no index arithmetic in the steps);
 // GIDX = 1 (slice too large for the LDS budget) reads g_idx per step from global memory.
+#include <type_traits>
+
 #include "device_common.h"
 #include "launch.h"
 #include "splitk.h"
@@ -55,8 +57,15 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 // and the zero points and scales are splatted once per round instead of once per step.
 // WV: waves per workgroup when it differs from skinny_waves (8 for 64-row GPTQ tiles, chosen
 // on the host where K allows); 0 for the default.
-template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false, int WV = 0>
+// E: the element type of x, the scales and the output. With bf16 a weight is
+// RNE_bf16((q - z) * s) (deq2_bf16: exact fp32 product, one rounding) and the MFMA is the
+// bf16 one; act-order stays fp16 (its table holds fp16 zero points).
+template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false, int WV = 0,
+          typename E = half_t>
 __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) skinny_kernel(SkinnyParams p) {
+    constexpr bool BF = std::is_same<E, bf16_t>::value;
+    typedef typename vec8<E>::type v8_t;
+    static_assert(!BF || !GIDX, "bf16: plain group order");
     static_assert(!RG || !GIDX, "one group per round needs plain group order");
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
@@ -255,9 +264,16 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
         __syncthreads();
     }
 
-    // zero point (as fp16 1024 + z) and scale per column, splatted; with RG they are set by
-    // the first step of a round and kept for the others
+    // zero point (as fp16 1024 + z) and scale per column, splatted (bf16: the scale and
+    // -z * s in fp32); with RG they are set by the first step of a round and kept for the
+    // others
     half2_t hz[CPL], hs[CPL];
+    float fs[CPL], fnz[CPL];
+    // the element pair of the nibbles at bits 0 and 16 of v, dequantised for column c
+    auto dq = [&](uint32_t v, int c) __attribute__((always_inline)) -> uint32_t {
+        if constexpr (BF) return deq2_bf16(v, fs[c], fnz[c]);
+        else return as_u32(deq2(nib_pair(v), hz[c], hs[c]));
+    };
 
     // one k32 step from ring slot u
     auto compute = [&](int u) __attribute__((always_inline)) {
@@ -268,16 +284,22 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
             if constexpr (FMT == FMT_GPTQ_SYM) z = 8;
             else if constexpr (FMT == FMT_AWQ) z = nib(zreg[u], awq_slot(cw));
             else z = nib(zreg[u], cw) + p.zero_offset;
-            const half_t zh = (half_t)(1024 + z);
-            hz[c] = half2_t{zh, zh};
-            const half2_t sv = as_h2(sreg[u][c >> 1]);
-            const half_t sc = (c & 1) ? sv.y : sv.x;
-            hs[c] = half2_t{sc, sc};
+            if constexpr (BF) {
+                const uint32_t sw = sreg[u][c >> 1];
+                fs[c] = bf16_bits_to_f32((c & 1) ? sw >> 16 : sw & 0xFFFFu);
+                fnz[c] = -(float)z * fs[c];
+            } else {
+                const half_t zh = (half_t)(1024 + z);
+                hz[c] = half2_t{zh, zh};
+                const half2_t sv = as_h2(sreg[u][c >> 1]);
+                const half_t sc = (c & 1) ? sv.y : sv.x;
+                hs[c] = half2_t{sc, sc};
+            }
         }
         // dequantise B fragments
-        half8_t bf[CPL];
+        v8_t bf[CPL];
         if constexpr (FMT == FMT_AWQ) {
-            half2_t pr[4][CPL];
+            uint32_t pr[4][CPL];
 #pragma unroll
             for (int rp = 0; rp < 4; ++rp) {
                 const uint32_t a = bw[u][2 * rp], b = bw[u][2 * rp + 1];
@@ -289,20 +311,20 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
                     for (int sl = 0; sl < 8; ++sl) {
                         const uint32_t src = sl < 4 ? p0 : p1;
                         const int col = awq_col_of_slot(sl);
-                        pr[rp][col] = deq2(nib_pair(src >> (4 * (sl & 3))), hz[col], hs[col]);
+                        pr[rp][col] = dq(src >> (4 * (sl & 3)), col);
                     }
                 } else {
                     // columns 4h..4h+3 of the word: slots 2h, 4+2h, 2h+1, 5+2h
                     const int sh = 8 * (j & 1);
                     const uint32_t q0 = p0 >> sh, q1 = p1 >> sh;
-                    pr[rp][0] = deq2(nib_pair(q0), hz[0], hs[0]);
-                    pr[rp][1] = deq2(nib_pair(q1), hz[1], hs[1]);
-                    pr[rp][2] = deq2(nib_pair(q0 >> 4), hz[2], hs[2]);
-                    pr[rp][3] = deq2(nib_pair(q1 >> 4), hz[3], hs[3]);
+                    pr[rp][0] = dq(q0, 0);
+                    pr[rp][1] = dq(q1, 1);
+                    pr[rp][2] = dq(q0 >> 4, 2);
+                    pr[rp][3] = dq(q1 >> 4, 3);
                 }
             }
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) bf[c] = cat8(pr[0][c], pr[1][c], pr[2][c], pr[3][c]);
+            for (int c = 0; c < CPL; ++c) bf[c] = __builtin_bit_cast(v8_t, u32x4{pr[0][c], pr[1][c], pr[2][c], pr[3][c]});
         } else if constexpr (GIDX != 0) {
             // entries of rows k0..k7 for the lane's columns; a g_idx outside the table
             // is clamped into [0, groups - 1], as in the generic kernel
@@ -351,8 +373,7 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 const uint32_t w = bw[u][c];
-                bf[c] = cat8(deq2(nib_pair(w), hz[c], hs[c]), deq2(nib_pair(w >> 4), hz[c], hs[c]),
-                             deq2(nib_pair(w >> 8), hz[c], hs[c]), deq2(nib_pair(w >> 12), hz[c], hs[c]));
+                bf[c] = __builtin_bit_cast(v8_t, u32x4{dq(w, c), dq(w >> 4, c), dq(w >> 8, c), dq(w >> 12, c)});
             }
         }
         // MFMAs
@@ -363,10 +384,9 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
             if constexpr (FMT != FMT_AWQ)   // k order (0,4)(1,5)(2,6)(3,7) as in the GPTQ unpack
                 a = u32x4{perm(a.z, a.x, 0x05040100u), perm(a.z, a.x, 0x07060302u),
                           perm(a.w, a.y, 0x05040100u), perm(a.w, a.y, 0x07060302u)};
-            const half8_t af = __builtin_bit_cast(half8_t, a);
+            const v8_t af = __builtin_bit_cast(v8_t, a);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c)
-                acc[r][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[c], acc[r][c], 0, 0, 0);
+            for (int c = 0; c < CPL; ++c) acc[r][c] = mfma16x16x32(af, bf[c], acc[r][c]);
         }
     };
 
@@ -432,12 +452,12 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
 #pragma unroll
         for (int w = 1; w < RW; ++w) v += red[w][m][col];
         const size_t off = (size_t)m * p.N + n0 + col;
-        if (p.splits == 1) p.out[off] = (half_t)v;
+        if (p.splits == 1) reinterpret_cast<E*>(p.out)[off] = (E)v;
         else st_partial<SC>(p.ws + (size_t)split * p.M * p.N + off, v);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.flags, ct), p.splits, &flag))
-        splitk_finish_rows<SC>(p.ws, p.out, p.splits, p.M, p.N, 0, p.M, n0, WN);
+        splitk_finish_rows<SC, E>(p.ws, reinterpret_cast<E*>(p.out), p.splits, p.M, p.N, 0, p.M, n0, WN);
 }
 
 // ------------------------------------------------------------------ host side
@@ -515,13 +535,14 @@ SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool 
     return s;
 }
 
-template <int FMT, int BM, int CPL, bool XCD, int WV>
+template <int FMT, int BM, int CPL, bool XCD, int WV, typename E>
 static hipError_t launch_xw(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     // 8-wave 64-row tiles keep a 2-step ring: two waves per SIMD need <= 256 registers
     constexpr int PF = FMT == FMT_AWQ ? 3 : WV == 8 ? 2 : 4;
     constexpr int NTH = 64 * (WV ? WV : skinny_waves(FMT, BM, CPL));
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
-    if constexpr (FMT != FMT_AWQ) {
+    if (p.g_idx && !std::is_same<E, half_t>::value) return hipErrorInvalidValue;   // fp16 only
+    if constexpr (FMT != FMT_AWQ && std::is_same<E, half_t>::value) {
         if (p.g_idx) {
             // act-order waves with exactly one ring of steps run without a loop: the loop's
             // ring copies raise the kernel to 186 VGPRs, two waves per SIMD instead of three
@@ -546,56 +567,61 @@ static hipError_t launch_xw(const SkinnyParams& p, const SkinnyShape& s, hipStre
         // one group per ring round (RG): the wave's rounds start on multiples of 32 PF rows
         const bool rg = p.G % (32 * PF) == 0 && s.steps_per_wave % PF == 0;
         if (s.steps_per_wave == PF) {   // as above: M=16, 4096 -> 6144 9.4 -> 8.6 us
-            if (rg) hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, true, WV>), grid, dim3(NTH), 0, st, p);
-            else hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, false, WV>), grid, dim3(NTH), 0, st, p);
+            if (rg) hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, true, WV, E>), grid, dim3(NTH), 0, st, p);
+            else hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, PF, false, WV, E>), grid, dim3(NTH), 0, st, p);
             return hipGetLastError();
         }
         if (rg) {
-            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, true, WV>), grid, dim3(NTH), 0, st, p);
+            hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, true, WV, E>), grid, dim3(NTH), 0, st, p);
             return hipGetLastError();
         }
     }
-    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, false, WV>), grid, dim3(NTH), 0, st, p);
+    hipLaunchKernelGGL((skinny_kernel<FMT, BM, CPL, PF, 0, XCD, 0, false, WV, E>), grid, dim3(NTH), 0, st, p);
     return hipGetLastError();
 }
 
-template <int FMT, int BM, int CPL, bool XCD>
+template <int FMT, int BM, int CPL, bool XCD, typename E>
 static hipError_t launch_x(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (BM == 64 && FMT != FMT_AWQ && CPL < 8) {
-        if (s.waves == 8) return launch_xw<FMT, BM, CPL, XCD, 8>(p, s, st);
+        if (s.waves == 8) return launch_xw<FMT, BM, CPL, XCD, 8, E>(p, s, st);
     }
-    return launch_xw<FMT, BM, CPL, XCD, 0>(p, s, st);
+    return launch_xw<FMT, BM, CPL, XCD, 0, E>(p, s, st);
 }
 
-template <int FMT, int BM, int CPL>
+template <int FMT, int BM, int CPL, typename E>
 static hipError_t launch_t(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
-    return s.xcd ? launch_x<FMT, BM, CPL, true>(p, s, st) : launch_x<FMT, BM, CPL, false>(p, s, st);
+    return s.xcd ? launch_x<FMT, BM, CPL, true, E>(p, s, st) : launch_x<FMT, BM, CPL, false, E>(p, s, st);
 }
 
-template <int FMT, int BM>
+template <int FMT, int BM, typename E>
 static hipError_t launch_bm(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     if constexpr (FMT != FMT_AWQ) {
-        if (s.cpl == 2) return launch_t<FMT, BM, 2>(p, s, st);
+        if (s.cpl == 2) return launch_t<FMT, BM, 2, E>(p, s, st);
     } else {
-        if (s.cpl == 8) return launch_t<FMT, BM, 8>(p, s, st);
+        if (s.cpl == 8) return launch_t<FMT, BM, 8, E>(p, s, st);
     }
-    return launch_t<FMT, BM, 4>(p, s, st);
+    return launch_t<FMT, BM, 4, E>(p, s, st);
 }
 
-template <int FMT>
+template <int FMT, typename E>
 static hipError_t launch_fmt(const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
     switch (s.bm) {
-        case 16: return launch_bm<FMT, 16>(p, s, st);
-        case 32: return launch_bm<FMT, 32>(p, s, st);
-        default: return launch_bm<FMT, 64>(p, s, st);
+        case 16: return launch_bm<FMT, 16, E>(p, s, st);
+        case 32: return launch_bm<FMT, 32, E>(p, s, st);
+        default: return launch_bm<FMT, 64, E>(p, s, st);
     }
 }
 
-hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+template <typename E>
+static hipError_t launch_e(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st) {
+    if (fmt == FMT_AWQ) return launch_fmt<FMT_AWQ, E>(p, s, st);
+    if (fmt == FMT_GPTQ) return launch_fmt<FMT_GPTQ, E>(p, s, st);
+    return launch_fmt<FMT_GPTQ_SYM, E>(p, s, st);
+}
+
+hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st, bool bf16) {
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
-    if (fmt == FMT_AWQ) return launch_fmt<FMT_AWQ>(p, s, st);
-    if (fmt == FMT_GPTQ) return launch_fmt<FMT_GPTQ>(p, s, st);
-    return launch_fmt<FMT_GPTQ_SYM>(p, s, st);
+    return bf16 ? launch_e<bf16_t>(fmt, p, s, st) : launch_e<half_t>(fmt, p, s, st);
 }
 
 }  // namespace w4a16

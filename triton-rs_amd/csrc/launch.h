@@ -114,7 +114,9 @@ size_t prefill_dma_lds(int bm, int bn);
 
 // max_ksplit caps the K split (1: never split, so no scratch is needed).
 PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int max_ksplit = 4);
-hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st);
+// bf16: x, scales and out are bfloat16 (pipelined kernel, dense checkpoint layouts only)
+hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st,
+                          bool bf16 = false);
 bool moe_gemm_supported(int N, int K, int G, int block_m);
 hipError_t launch_moe_gemm(int fmt, const PrefillParams& p, int block_m, int max_blocks,
                            hipStream_t st);
@@ -168,7 +170,9 @@ constexpr size_t SKINNY_GIDX_MAX_LDS = 64 * 1024;
 
 SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx = false,
                          bool xcd_placement = false);
-hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st);
+// bf16: x, scales and out are bfloat16 (plain group order only)
+hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st,
+                         bool bf16 = false);
 
 // Generic strided GEMM with the reference kernels' parameter list
 // (w4a16_gptq_gemm_typed.rs:110-128, awq_gemm_int4_typed.rs:96-114) plus optional g_idx.

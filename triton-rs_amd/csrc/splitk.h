@@ -104,9 +104,10 @@ constexpr int FB = 16;
 constexpr int FB4 = 16;
 constexpr int FINISH_MAX_THREADS = 512;
 
-template <int SC>
+// E: the output element (fp16, or bf16 for the bfloat16 instantiations).
+template <int SC, typename E = half_t>
 __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
-                                                   half_t* __restrict__ out, int splits, int M,
+                                                   E* __restrict__ out, int splits, int M,
                                                    int N, int m0, int rows, int n0, int C) {
     __shared__ float4_t part[FINISH_MAX_THREADS];
     const int T = blockDim.x;   // <= FINISH_MAX_THREADS
@@ -147,7 +148,7 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
             if (gi == 0)
                 for (int g = 1; g < groups; ++g) acc += reinterpret_cast<float*>(part)[g * entries + e];
         }
-        if (gi == 0) out[off] = (half_t)acc;
+        if (gi == 0) out[off] = (E)acc;
         return;
     }
     const int cpr = C / 4;                       // chunks per row
@@ -173,11 +174,9 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
 #pragma unroll
             for (int t = 0; t < FB4 / 2; ++t)
                 if (t < splits) { a += va[t]; b += vb[t]; }
-            *reinterpret_cast<u32x2*>(out + offa) =
-                u32x2{as_u32(half2_t{(half_t)a[0], (half_t)a[1]}), as_u32(half2_t{(half_t)a[2], (half_t)a[3]})};
+            *reinterpret_cast<u32x2*>(out + offa) = u32x2{pack2(E{}, a[0], a[1]), pack2(E{}, a[2], a[3])};
             if (okb)
-                *reinterpret_cast<u32x2*>(out + offb) =
-                    u32x2{as_u32(half2_t{(half_t)b[0], (half_t)b[1]}), as_u32(half2_t{(half_t)b[2], (half_t)b[3]})};
+                *reinterpret_cast<u32x2*>(out + offb) = u32x2{pack2(E{}, b[0], b[1]), pack2(E{}, b[2], b[3])};
         }
         return;
     }
@@ -208,11 +207,8 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
             }
             __syncthreads();
         }
-        if (gi == 0 && ch < chunks) {
-            const half2_t lo = {(half_t)acc[0], (half_t)acc[1]};
-            const half2_t hi = {(half_t)acc[2], (half_t)acc[3]};
-            *reinterpret_cast<u32x2*>(out + off) = u32x2{as_u32(lo), as_u32(hi)};
-        }
+        if (gi == 0 && ch < chunks)
+            *reinterpret_cast<u32x2*>(out + off) = u32x2{pack2(E{}, acc[0], acc[1]), pack2(E{}, acc[2], acc[3])};
     }
 }
 
