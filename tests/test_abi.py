@@ -232,10 +232,10 @@ def test_prepared_kernels_isa(tmp_path):
 
 
 def test_bf16_flag_plans_and_is_refused_elsewhere():
-    """W4A16_BF16 plans the small-batch kernel up to 64 rows and the pipelined prefill beyond
-    (plain group order, the shapes they take), the generic kernel for act-order and other
-    shapes; entry points without a bfloat16 instantiation report the flagged value as an
-    unknown format (no GPU call)."""
+    """W4A16_BF16 plans the VALU GEMV up to 4 rows, the small-batch kernel up to 64 and the
+    pipelined prefill beyond (plain group order, the shapes they take), the generic kernel for
+    act-order and other shapes; entry points without a bfloat16 instantiation report the
+    flagged value as an unknown format (no GPU call)."""
     P = pkg()
     L = P.lib()
     k = ctypes.c_int(0)
@@ -243,7 +243,7 @@ def test_bf16_flag_plans_and_is_refused_elsewhere():
     def plan(fmt, M, N, K, gidx=0):
         assert L.w4a16_gemm_plan(fmt, M, N, K, 128, gidx, ctypes.byref(k)) == P.OK
         return P.KERNELS[k.value]
-    for M, N, K, want in ((1, 14336, 4096, "skinny"), (8, 4096, 14336, "skinny"),
+    for M, N, K, want in ((1, 14336, 4096, "gemv"), (4, 4096, 14336, "gemv"), (8, 4096, 14336, "skinny"),
                           (16, 6144, 4096, "skinny"), (64, 6144, 4096, "skinny"),
                           (65, 6144, 4096, "prefill"), (2048, 4096, 14336, "prefill"),
                           (33, 136, 384, "strided")):
@@ -261,10 +261,21 @@ def test_bf16_flag_plans_and_is_refused_elsewhere():
 
 def test_bf16_fast_kernels_isa(tmp_path):
     """The bfloat16 instances of the small-batch and prefill kernels run bf16 MFMA on weights
-    rounded with v_cvt_pk_bf16_f32 (from v_cvt_f32_ubyte nibble conversions), and none spills;
-    their fp16 twins have neither."""
+    rounded with v_cvt_pk_bf16_f32 (from v_cvt_f32_ubyte nibble conversions), the bf16 VALU
+    GEMVs v_dot2c_f32_bf16 without MFMA, and none spills; their fp16 twins have none of it."""
     bdir = os.path.join(ROOT, "triton-rs_amd", "_build")
+    gv = os.path.join(bdir, "kernels_gemv.o")
     objs = [os.path.join(bdir, f) for f in ("kernels_skinny.o", "kernels_prefill.o")]
+    if not all(os.path.exists(o) for o in objs + [gv]):
+        pytest.skip("build objects not present (run build first)")
+    gk = {n: b for n, b in _disassemble_tu(gv, tmp_path).items()
+          if "gemv_awq_kernel" in n or "gemv_gptq_kernel" in n}
+    gbf = {n: b for n, b in gk.items() if "DF16b" in n}
+    assert len(gbf) >= 60, len(gbf)
+    for n, b in gk.items():
+        bf = "DF16b" in n
+        assert ("v_dot2c_f32_bf16" in b) == bf and ("v_dot2c_f32_f16" in b) != bf, n
+        assert "v_mfma" not in b and "scratch_" not in b, n
     if not all(os.path.exists(o) for o in objs):
         pytest.skip("build objects not present (run build first)")
     seen = 0

@@ -1,8 +1,8 @@
 """GPU parity of the bfloat16 instantiation (W4A16_BF16 flag): dequantised weights bit-exact
 against the oracle, GEMM outputs within the path's 1e-2 bar of the oracle's float64
 accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32,
-on each kernel bf16 runs (small-batch up to 64 rows, pipelined prefill beyond, the generic
-kernel for act-order and other shapes). The reference kernels are generic over the element
+on each kernel bf16 runs (VALU GEMV up to 4 rows, small-batch up to 64, pipelined prefill
+beyond, the generic kernel for act-order and other shapes). The reference kernels are generic over the element
 type and name bf16 (w4a16_gptq_gemm_typed.rs:65-67)."""
 import numpy as np
 import pytest
@@ -65,7 +65,7 @@ def test_dequant_bf16_act_order_bit_exact(torch_cuda, orc):
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
-@pytest.mark.parametrize("M,K,N,kernel", [(1, 1024, 512, "skinny"), (7, 512, 256, "skinny"),
+@pytest.mark.parametrize("M,K,N,kernel", [(1, 1024, 512, "gemv"), (7, 512, 256, "skinny"),
                                           (64, 2048, 768, "skinny"), (200, 1024, 512, "prefill"),
                                           (33, 384, 136, "strided")])
 def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N, kernel):
@@ -84,15 +84,19 @@ def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N, kernel):
 
 
 @pytest.mark.parametrize("fmt,M,K,N,kernel", [
-    (AWQ, 1, 4096, 14336, "skinny"),      # config 1's shapes in bf16
+    (AWQ, 1, 4096, 14336, "gemv"),        # config 1's shapes in bf16
+    (AWQ, 1, 14336, 4096, "gemv"),
+    (AWQ, 4, 4096, 14336, "gemv"),
     (AWQ, 8, 14336, 4096, "skinny"),
+    (SYM, 1, 4096, 4096, "gemv"),         # config 0's shape
+    (GPTQ, 3, 14336, 4096, "gemv"),
     (GPTQ, 16, 4096, 6144, "skinny"),     # config 2's shape, plain group order
     (GPTQ, 64, 4096, 6144, "skinny"),
     (SYM, 256, 8192, 1024, "prefill"),    # prefill with its K split across workgroups
     (AWQ, 2048, 4096, 14336, "prefill"),  # config 3
 ])
 def test_gemm_bf16_fast_paths_full_size(torch_cuda, orc, fmt, M, K, N, kernel):
-    """The bf16 small-batch and prefill kernels at the benchmark shapes: every row up to 16
+    """The bf16 GEMV, small-batch and prefill kernels at the benchmark shapes: every row up to 16
     rows, else 16 sampled rows (the first and last among them), against the oracle's bf16
     GEMM; a second call is bit-identical (fixed-order split-K sums)."""
     torch = torch_cuda
@@ -132,13 +136,14 @@ def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
-@pytest.mark.parametrize("M,K,N,G", [(9, 256, 128, 64), (1, 4096, 512, 128), (40, 4096, 768, 128),
-                                     (256, 8192, 1024, 128)])
+@pytest.mark.parametrize("M,K,N,G", [(9, 256, 128, 64), (1, 4096, 512, 128), (3, 4096, 1024, 128),
+                                     (40, 4096, 768, 128), (256, 8192, 1024, 128)])
 def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt, M, K, N, G):
     """x in multiples of 1/2 up to 2, scales 2^-7: every product and partial sum is exact in
     fp32, so the output is the exact sum rounded once to bf16, identical to the oracle, on
-    the small-batch kernel (with and without a K split across workgroups) and the prefill
-    kernel (256 rows: K split in 4)."""
+    the GEMV (1 and 3 rows, K split with the fixed-point hand-off), the small-batch kernel
+    (with and without a K split across workgroups) and the prefill kernel (256 rows: K split
+    in 4)."""
     torch = torch_cuda
     g = np.random.default_rng(740 + fmt)
     q = g.integers(0, 16, size=(K, N), dtype=np.int32)

@@ -206,11 +206,13 @@ static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DE
     return W4A16_KERNEL_STRIDED;
 }
 
-// bfloat16 elements (W4A16_BF16): the small-batch kernel up to 64 rows and the pipelined
-// prefill beyond, both in plain group order on the checkpoint layouts; act-order and the
-// shapes those kernels reject run the generic kernel.
+// bfloat16 elements (W4A16_BF16): the VALU GEMVs up to GEMV_MAX_M rows, the small-batch
+// kernel up to 64 and the pipelined prefill beyond, all in plain group order on the
+// checkpoint layouts; act-order and the shapes those kernels reject run the generic kernel.
 static int plan_bf16(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) return W4A16_KERNEL_STRIDED;
+    const GemvShape gv = gemv_shape(fmt, M, N, K, G, false, /*valu_only=*/true);
+    if (M <= GEMV_MAX_M && gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
     const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);
     if (M <= 64 && sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
     const PrefillShape ps = prefill_shape(fmt, M, N, K, G, cus);
@@ -324,7 +326,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
             kernel = g_idx ? W4A16_KERNEL_STRIDED
                            : unsplit_prefill_ok() ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     } else if (kernel == W4A16_KERNEL_GEMV) {
-        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd);
+        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd, bf16);
         if (s.splits > 1 && !scratch_fits((size_t)s.col_tiles, (size_t)s.splits * M * N * sizeof(float)))
             kernel = unsplit_prefill_ok() ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     }
@@ -407,7 +409,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     }
 
     if (kernel == W4A16_KERNEL_GEMV) {
-        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd);
+        const GemvShape s = gemv_shape(fmt, M, N, K, G, xcd, bf16);
         GemvParams p{};
         p.x = static_cast<const half_t*>(x);
         p.qweight = static_cast<const uint32_t*>(qweight);
@@ -430,7 +432,7 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
             p.slots = sc.slots;
             p.masks = sc.masks;
         }
-        hipError_t e = launch_gemv(fmt, p, s, st);
+        hipError_t e = launch_gemv(fmt, p, s, st, bf16);
         if (e != hipSuccess) return hip_fail(e, "gemv launch");
         return W4A16_OK;
     }

@@ -69,6 +69,23 @@ __device__ __forceinline__ half2_t nib_pair16(uint32_t v) {
 __device__ __forceinline__ float dot2(half2_t a, half2_t b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }
+// the same for bf16 pairs (v_dot2c_f32_bf16)
+__device__ __forceinline__ float dot2(bf16x2_t a, bf16x2_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+}
+
+// bf16 pair (128 + nibble at bit 0, 128 + nibble at bit 16) from v: 0x4300 | q is the bf16
+// number 128 + q (ulp 1 in [128, 256)). bf16 keeps 7 fraction bits, so a nibble must sit at
+// bits 0..3 (no 16 q form as for fp16).
+constexpr uint32_t MAGIC2_BF16 = 0x43004300u;   // (128, 128) as two bf16
+__device__ __forceinline__ bf16x2_t nib_pair_bf16(uint32_t v) {
+    return __builtin_bit_cast(bf16x2_t, and_or(v, vconst(0x000F000Fu), vconst(MAGIC2_BF16)));
+}
+
+// element pair type and the bias of the exponent trick per element type
+template <typename E> struct pair2;
+template <> struct pair2<half_t> { typedef half2_t type; static constexpr float bias = 1024.0f; };
+template <> struct pair2<bf16_t> { typedef bf16x2_t type; static constexpr float bias = 128.0f; };
 
 // Nibble slot that column n occupies in an AWQ word: (n%8)/2 + (n%8)%2*4
 // (awq_gemm_int4_typed.rs:139-151). Slot s is read from bits [4s, 4s+4).

@@ -18,6 +18,8 @@
 // which equals the reference's dequant-then-dot up to fp32 rounding (the reference rounds
 // each dequantised weight to fp16 first; the difference is < 2^-11 relative per term).
 // The AWQ matrix-core kernel (M = 2..8) moves the dot products to v_mfma (below).
+#include <type_traits>
+
 #include "device_common.h"
 #include "launch.h"
 #include "splitk.h"
@@ -36,9 +38,13 @@ namespace w4a16 {
 // are consumed while the scales are still in flight; issued first, the scattered scale and
 // zero requests cost 0.3 us at K=4096, N=14336 (7.93 vs 8.28 us, same kernel otherwise), and
 // cached rather than streamed 0.2 us more. The scheduling barriers keep this order.
-template <int M, int CW, int RL, int WAVES, bool XCD, bool FIX>
+// E: the element type of x, the scales and the output. bf16 unpacks 128 + q (every nibble
+// shifted to bits 0..3) and accumulates with v_dot2c_f32_bf16: s * (A - 128 X - z X).
+template <int M, int CW, int RL, int WAVES, bool XCD, bool FIX, typename E = half_t>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_awq_kernel(GemvParams p) {
+    constexpr bool BF = std::is_same<E, bf16_t>::value;
+    typedef typename pair2<E>::type e2_t;
     constexpr int LPR = 32 / CW;
     constexpr int RPW = 64 / LPR;
     constexpr int RB = RPW * WAVES;
@@ -64,7 +70,7 @@ gemv_awq_kernel(GemvParams p) {
     const int g = k0 / p.G;
 
     // ---- x pairs (rows 2i, 2i+1 of this lane) for every m, and X = sum of x
-    half2_t xs[M][RL / 2];
+    e2_t xs[M][RL / 2];
     float X[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
@@ -72,8 +78,8 @@ gemv_awq_kernel(GemvParams p) {
 #pragma unroll
         for (int i = 0; i < RL / 8; ++i) {
             const uint4 v = xp[i];
-            xs[m][4 * i + 0] = as_h2(v.x); xs[m][4 * i + 1] = as_h2(v.y);
-            xs[m][4 * i + 2] = as_h2(v.z); xs[m][4 * i + 3] = as_h2(v.w);
+            xs[m][4 * i + 0] = __builtin_bit_cast(e2_t, v.x); xs[m][4 * i + 1] = __builtin_bit_cast(e2_t, v.y);
+            xs[m][4 * i + 2] = __builtin_bit_cast(e2_t, v.z); xs[m][4 * i + 3] = __builtin_bit_cast(e2_t, v.w);
         }
     }
 
@@ -106,15 +112,15 @@ gemv_awq_kernel(GemvParams p) {
             reinterpret_cast<const u32x4*>(p.scales + (size_t)g * p.N + 8 * (wc0 + c)));
     }
     __builtin_amdgcn_sched_barrier(0);
-    float X1024[M];
+    float XB[M];   // the exponent trick's bias (1024 or 128) times X
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         float sx = 0.f;
-        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+        const e2_t one2 = {(E)1.0f, (E)1.0f};
 #pragma unroll
         for (int i = 0; i < RL / 2; ++i) sx = dot2(xs[m][i], one2, sx);
         X[m] = sx;
-        X1024[m] = 1024.0f * sx;
+        XB[m] = pair2<E>::bias * sx;
     }
 
     // ---- main loop: acc[m][cw][slot]
@@ -135,15 +141,22 @@ gemv_awq_kernel(GemvParams p) {
             const uint32_t lo = perm(b, a, 0x05040100u);
             const uint32_t hi = perm(b, a, 0x07060302u);
             const uint32_t lo8 = lo >> 8, hi8 = hi >> 8;
-            half2_t h[8];
-            h[0] = nib_pair(lo);      // slot 0: 1024 + q
-            h[1] = nib_pair16(lo);    // slot 1: 1024 + 16 q
-            h[2] = nib_pair(lo8);     // slot 2
-            h[3] = nib_pair16(lo8);   // slot 3 (x16)
-            h[4] = nib_pair(hi);      // slot 4
-            h[5] = nib_pair16(hi);    // slot 5 (x16)
-            h[6] = nib_pair(hi8);     // slot 6
-            h[7] = nib_pair16(hi8);   // slot 7 (x16)
+            e2_t h[8];
+            if constexpr (BF) {       // slot s: 128 + q
+                h[0] = nib_pair_bf16(lo);       h[1] = nib_pair_bf16(lo >> 4);
+                h[2] = nib_pair_bf16(lo8);      h[3] = nib_pair_bf16(lo8 >> 4);
+                h[4] = nib_pair_bf16(hi);       h[5] = nib_pair_bf16(hi >> 4);
+                h[6] = nib_pair_bf16(hi8);      h[7] = nib_pair_bf16(hi8 >> 4);
+            } else {
+                h[0] = nib_pair(lo);      // slot 0: 1024 + q
+                h[1] = nib_pair16(lo);    // slot 1: 1024 + 16 q
+                h[2] = nib_pair(lo8);     // slot 2
+                h[3] = nib_pair16(lo8);   // slot 3 (x16)
+                h[4] = nib_pair(hi);      // slot 4
+                h[5] = nib_pair16(hi);    // slot 5 (x16)
+                h[6] = nib_pair(hi8);     // slot 6
+                h[7] = nib_pair16(hi8);   // slot 7 (x16)
+            }
 #pragma unroll
             for (int m = 0; m < M; ++m)
 #pragma unroll
@@ -154,7 +167,7 @@ gemv_awq_kernel(GemvParams p) {
     // ---- zero point and scale, once per lane and column; columns written in natural order
 #pragma unroll
     for (int c = 0; c < CW; ++c) {
-        const half_t* sh = reinterpret_cast<const half_t*>(&sv[c]);
+        const E* sh = reinterpret_cast<const E*>(&sv[c]);
 #pragma unroll
         for (int m = 0; m < M; ++m) {
             float col[8];
@@ -162,9 +175,9 @@ gemv_awq_kernel(GemvParams p) {
             for (int s = 0; s < 8; ++s) {
                 const int n = awq_col_of_slot(s);
                 const float z = (float)nib(qz[c], s);
-                // odd slots were unpacked as 1024 + 16 q
-                const float u = (s & 1) ? __builtin_fmaf(acc[m][c][s] - X1024[m], 1.0f / 16.0f, -z * X[m])
-                                        : acc[m][c][s] - X1024[m] - z * X[m];
+                // fp16: odd slots were unpacked as 1024 + 16 q
+                const float u = (!BF && (s & 1)) ? __builtin_fmaf(acc[m][c][s] - XB[m], 1.0f / 16.0f, -z * X[m])
+                                                 : acc[m][c][s] - XB[m] - z * X[m];
                 col[n] = (float)sh[n] * u;
             }
             float4* dst = reinterpret_cast<float4*>(&red[rb][m][(cl * CW + c) * 8]);
@@ -177,12 +190,12 @@ gemv_awq_kernel(GemvParams p) {
     // ---- reduce over row blocks; write partial (or the output when there is one split)
     const int n0 = ct * C;
     if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
-        constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
-        size_t off[E];
-        float v[E];
+        constexpr int T = 64 * WAVES, NE = (M * C + T - 1) / T;
+        size_t off[NE];
+        float v[NE];
         int n = 0;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < NE; ++e) {
             const int i = (int)threadIdx.x + e * T;
             if (i >= M * C) break;
             const int m = i / C, cidx = i - m * C;
@@ -193,7 +206,8 @@ gemv_awq_kernel(GemvParams p) {
             v[e] = s;
             n = e + 1;
         }
-        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        splitk_fixed_commit<SC, NE, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, reinterpret_cast<E*>(p.out),
+                                       off, v, n, split, p.splits);
         return;
     } else {
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
@@ -202,12 +216,12 @@ gemv_awq_kernel(GemvParams p) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
-        if (p.splits == 1) p.out[off] = (half_t)s;
+        if (p.splits == 1) reinterpret_cast<E*>(p.out)[off] = (E)s;
         else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
-        splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+        splitk_finish<M, SC, E>(p.ws, reinterpret_cast<E*>(p.out), p.splits, p.N, n0, C);
     }
 }
 
@@ -215,9 +229,12 @@ gemv_awq_kernel(GemvParams p) {
 
 // Tile: C = LPR * CW columns x R k-rows. A lane owns CW consecutive columns (one 128-bit
 // load per packed row for CW = 4) and RL consecutive packed rows (8*RL k, one group).
-template <int FMT, int M, int CW, int RL, int WAVES, int LPR, bool XCD, bool FIX>
+// E: as for the AWQ kernel (bf16: every nibble at bits 0..3, bias 128).
+template <int FMT, int M, int CW, int RL, int WAVES, int LPR, bool XCD, bool FIX, typename E = half_t>
 __global__ void __launch_bounds__(64 * WAVES)
 gemv_gptq_kernel(GemvParams p) {
+    constexpr bool BF = std::is_same<E, bf16_t>::value;
+    typedef typename pair2<E>::type e2_t;
     constexpr int RPW = 64 / LPR;
     constexpr int RB = RPW * WAVES;
     constexpr int C = LPR * CW;
@@ -240,26 +257,26 @@ gemv_gptq_kernel(GemvParams p) {
     const int g = k0 / p.G;
 
     // x for packed row j, rearranged to the unpack order: (x0,x4) (x1,x5) (x2,x6) (x3,x7)
-    half2_t xs[M][RL][4];
+    e2_t xs[M][RL][4];
     float X[M], B[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) {
         float x1 = 0.f, x16 = 0.f;
-        const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+        const e2_t one2 = {(E)1.0f, (E)1.0f};
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
             const uint4 v = *reinterpret_cast<const uint4*>(p.x + (size_t)m * p.K + k0 + 8 * j);
-            xs[m][j][0] = as_h2(perm(v.z, v.x, 0x05040100u));
-            xs[m][j][1] = as_h2(perm(v.z, v.x, 0x07060302u));
-            xs[m][j][2] = as_h2(perm(v.w, v.y, 0x05040100u));
-            xs[m][j][3] = as_h2(perm(v.w, v.y, 0x07060302u));
+            xs[m][j][0] = __builtin_bit_cast(e2_t, perm(v.z, v.x, 0x05040100u));
+            xs[m][j][1] = __builtin_bit_cast(e2_t, perm(v.z, v.x, 0x07060302u));
+            xs[m][j][2] = __builtin_bit_cast(e2_t, perm(v.w, v.y, 0x05040100u));
+            xs[m][j][3] = __builtin_bit_cast(e2_t, perm(v.w, v.y, 0x07060302u));
             x1 = dot2(xs[m][j][0], one2, x1);
             x1 = dot2(xs[m][j][2], one2, x1);
             x16 = dot2(xs[m][j][1], one2, x16);
             x16 = dot2(xs[m][j][3], one2, x16);
         }
         X[m] = x1 + x16;
-        B[m] = 1024.0f * (x1 + x16 * (1.0f / 16.0f));
+        B[m] = BF ? 128.0f * X[m] : 1024.0f * (x1 + x16 * (1.0f / 16.0f));
     }
 
     uint32_t w[RL][CW];
@@ -290,10 +307,16 @@ gemv_gptq_kernel(GemvParams p) {
         for (int c = 0; c < CW; ++c) {
             const uint32_t q = w[j][c];
             const uint32_t q8 = q >> 8;
-            const half2_t h0 = nib_pair(q);      // k0, k4
-            const half2_t h1 = nib_pair16(q);    // k1, k5 (x16)
-            const half2_t h2 = nib_pair(q8);     // k2, k6
-            const half2_t h3 = nib_pair16(q8);   // k3, k7 (x16)
+            e2_t h0, h1, h2, h3;
+            if constexpr (BF) {
+                h0 = nib_pair_bf16(q);   h1 = nib_pair_bf16(q >> 4);     // (k0, k4), (k1, k5)
+                h2 = nib_pair_bf16(q8);  h3 = nib_pair_bf16(q8 >> 4);    // (k2, k6), (k3, k7)
+            } else {
+                h0 = nib_pair(q);      // k0, k4
+                h1 = nib_pair16(q);    // k1, k5 (x16)
+                h2 = nib_pair(q8);     // k2, k6
+                h3 = nib_pair16(q8);   // k3, k7 (x16)
+            }
 #pragma unroll
             for (int m = 0; m < M; ++m) {
                 a1[m][c] = dot2(h0, xs[m][j][0], a1[m][c]);
@@ -307,34 +330,35 @@ gemv_gptq_kernel(GemvParams p) {
     // zero point and scale for the lane's CW columns (same qzeros word: CW divides 8)
     uint32_t qz = 0;
     if constexpr (FMT == FMT_GPTQ) qz = p.qzeros[(size_t)g * (p.N >> 3) + (c0 >> 3)];
-    half_t sc[CW];
+    E sc[CW];
+    const E* scales = reinterpret_cast<const E*>(p.scales);
     if constexpr (CW == 4) {
-        const uint2 v = *reinterpret_cast<const uint2*>(p.scales + (size_t)g * p.N + c0);
-        const half_t* hv = reinterpret_cast<const half_t*>(&v);
+        const uint2 v = *reinterpret_cast<const uint2*>(scales + (size_t)g * p.N + c0);
+        const E* hv = reinterpret_cast<const E*>(&v);
 #pragma unroll
         for (int c = 0; c < 4; ++c) sc[c] = hv[c];
     } else {
 #pragma unroll
-        for (int c = 0; c < CW; ++c) sc[c] = p.scales[(size_t)g * p.N + c0 + c];
+        for (int c = 0; c < CW; ++c) sc[c] = scales[(size_t)g * p.N + c0 + c];
     }
 #pragma unroll
     for (int m = 0; m < M; ++m) {
 #pragma unroll
         for (int c = 0; c < CW; ++c) {
             const float z = (float)zero_of<FMT>(qz, c0 + c, p.zero_offset);
-            const float u = a1[m][c] + a16[m][c] * (1.0f / 16.0f) - B[m] - z * X[m];
+            const float u = a1[m][c] + a16[m][c] * (BF ? 1.0f : 1.0f / 16.0f) - B[m] - z * X[m];
             red[rb][m][cl * CW + c] = (float)sc[c] * u;
         }
     }
     __syncthreads();
 
     if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
-        constexpr int T = 64 * WAVES, E = (M * C + T - 1) / T;
-        size_t off[E];
-        float v[E];
+        constexpr int T = 64 * WAVES, NE = (M * C + T - 1) / T;
+        size_t off[NE];
+        float v[NE];
         int n = 0;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < NE; ++e) {
             const int i = (int)threadIdx.x + e * T;
             if (i >= M * C) break;
             const int m = i / C, cidx = i - m * C;
@@ -345,7 +369,8 @@ gemv_gptq_kernel(GemvParams p) {
             v[e] = s;
             n = e + 1;
         }
-        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        splitk_fixed_commit<SC, NE, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, reinterpret_cast<E*>(p.out),
+                                       off, v, n, split, p.splits);
         return;
     } else {
     for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
@@ -354,12 +379,12 @@ gemv_gptq_kernel(GemvParams p) {
 #pragma unroll
         for (int r = 0; r < RB; ++r) s += red[r][m][cidx];
         const size_t off = (size_t)m * p.N + n0 + cidx;
-        if (p.splits == 1) p.out[off] = (half_t)s;
+        if (p.splits == 1) reinterpret_cast<E*>(p.out)[off] = (E)s;
         else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
     }
     if (p.splits == 1) return;
     if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
-        splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+        splitk_finish<M, SC, E>(p.ws, reinterpret_cast<E*>(p.out), p.splits, p.N, n0, C);
     }
 }
 
@@ -771,7 +796,7 @@ constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R
 constexpr int AR_MIN_M = 3, AR_WAVES = 8, AR_ROWS = 128 * AR_WAVES;
 }  // namespace
 
-GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bool valu_only) {
     GemvShape s{};
     // AWQ: the row-paired matrix-core kernel for M = 3..8 where its tile fits (K a multiple of
     // 1024, groups of 128 rows or more); the block-diagonal matrix-core kernel for M = 2 and
@@ -784,7 +809,7 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     const bool wide_fits = mfma_fits && K % AMW_ROWS == 0 && G % AMW_R == 0;
     const bool rows_fits = N % 256 == 0 && K % AR_ROWS == 0 && G % 128 == 0 && K % G == 0 &&
                            (size_t)K * N / 2 < ((size_t)1 << 31);
-    if (fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
+    if (!valu_only && fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
         s.ok = true; s.mfma = true; s.awq_rows = true; s.col_tiles = N / 256;
         // 4 waves (512-row workgroups) where 8 would leave fewer than 64 workgroups (graph
         // replays, one GPU's share of an 8-way tensor-parallel layer, K=4096 -> N=1792: M=4
@@ -792,7 +817,7 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
         const int w = (N / 256) * (K / AR_ROWS) < 64 ? AR_WAVES / 2 : AR_WAVES;
         s.splits = K / (128 * w);
         s.threads = 64 * w;
-    } else if (fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
+    } else if (!valu_only && fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
         s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
         s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
@@ -831,12 +856,13 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement) {
     return s;
 }
 
-template <int M, bool XCD, bool FIX>
+template <int M, bool XCD, bool FIX, typename E>
 static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     const dim3 block(s.threads);
+    constexpr bool H = std::is_same<E, half_t>::value;   // the matrix-core GEMVs are fp16 only
     if (fmt == FMT_AWQ && s.mfma) {
-        if constexpr (M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
+        if constexpr (H && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
             if (s.awq_rows) {
                 if (s.threads == 64 * AR_WAVES)
                     hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX>), grid, block, 0, st, p);
@@ -845,7 +871,7 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
                 return;
             }
         }
-        if constexpr (M <= GEMV_MFMA_MAX_M) {
+        if constexpr (H && M <= GEMV_MFMA_MAX_M) {
             if (s.mfma_wide)
                 hipLaunchKernelGGL((gemv_awq_mfma_kernel<M, AM_CW, AMW_R, AMW_WAVES, AM_PF, XCD, FIX>), grid, block, 0, st, p);
             else
@@ -855,61 +881,71 @@ static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hip
         if constexpr (M == 1) {
             if (fmt != FMT_AWQ && s.gptq_deep) {
                 if (fmt == FMT_GPTQ)
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX, E>), grid, block, 0, st, p);
                 else
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL1, GQ_WAVES, GQ_LPR, XCD, FIX, E>), grid, block, 0, st, p);
                 return;
             }
         }
         if constexpr (M > 1) {
             if (fmt != FMT_AWQ && s.gptq_narrow) {
                 if (fmt == FMT_GPTQ)
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX, E>), grid, block, 0, st, p);
                 else
-                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPRN, XCD, FIX, E>), grid, block, 0, st, p);
                 return;
             }
         }
         if constexpr (M == 1) {
             if (fmt == FMT_AWQ && s.awq_deep) {
-                hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES_DEEP, XCD, FIX>), grid, block, 0, st, p);
+                hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES_DEEP, XCD, FIX, E>), grid, block, 0, st, p);
                 return;
             }
         }
         if (fmt == FMT_AWQ)
-            hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD, FIX>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_awq_kernel<M, AWQ_CW, AWQ_RL, AWQ_WAVES, XCD, FIX, E>), grid, block, 0, st, p);
         else if (fmt == FMT_GPTQ)
-            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX, E>), grid, block, 0, st, p);
         else
-            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX>), grid, block, 0, st, p);
+            hipLaunchKernelGGL((gemv_gptq_kernel<FMT_GPTQ_SYM, M, GQ_CW, GQ_RL, GQ_WAVES, GQ_LPR, XCD, FIX, E>), grid, block, 0, st, p);
     }
 }
 
-template <int M>
+template <int M, typename E>
 static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (M > GEMV_MAX_M && !(fmt == FMT_AWQ && s.mfma)) return hipErrorInvalidValue;
+    if (!std::is_same<E, half_t>::value && s.mfma) return hipErrorInvalidValue;
     // the hand-off protocol is a template parameter: each kernel carries only the one it uses
     if (p.fixed) {
-        if (s.xcd) launch_gemv_mx<M, true, true>(fmt, p, s, st);
-        else launch_gemv_mx<M, false, true>(fmt, p, s, st);
+        if (s.xcd) launch_gemv_mx<M, true, true, E>(fmt, p, s, st);
+        else launch_gemv_mx<M, false, true, E>(fmt, p, s, st);
     } else {
-        if (s.xcd) launch_gemv_mx<M, true, false>(fmt, p, s, st);
-        else launch_gemv_mx<M, false, false>(fmt, p, s, st);
+        if (s.xcd) launch_gemv_mx<M, true, false, E>(fmt, p, s, st);
+        else launch_gemv_mx<M, false, false, E>(fmt, p, s, st);
     }
     return hipGetLastError();
 }
 
-hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
+hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st, bool bf16) {
+    if (bf16) {   // the VALU kernels (M <= GEMV_MAX_M)
+        switch (p.M) {
+            case 1: return launch_gemv_m<1, bf16_t>(fmt, p, s, st);
+            case 2: return launch_gemv_m<2, bf16_t>(fmt, p, s, st);
+            case 3: return launch_gemv_m<3, bf16_t>(fmt, p, s, st);
+            case 4: return launch_gemv_m<4, bf16_t>(fmt, p, s, st);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (p.M) {
-        case 1: return launch_gemv_m<1>(fmt, p, s, st);
-        case 2: return launch_gemv_m<2>(fmt, p, s, st);
-        case 3: return launch_gemv_m<3>(fmt, p, s, st);
-        case 4: return launch_gemv_m<4>(fmt, p, s, st);
-        case 5: return launch_gemv_m<5>(fmt, p, s, st);
-        case 6: return launch_gemv_m<6>(fmt, p, s, st);
-        case 7: return launch_gemv_m<7>(fmt, p, s, st);
-        case 8: return launch_gemv_m<8>(fmt, p, s, st);
+        case 1: return launch_gemv_m<1, half_t>(fmt, p, s, st);
+        case 2: return launch_gemv_m<2, half_t>(fmt, p, s, st);
+        case 3: return launch_gemv_m<3, half_t>(fmt, p, s, st);
+        case 4: return launch_gemv_m<4, half_t>(fmt, p, s, st);
+        case 5: return launch_gemv_m<5, half_t>(fmt, p, s, st);
+        case 6: return launch_gemv_m<6, half_t>(fmt, p, s, st);
+        case 7: return launch_gemv_m<7, half_t>(fmt, p, s, st);
+        case 8: return launch_gemv_m<8, half_t>(fmt, p, s, st);
         default: return hipErrorInvalidValue;
     }
 }

@@ -212,10 +212,10 @@ __device__ __forceinline__ void splitk_finish_rows(const float* __restrict__ ws,
     }
 }
 
-template <int M, int SC>
-__device__ __forceinline__ void splitk_finish(const float* __restrict__ ws, half_t* __restrict__ out,
+template <int M, int SC, typename E = half_t>
+__device__ __forceinline__ void splitk_finish(const float* __restrict__ ws, E* __restrict__ out,
                                               int splits, int N, int n0, int C) {
-    splitk_finish_rows<SC>(ws, out, splits, M, N, 0, M, n0, C);
+    splitk_finish_rows<SC, E>(ws, out, splits, M, N, 0, M, n0, C);
 }
 
 // ------------------------------------------------------------------ fixed-point hand-off
@@ -252,11 +252,12 @@ constexpr uint64_t FIX_ARRIVE = 1ull << 58, FIX_OVER = 1ull << 53, FIX_BIAS = 1u
 // this split's fp32 partials v[0..n), n <= E. ws is the fp32 partial buffer [splits][M][N]
 // (used only for out-of-range partials). All adds are issued before the first result is
 // used, so a thread's entries cost one round trip together.
-template <int SC, int E>
+// T: the output element (fp16 or bf16).
+template <int SC, int E, typename T = half_t>
 __device__ __forceinline__ void splitk_fixed_commit(uint64_t* __restrict__ slots,
                                                     uint32_t* __restrict__ masks,
                                                     float* __restrict__ ws, size_t mn,
-                                                    half_t* __restrict__ out,
+                                                    T* __restrict__ out,
                                                     const size_t (&off)[E], const float (&v)[E],
                                                     int n, int split, int splits) {
     uint64_t add[E], old[E];
@@ -295,7 +296,7 @@ __device__ __forceinline__ void splitk_fixed_commit(uint64_t* __restrict__ slots
                                     : __hip_atomic_load(ws + (size_t)s * mn + off[e], __ATOMIC_RELAXED, SC);
             __hip_atomic_store(masks + off[e], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        out[off[e]] = (half_t)r;
+        out[off[e]] = (T)r;
         __hip_atomic_store(slots + off[e], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
