@@ -199,8 +199,9 @@ def test_kernel_choice_evidence_in_isa(tmp_path):
     for name, body in gemv.items():
         assert "v_mfma" not in body, name
         assert "v_dot2" in body, name
-    for name, body in gemv_mc.items():
-        assert "v_mfma_f32_16x16x32_f16" in body, name
+    for name, body in gemv_mc.items():   # the row-paired kernel also comes in bf16
+        bf16 = "DF16b" in name
+        assert ("v_mfma_f32_16x16x32_bf16" if bf16 else "v_mfma_f32_16x16x32_f16") in body, name
     for name, body in strided.items():
         bf16 = "DF16b" in name        # the __bf16 element type in the mangled name
         assert ("v_mfma_f32_16x16x32_bf16" if bf16 else "v_mfma_f32_16x16x32_f16") in body, name
@@ -243,12 +244,15 @@ def test_bf16_flag_plans_and_is_refused_elsewhere():
     def plan(fmt, M, N, K, gidx=0):
         assert L.w4a16_gemm_plan(fmt, M, N, K, 128, gidx, ctypes.byref(k)) == P.OK
         return P.KERNELS[k.value]
-    for M, N, K, want in ((1, 14336, 4096, "gemv"), (4, 4096, 14336, "gemv"), (8, 4096, 14336, "skinny"),
+    for M, N, K, want in ((1, 14336, 4096, "gemv"), (4, 4096, 14336, "gemv"),
                           (16, 6144, 4096, "skinny"), (64, 6144, 4096, "skinny"),
                           (65, 6144, 4096, "prefill"), (2048, 4096, 14336, "prefill"),
                           (33, 136, 384, "strided")):
         assert plan(P.FMT_AWQ | P.BF16, M, N, K) == want, (M, N, K)
         assert plan(P.FMT_GPTQ | P.BF16, M, N, K) == want, (M, N, K)
+    # 5..8 rows: the row-paired AWQ GEMV, GPTQ the small-batch kernel
+    assert plan(P.FMT_AWQ | P.BF16, 8, 4096, 14336) == "gemv"
+    assert plan(P.FMT_GPTQ | P.BF16, 8, 4096, 14336) == "skinny"
     assert plan(P.FMT_GPTQ | P.BF16, 16, 6144, 4096, gidx=1) == "strided"
     assert plan(P.FMT_GPTQ | P.BF16, 2048, 6144, 4096, gidx=1) == "strided"
     assert plan(P.FMT_AWQ, 1, 14336, 4096) == "gemv"

@@ -2,7 +2,8 @@
 against the oracle, GEMM outputs within the path's 1e-2 bar of the oracle's float64
 accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32,
 on each kernel bf16 runs (VALU GEMV up to 4 rows, small-batch up to 64, pipelined prefill
-beyond, the generic kernel for act-order and other shapes). The reference kernels are generic over the element
+beyond, the generic kernel for act-order and other shapes; AWQ's row-paired matrix-core GEMV
+up to 8 rows). The reference kernels are generic over the element
 type and name bf16 (w4a16_gptq_gemm_typed.rs:65-67)."""
 import numpy as np
 import pytest
@@ -87,7 +88,9 @@ def test_gemm_bf16_matches_oracle(torch_cuda, orc, fmt, M, K, N, kernel):
     (AWQ, 1, 4096, 14336, "gemv"),        # config 1's shapes in bf16
     (AWQ, 1, 14336, 4096, "gemv"),
     (AWQ, 4, 4096, 14336, "gemv"),
-    (AWQ, 8, 14336, 4096, "skinny"),
+    (AWQ, 5, 4096, 14336, "gemv"),        # row-paired matrix-core GEMV
+    (AWQ, 8, 14336, 4096, "gemv"),
+    (GPTQ, 8, 4096, 14336, "skinny"),
     (SYM, 1, 4096, 4096, "gemv"),         # config 0's shape
     (GPTQ, 3, 14336, 4096, "gemv"),
     (GPTQ, 16, 4096, 6144, "skinny"),     # config 2's shape, plain group order
@@ -137,11 +140,12 @@ def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
 @pytest.mark.parametrize("M,K,N,G", [(9, 256, 128, 64), (1, 4096, 512, 128), (3, 4096, 1024, 128),
-                                     (40, 4096, 768, 128), (256, 8192, 1024, 128)])
+                                     (6, 4096, 1024, 128), (40, 4096, 768, 128), (256, 8192, 1024, 128)])
 def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt, M, K, N, G):
     """x in multiples of 1/2 up to 2, scales 2^-7: every product and partial sum is exact in
     fp32, so the output is the exact sum rounded once to bf16, identical to the oracle, on
-    the GEMV (1 and 3 rows, K split with the fixed-point hand-off), the small-batch kernel
+    the GEMVs (1 and 3 rows, and AWQ's row-paired one at 6; K split with the fixed-point
+    hand-off), the small-batch kernel
     (with and without a K split across workgroups) and the prefill kernel (256 rows: K split
     in 4)."""
     torch = torch_cuda

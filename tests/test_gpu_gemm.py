@@ -112,6 +112,37 @@ def test_gemv_full_size(torch_cuda, orc, fmt, M, K, N):
     assert_parity(y, _oracle(orc, p), what=f"full fmt={fmt} M={M} K={K} N={N}")
 
 
+@pytest.mark.parametrize("bf16", [False, True])
+@pytest.mark.parametrize("fmt,M,kernel", [(AWQ, 1, "gemv"), (AWQ, 2, "gemv"), (AWQ, 3, "gemv"),
+                                          (AWQ, 8, "gemv"), (GPTQ, 1, "gemv"), (GPTQ, 4, "gemv"),
+                                          (SYM, 2, "gemv"), (GPTQ, 16, "skinny")])
+def test_spike_inputs_give_weight_rows(torch_cuda, fmt, M, kernel, bf16):
+    """x = e_k (one 1 per row, at a different k in each row) returns row k of the dequantised
+    weights exactly: (bias + q) - bias - z is exact, so every output is RNE((q - z) * s) with
+    nothing else added. The spikes sit at every element of a 16-byte x chunk and at block and
+    group edges, so a kernel that reads a wrong element of its x fragment, or sums x over the
+    wrong rows for its zero-point correction, fails here (the sum of a random x can hide it)."""
+    torch = torch_cuda
+    P = pkg()
+    K, N, G = 1024, 512, 128
+    dt = torch.bfloat16 if bf16 else torch.float16
+    p = Problem(fmt, M=1, K=K, N=N, G=G, seed=0x5B1CE + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, G, bf16=bf16) == kernel
+    qw = to_dev(p.qweight)
+    qz = None if p.qzeros is None else to_dev(p.qzeros)
+    sc = to_dev(p.scales).to(dt)
+    W = P.dequant(qw, sc, qz, fmt=FMT_NAME[fmt], K=K, group_size=G)
+    ks = [0, 1, 2, 3, 4, 5, 6, 7, 8, 15, 16, 31, 32, 100, 127, 128, 129, 255, 511, 513, K - 1]
+    for i in range(0, len(ks), M):
+        rows = (ks[i:i + M] + [0] * M)[:M]
+        x = torch.zeros((M, K), dtype=dt, device="cuda:0")
+        for m, k in enumerate(rows):
+            x[m, k] = 1
+        y = P.gemm(x, qw, sc, qz, fmt=FMT_NAME[fmt], group_size=G)
+        for m, k in enumerate(rows):
+            assert torch.equal(y[m], W[k]), (fmt, M, bf16, k)
+
+
 def test_gemv_deterministic_and_reusable(torch_cuda, orc):
     """Split-K fix-up sums in a fixed order and leaves the workspace ready for the next call."""
     P = pkg()

@@ -206,13 +206,14 @@ static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DE
     return W4A16_KERNEL_STRIDED;
 }
 
-// bfloat16 elements (W4A16_BF16): the VALU GEMVs up to GEMV_MAX_M rows, the small-batch
-// kernel up to 64 and the pipelined prefill beyond, all in plain group order on the
-// checkpoint layouts; act-order and the shapes those kernels reject run the generic kernel.
+// bfloat16 elements (W4A16_BF16): the VALU GEMVs (and the row-paired AWQ one up to 8 rows),
+// the small-batch kernel up to 64 and the pipelined prefill beyond, all in plain group order
+// on the checkpoint layouts; act-order and the shapes those kernels reject run the generic
+// kernel.
 static int plan_bf16(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) return W4A16_KERNEL_STRIDED;
-    const GemvShape gv = gemv_shape(fmt, M, N, K, G, false, /*valu_only=*/true);
-    if (M <= GEMV_MAX_M && gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
+    const GemvShape gv = gemv_shape(fmt, M, N, K, G, false, /*bf16=*/true);
+    if (gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
     const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);
     if (M <= 64 && sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
     const PrefillShape ps = prefill_shape(fmt, M, N, K, G, cus);

@@ -87,6 +87,13 @@ template <typename E> struct pair2;
 template <> struct pair2<half_t> { typedef half2_t type; static constexpr float bias = 1024.0f; };
 template <> struct pair2<bf16_t> { typedef bf16x2_t type; static constexpr float bias = 128.0f; };
 
+// 32 bits as an element pair. Take the word by value: __builtin_bit_cast applied directly to
+// an element of an ext_vector_type value (v.y) reads element 0 with this compiler.
+template <typename E>
+__device__ __forceinline__ typename pair2<E>::type as_pair(uint32_t u) {
+    return __builtin_bit_cast(typename pair2<E>::type, u);
+}
+
 // Nibble slot that column n occupies in an AWQ word: (n%8)/2 + (n%8)%2*4
 // (awq_gemm_int4_typed.rs:139-151). Slot s is read from bits [4s, 4s+4).
 __host__ __device__ constexpr int awq_slot(int n) { return ((n & 7) >> 1) + ((n & 1) << 2); }

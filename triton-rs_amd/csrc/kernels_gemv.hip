@@ -78,8 +78,8 @@ gemv_awq_kernel(GemvParams p) {
 #pragma unroll
         for (int i = 0; i < RL / 8; ++i) {
             const uint4 v = xp[i];
-            xs[m][4 * i + 0] = __builtin_bit_cast(e2_t, v.x); xs[m][4 * i + 1] = __builtin_bit_cast(e2_t, v.y);
-            xs[m][4 * i + 2] = __builtin_bit_cast(e2_t, v.z); xs[m][4 * i + 3] = __builtin_bit_cast(e2_t, v.w);
+            xs[m][4 * i + 0] = as_pair<E>(v.x); xs[m][4 * i + 1] = as_pair<E>(v.y);
+            xs[m][4 * i + 2] = as_pair<E>(v.z); xs[m][4 * i + 3] = as_pair<E>(v.w);
         }
     }
 
@@ -266,10 +266,10 @@ gemv_gptq_kernel(GemvParams p) {
 #pragma unroll
         for (int j = 0; j < RL; ++j) {
             const uint4 v = *reinterpret_cast<const uint4*>(p.x + (size_t)m * p.K + k0 + 8 * j);
-            xs[m][j][0] = __builtin_bit_cast(e2_t, perm(v.z, v.x, 0x05040100u));
-            xs[m][j][1] = __builtin_bit_cast(e2_t, perm(v.z, v.x, 0x07060302u));
-            xs[m][j][2] = __builtin_bit_cast(e2_t, perm(v.w, v.y, 0x05040100u));
-            xs[m][j][3] = __builtin_bit_cast(e2_t, perm(v.w, v.y, 0x07060302u));
+            xs[m][j][0] = as_pair<E>(perm(v.z, v.x, 0x05040100u));
+            xs[m][j][1] = as_pair<E>(perm(v.z, v.x, 0x07060302u));
+            xs[m][j][2] = as_pair<E>(perm(v.w, v.y, 0x05040100u));
+            xs[m][j][3] = as_pair<E>(perm(v.w, v.y, 0x07060302u));
             x1 = dot2(xs[m][j][0], one2, x1);
             x1 = dot2(xs[m][j][2], one2, x1);
             x16 = dot2(xs[m][j][1], one2, x16);
@@ -612,9 +612,13 @@ gemv_awq_mfma_kernel(GemvParams p) {
 // Measured against gemv_awq_mfma_kernel (graph replays, 20 rotated weight sets): K=4096 ->
 // N=14336 M=3/4/5/8: 10.9/10.3/13.3/14.4 -> 9.4/9.7/10.8/11.3 us; K=14336 -> N=4096 M=4/8:
 // 10.2/15.6 -> 9.7/12.4 us; at M = 2 (8.4 vs 9.0 us) and M = 1 the other kernels stay.
-template <int M, int W, bool FIX>
+// E: the element type (bf16: 128 + q with every nibble shifted to bits 0..3, bf16 MFMA).
+template <int M, int W, bool FIX, typename E = half_t>
 __global__ void __launch_bounds__(64 * W)
 gemv_awq_rows_kernel(GemvParams p) {
+    constexpr bool BF = std::is_same<E, bf16_t>::value;
+    typedef typename pair2<E>::type e2_t;
+    typedef typename vec8<E>::type v8_t;
     constexpr int C = 256;
     constexpr int SC = SCOPE_DEVICE;
     static_assert(64 * W <= FINISH_MAX_THREADS, "split-K finish buffer");
@@ -663,12 +667,12 @@ gemv_awq_rows_kernel(GemvParams p) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) acc[c][s] = float4_t{0.f, 0.f, 0.f, 0.f};
     float xs = 0.f;
-    const half2_t one2 = {(half_t)1.0f, (half_t)1.0f};
+    const e2_t one2 = {(E)1.0f, (E)1.0f};
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-        const half8_t xa = __builtin_bit_cast(half8_t, xv[b]);
-        xs = dot2(as_h2(xv[b].x), one2, xs); xs = dot2(as_h2(xv[b].y), one2, xs);
-        xs = dot2(as_h2(xv[b].z), one2, xs); xs = dot2(as_h2(xv[b].w), one2, xs);
+        const v8_t xa = __builtin_bit_cast(v8_t, xv[b]);
+        xs = dot2(as_pair<E>(xv[b].x), one2, xs); xs = dot2(as_pair<E>(xv[b].y), one2, xs);
+        xs = dot2(as_pair<E>(xv[b].z), one2, xs); xs = dot2(as_pair<E>(xv[b].w), one2, xs);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             uint32_t h[4][8];
@@ -679,15 +683,21 @@ gemv_awq_rows_kernel(GemvParams p) {
                 // bytes {a0, a1, b0, b1} and {a2, a3, b2, b3}: slots 0-3 / 4-7 of the two rows
                 const uint32_t lo = perm(bb, a, 0x05040100u), hi = perm(bb, a, 0x07060302u);
                 const uint32_t lo8 = lo >> 8, hi8 = hi >> 8;
-                h[i2][0] = as_u32(nib_pair(lo));   h[i2][1] = as_u32(nib_pair16(lo));
-                h[i2][2] = as_u32(nib_pair(lo8));  h[i2][3] = as_u32(nib_pair16(lo8));
-                h[i2][4] = as_u32(nib_pair(hi));   h[i2][5] = as_u32(nib_pair16(hi));
-                h[i2][6] = as_u32(nib_pair(hi8));  h[i2][7] = as_u32(nib_pair16(hi8));
+                if constexpr (BF) {
+                    auto bp = [](uint32_t v) { return __builtin_bit_cast(uint32_t, nib_pair_bf16(v)); };
+                    h[i2][0] = bp(lo);   h[i2][1] = bp(lo >> 4);  h[i2][2] = bp(lo8);  h[i2][3] = bp(lo8 >> 4);
+                    h[i2][4] = bp(hi);   h[i2][5] = bp(hi >> 4);  h[i2][6] = bp(hi8);  h[i2][7] = bp(hi8 >> 4);
+                } else {
+                    h[i2][0] = as_u32(nib_pair(lo));   h[i2][1] = as_u32(nib_pair16(lo));
+                    h[i2][2] = as_u32(nib_pair(lo8));  h[i2][3] = as_u32(nib_pair16(lo8));
+                    h[i2][4] = as_u32(nib_pair(hi));   h[i2][5] = as_u32(nib_pair16(hi));
+                    h[i2][6] = as_u32(nib_pair(hi8));  h[i2][7] = as_u32(nib_pair16(hi8));
+                }
             }
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const u32x4 bv = {h[0][s], h[1][s], h[2][s], h[3][s]};
-                acc[c][s] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, __builtin_bit_cast(half8_t, bv), acc[c][s], 0, 0, 0);
+                acc[c][s] = mfma16x16x32(xa, __builtin_bit_cast(v8_t, bv), acc[c][s]);
             }
         }
     }
@@ -703,18 +713,18 @@ gemv_awq_rows_kernel(GemvParams p) {
     for (int i = 0; i < 4; ++i) {
         const int m = 4 * kg + i;
         if (m >= M) continue;
-        const float X = Xr[i], X1024 = 1024.0f * Xr[i];
+        const float X = Xr[i], XB = pair2<E>::bias * Xr[i];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const half_t* sh = reinterpret_cast<const half_t*>(&sv[c]);
+            const E* sh = reinterpret_cast<const E*>(&sv[c]);
             float col[8];
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
                 const int n = awq_col_of_slot(s);
                 const float z = (float)nib(qz[c], s);
-                // odd slots were unpacked as 1024 + 16 q
-                const float u = (s & 1) ? __builtin_fmaf(acc[c][s][i] - X1024, 1.0f / 16.0f, -z * X)
-                                        : acc[c][s][i] - X1024 - z * X;
+                // fp16: odd slots were unpacked as 1024 + 16 q
+                const float u = (!BF && (s & 1)) ? __builtin_fmaf(acc[c][s][i] - XB, 1.0f / 16.0f, -z * X)
+                                                 : acc[c][s][i] - XB - z * X;
                 col[n] = (float)sh[n] * u;
             }
             float4* dst = reinterpret_cast<float4*>(&red[wave][m][8 * (2 * jw + c)]);
@@ -727,12 +737,12 @@ gemv_awq_rows_kernel(GemvParams p) {
     // ---- reduce over waves; split-K hand-off
     const int n0 = ct * C;
     if constexpr (FIX) {   // fixed-point hand-off (splitk.h): one atomic per entry, no reload
-        constexpr int T = 64 * W, E = (M * C + T - 1) / T;
-        size_t off[E];
-        float v[E];
+        constexpr int T = 64 * W, NE = (M * C + T - 1) / T;
+        size_t off[NE];
+        float v[NE];
         int n = 0;
 #pragma unroll
-        for (int e = 0; e < E; ++e) {
+        for (int e = 0; e < NE; ++e) {
             const int i = (int)threadIdx.x + e * T;
             if (i >= M * C) break;
             const int m = i / C, cidx = i - m * C;
@@ -743,7 +753,8 @@ gemv_awq_rows_kernel(GemvParams p) {
             v[e] = s;
             n = e + 1;
         }
-        splitk_fixed_commit<SC, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, p.out, off, v, n, split, p.splits);
+        splitk_fixed_commit<SC, NE, E>(p.slots, p.masks, p.ws, (size_t)M * p.N, reinterpret_cast<E*>(p.out),
+                                       off, v, n, split, p.splits);
     } else {
         for (int i = threadIdx.x; i < M * C; i += blockDim.x) {
             const int m = i / C, cidx = i - m * C;
@@ -751,12 +762,12 @@ gemv_awq_rows_kernel(GemvParams p) {
 #pragma unroll
             for (int r = 0; r < W; ++r) s += red[r][m][cidx];
             const size_t off = (size_t)m * p.N + n0 + cidx;
-            if (p.splits == 1) p.out[off] = (half_t)s;
+            if (p.splits == 1) reinterpret_cast<E*>(p.out)[off] = (E)s;
             else st_partial<SC>(p.ws + (size_t)split * M * p.N + off, s);
         }
         if (p.splits == 1) return;
         if (splitk_arrive(splitk_counter(p.counters, ct), p.splits, &flag))
-            splitk_finish<M, SC>(p.ws, p.out, p.splits, p.N, n0, C);
+            splitk_finish<M, SC, E>(p.ws, reinterpret_cast<E*>(p.out), p.splits, p.N, n0, C);
     }
 }
 
@@ -796,7 +807,7 @@ constexpr int AM_COLS = 128 * AM_CW, AM_ROWS = AM_R * AM_WAVES, AMW_ROWS = AMW_R
 constexpr int AR_MIN_M = 3, AR_WAVES = 8, AR_ROWS = 128 * AR_WAVES;
 }  // namespace
 
-GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bool valu_only) {
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bool bf16) {
     GemvShape s{};
     // AWQ: the row-paired matrix-core kernel for M = 3..8 where its tile fits (K a multiple of
     // 1024, groups of 128 rows or more); the block-diagonal matrix-core kernel for M = 2 and
@@ -809,7 +820,7 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bo
     const bool wide_fits = mfma_fits && K % AMW_ROWS == 0 && G % AMW_R == 0;
     const bool rows_fits = N % 256 == 0 && K % AR_ROWS == 0 && G % 128 == 0 && K % G == 0 &&
                            (size_t)K * N / 2 < ((size_t)1 << 31);
-    if (!valu_only && fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
+    if (fmt == FMT_AWQ && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && rows_fits) {
         s.ok = true; s.mfma = true; s.awq_rows = true; s.col_tiles = N / 256;
         // 4 waves (512-row workgroups) where 8 would leave fewer than 64 workgroups (graph
         // replays, one GPU's share of an 8-way tensor-parallel layer, K=4096 -> N=1792: M=4
@@ -817,7 +828,7 @@ GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bo
         const int w = (N / 256) * (K / AR_ROWS) < 64 ? AR_WAVES / 2 : AR_WAVES;
         s.splits = K / (128 * w);
         s.threads = 64 * w;
-    } else if (!valu_only && fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
+    } else if (!bf16 && fmt == FMT_AWQ && M >= 2 && M <= GEMV_MFMA_MAX_M && mfma_fits) {
         s.ok = true; s.mfma = true; s.mfma_wide = wide_fits; s.col_tiles = N / AM_COLS;
         s.splits = K / (wide_fits ? AMW_ROWS : AM_ROWS);
         s.threads = 64 * (wide_fits ? AMW_WAVES : AM_WAVES);
@@ -860,14 +871,14 @@ template <int M, bool XCD, bool FIX, typename E>
 static void launch_gemv_mx(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
     const dim3 block(s.threads);
-    constexpr bool H = std::is_same<E, half_t>::value;   // the matrix-core GEMVs are fp16 only
+    constexpr bool H = std::is_same<E, half_t>::value;   // the block-diagonal GEMV is fp16 only
     if (fmt == FMT_AWQ && s.mfma) {
-        if constexpr (H && M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
+        if constexpr (M >= AR_MIN_M && M <= GEMV_MFMA_MAX_M && !XCD) {
             if (s.awq_rows) {
                 if (s.threads == 64 * AR_WAVES)
-                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES, FIX, E>), grid, block, 0, st, p);
                 else
-                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES / 2, FIX>), grid, block, 0, st, p);
+                    hipLaunchKernelGGL((gemv_awq_rows_kernel<M, AR_WAVES / 2, FIX, E>), grid, block, 0, st, p);
                 return;
             }
         }
@@ -915,7 +926,7 @@ template <int M, typename E>
 static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st) {
     (void)hipGetLastError();  // launch errors below are ours, not an earlier call's
     if (M > GEMV_MAX_M && !(fmt == FMT_AWQ && s.mfma)) return hipErrorInvalidValue;
-    if (!std::is_same<E, half_t>::value && s.mfma) return hipErrorInvalidValue;
+    if (!std::is_same<E, half_t>::value && s.mfma && !s.awq_rows) return hipErrorInvalidValue;
     // the hand-off protocol is a template parameter: each kernel carries only the one it uses
     if (p.fixed) {
         if (s.xcd) launch_gemv_mx<M, true, true, E>(fmt, p, s, st);
@@ -928,12 +939,16 @@ static hipError_t launch_gemv_m(int fmt, const GemvParams& p, const GemvShape& s
 }
 
 hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st, bool bf16) {
-    if (bf16) {   // the VALU kernels (M <= GEMV_MAX_M)
+    if (bf16) {   // the VALU kernels and the row-paired AWQ kernel
         switch (p.M) {
             case 1: return launch_gemv_m<1, bf16_t>(fmt, p, s, st);
             case 2: return launch_gemv_m<2, bf16_t>(fmt, p, s, st);
             case 3: return launch_gemv_m<3, bf16_t>(fmt, p, s, st);
             case 4: return launch_gemv_m<4, bf16_t>(fmt, p, s, st);
+            case 5: return launch_gemv_m<5, bf16_t>(fmt, p, s, st);
+            case 6: return launch_gemv_m<6, bf16_t>(fmt, p, s, st);
+            case 7: return launch_gemv_m<7, bf16_t>(fmt, p, s, st);
+            case 8: return launch_gemv_m<8, bf16_t>(fmt, p, s, st);
             default: return hipErrorInvalidValue;
         }
     }

@@ -65,9 +65,9 @@ struct GemvShape {
 };
 
 // xcd_placement: the device hands workgroup b to XCD b mod 8 (check_xcd_placement).
-// valu_only: the VALU kernels only (bf16 elements: the matrix-core GEMVs are fp16)
-GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bool valu_only = false);
-// bf16: x, scales and out are bfloat16 (VALU kernels, M <= GEMV_MAX_M)
+// bf16: shapes for bfloat16 elements (no block-diagonal matrix-core GEMV, which is fp16 only)
+GemvShape gemv_shape(int fmt, int M, int N, int K, int G, bool xcd_placement, bool bf16 = false);
+// bf16: x, scales and out are bfloat16 (the VALU and row-paired AWQ kernels)
 hipError_t launch_gemv(int fmt, const GemvParams& p, const GemvShape& s, hipStream_t st, bool bf16 = false);
 // Runs a probe kernel on the current device and reports whether workgroups whose ids are
 // congruent mod 8 always share an XCD (synchronous; not for use under graph capture).
