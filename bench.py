@@ -449,13 +449,16 @@ def extras(torch, pkg, dev, stream, args):
                     "frac_mfma": round(tfl / FP16_DENSE_PEAK_TFLOPS, 4)}
         progress(f"{tag}: {res[tag]['us_per_call']} us")
 
-    def gemm_case(tag, fmt, M, K, N, G, n_sets, calls, g_idx=None):
+    def gemm_case(tag, fmt, M, K, N, G, n_sets, calls, g_idx=None, bf16=False):
         sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
-        x = torch.randn((M, K), device=dev, generator=gen).half()
-        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        dt = torch.bfloat16 if bf16 else torch.float16
+        if bf16:   # activations, scales and output in bfloat16 (W4A16_BF16)
+            sets = [(qw, sc.to(dt), qz) for qw, sc, qz in sets]
+        x = torch.randn((M, K), device=dev, generator=gen).to(dt)
+        out = torch.empty((M, N), dtype=dt, device=dev)
         # graph replays for every size: steady-state clocks, no host launch gaps
         ms = time_graphs(torch, pkg, x, sets, out, fmt, G, calls, 10, stream, g_idx=g_idx)
-        record(tag, fmt, M, K, N, G, ms, pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None),
+        record(tag, fmt, M, K, N, G, ms, pkg.plan(fmt, M, N, K, G, has_g_idx=g_idx is not None, bf16=bf16),
                act_order=g_idx is not None)
         del sets
 
@@ -525,6 +528,12 @@ def extras(torch, pkg, dev, stream, args):
 
     gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
     gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
+    # the same workloads with bfloat16 activations, scales and output
+    gemm_case("bf16_c0_gptq_sym_m1_k4096_n4096", "gptq_sym", 1, 4096, 4096, 128, 60, 1000, bf16=True)
+    for M in (1, 8):
+        gemm_case(f"bf16_c1_awq_m{M}_k4096_n14336", "awq", M, 4096, 14336, 128, 20, 1000, bf16=True)
+    gemm_case("bf16_c2_gptq_m16_k4096_n6144_no_gidx", "gptq", 16, 4096, 6144, 128, 40, 500, bf16=True)
+    gemm_case("bf16_c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300, bf16=True)
 
     # the prepared layout (w4a16_prepare_layout once per weight set, then w4a16_gemm_prepared);
     # the one-time prepare is timed on its own (one call, after a warm-up call)
