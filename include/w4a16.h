@@ -65,9 +65,9 @@ typedef enum { W4A16_FMT_GPTQ = 0, W4A16_FMT_GPTQ_SYM = 1, W4A16_FMT_AWQ = 2 } w
  * output is rounded to bf16 once. Plain group order runs the same kernels as fp16 (the
  * GEMVs, the small-batch kernel up to 64 rows, the pipelined prefill beyond; bf16 MFMA and
  * v_dot2c_f32_bf16) except the block-diagonal AWQ GEMV (GPTQ at 5..8 rows takes the
- * small-batch kernel); w4a16_gemm_plan reports which. Act-order and the shapes those kernels
- * reject run the generic kernel. The other entry points reject the flag as an unknown
- * format. */
+ * small-batch kernel); w4a16_gemm_plan reports which; act-order runs as for fp16. Shapes
+ * those kernels reject run the generic kernel. The other entry points reject
+ * the flag as an unknown format. */
 #define W4A16_BF16 0x100
 
 /* Kernel regimes reported by w4a16_gemm_plan(). */

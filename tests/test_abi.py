@@ -234,8 +234,8 @@ def test_prepared_kernels_isa(tmp_path):
 
 def test_bf16_flag_plans_and_is_refused_elsewhere():
     """W4A16_BF16 plans the VALU GEMV up to 4 rows, the small-batch kernel up to 64 and the
-    pipelined prefill beyond (plain group order, the shapes they take), the generic kernel for
-    act-order and other shapes; entry points without a bfloat16 instantiation report the
+    pipelined prefill beyond (act-order: the small-batch kernel, then the group-order prefill
+    route), the generic kernel for other shapes; entry points without a bfloat16 instantiation report the
     flagged value as an unknown format (no GPU call)."""
     P = pkg()
     L = P.lib()
@@ -253,8 +253,9 @@ def test_bf16_flag_plans_and_is_refused_elsewhere():
     # 5..8 rows: the row-paired AWQ GEMV, GPTQ the small-batch kernel
     assert plan(P.FMT_AWQ | P.BF16, 8, 4096, 14336) == "gemv"
     assert plan(P.FMT_GPTQ | P.BF16, 8, 4096, 14336) == "skinny"
-    assert plan(P.FMT_GPTQ | P.BF16, 16, 6144, 4096, gidx=1) == "strided"
-    assert plan(P.FMT_GPTQ | P.BF16, 2048, 6144, 4096, gidx=1) == "strided"
+    assert plan(P.FMT_GPTQ | P.BF16, 16, 6144, 4096, gidx=1) == "skinny"
+    assert plan(P.FMT_GPTQ | P.BF16, 2048, 6144, 4096, gidx=1) == "prefill"
+    assert plan(P.FMT_GPTQ | P.BF16, 33, 136, 384, gidx=1) == "strided"
     assert plan(P.FMT_AWQ, 1, 14336, 4096) == "gemv"
     assert L.w4a16_gemm_plan(P.FMT_AWQ | 0x200, 1, 512, 512, 128, 0, ctypes.byref(k)) == \
         P.ERR_INVALID_ARG

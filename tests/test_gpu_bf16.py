@@ -2,8 +2,8 @@
 against the oracle, GEMM outputs within the path's 1e-2 bar of the oracle's float64
 accumulation and bit-exact on inputs whose every product and partial sum is exact in fp32,
 on each kernel bf16 runs (VALU GEMV up to 4 rows, small-batch up to 64, pipelined prefill
-beyond, the generic kernel for act-order and other shapes; AWQ's row-paired matrix-core GEMV
-up to 8 rows). The reference kernels are generic over the element
+beyond, AWQ's row-paired matrix-core GEMV up to 8 rows; act-order on the small-batch kernel's
+group table and the group-order prefill route; the generic kernel for other shapes). The reference kernels are generic over the element
 type and name bf16 (w4a16_gptq_gemm_typed.rs:65-67)."""
 import numpy as np
 import pytest
@@ -125,17 +125,46 @@ def test_gemm_bf16_fast_paths_full_size(torch_cuda, orc, fmt, M, K, N, kernel):
     assert_parity(got, ref, what=f"bf16 {kernel} fmt={fmt} M={M} K={K} N={N}")
 
 
-def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc):
+@pytest.mark.parametrize("fmt,M,K,N,kernel", [(GPTQ, 16, 1024, 256, "skinny"),
+                                               (GPTQ, 16, 4096, 6144, "skinny"),   # config 2, bf16
+                                               (SYM, 64, 4096, 6144, "skinny"),
+                                               (GPTQ, 2048, 4096, 6144, "prefill"),
+                                               (GPTQ, 33, 384, 136, "strided")])
+def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc, fmt, M, K, N, kernel):
+    """bf16 act-order: the small-batch kernel's group table up to 64 rows, the group-order
+    prefill route beyond (per-call permutation, row repack and column gather), the generic
+    kernel for shapes neither takes; every row up to 16 rows, else 16 sampled rows."""
     torch = torch_cuda
-    p = Problem(GPTQ, M=16, K=1024, N=256, G=128, seed=730, act_order=True)
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=730 + M + fmt, act_order=True)
+    assert P.plan(FMT_NAME[fmt], M, N, K, p.G, has_g_idx=True, bf16=True) == kernel
+    x_bits = bf16_bits(torch, p.x.astype(np.float32))
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    y = P.gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
+               None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[fmt], group_size=p.G,
+               g_idx=to_dev(p.g_idx))
+    torch.cuda.synchronize()
+    rows = np.arange(M) if M <= 16 else np.random.default_rng(M).choice(M, 16, replace=False)
+    _, ref = orc.w4a16_gemm_bf16(fmt, x_bits[rows], p.qweight, s_bits, p.qzeros, K, N, p.G,
+                                 g_idx=p.g_idx)
+    assert_parity(y.float().cpu().numpy()[rows], ref, what=f"bf16 act-order {kernel} M={M}")
+
+
+def test_gemm_bf16_act_order_unequal_groups_runs_generic(torch_cuda, orc):
+    """Beyond 64 rows a g_idx whose groups do not each hold G rows fails the device-side
+    check of the prefill route, and the gated generic kernel runs in bf16."""
+    torch = torch_cuda
+    p = Problem(GPTQ, M=96, K=1024, N=256, G=128, seed=1337)
+    g_idx = np.random.default_rng(1337).integers(0, p.K // p.G, p.K).astype(np.int32)
+    g_idx[:5] = 0
     x_bits = bf16_bits(torch, p.x.astype(np.float32))
     s_bits = bf16_bits(torch, p.scales.astype(np.float32))
     y = pkg().gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
-                   to_dev(p.qzeros), fmt="gptq", group_size=p.G, g_idx=to_dev(p.g_idx))
+                   to_dev(p.qzeros), fmt="gptq", group_size=p.G, g_idx=to_dev(g_idx))
     torch.cuda.synchronize()
     _, ref = orc.w4a16_gemm_bf16(GPTQ, x_bits, p.qweight, s_bits, p.qzeros, p.K, p.N, p.G,
-                                 g_idx=p.g_idx)
-    assert_parity(y.float().cpu().numpy(), ref, what="bf16 act-order")
+                                 g_idx=g_idx)
+    assert_parity(y.float().cpu().numpy(), ref, what="bf16 act-order unequal groups")
 
 
 @pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])

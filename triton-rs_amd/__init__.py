@@ -268,8 +268,7 @@ def gemm(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
          g_idx: torch.Tensor | None = None, out: torch.Tensor | None = None,
          zero_offset: int = 1) -> torch.Tensor:
     """out[M, N] = x[M, K] @ dequant(qweight) with fp32 accumulation, in fp16 or, when x and
-    scales are bfloat16, in bfloat16 (the GEMV, small-batch and prefill kernels in plain group
-    order, the generic kernel with g_idx).
+    scales are bfloat16, in bfloat16 (the same kernels as fp16, act-order included).
 
     fmt: "gptq" (qweight int32 [K/8, N], qzeros [K/G, N/8], zero = nibble + zero_offset),
     "gptq_sym" (zero = 8, qzeros unused) or "awq" (qweight [K, N/8], AWQ nibble order).

@@ -186,9 +186,11 @@ static bool xcd_placement_cached() {
 
 // Act-order beyond the small-batch kernel: the per-call group order (act_order.hip) feeds the
 // prefill kernel; it needs K <= 32768 and at most 1024 groups.
-static bool act_order_prefill_ok(int fmt, int M, int N, int K, int G, int cus) {
-    return (fmt == W4A16_FMT_GPTQ || fmt == W4A16_FMT_GPTQ_SYM) && K <= 32768 && K % G == 0 &&
-           K / G <= 1024 && prefill_shape(fmt, M, N, K, G, cus).ok;
+static bool act_order_prefill_ok(int fmt, int M, int N, int K, int G, int cus, bool bf16 = false) {
+    if (!(fmt == W4A16_FMT_GPTQ || fmt == W4A16_FMT_GPTQ_SYM) || K > 32768 || K % G || K / G > 1024)
+        return false;
+    const PrefillShape ps = prefill_shape(fmt, M, N, K, G, cus);
+    return ps.ok && (!bf16 || ps.dma);   // bf16 runs the pipelined prefill only
 }
 
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
@@ -207,11 +209,15 @@ static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DE
 }
 
 // bfloat16 elements (W4A16_BF16): the VALU GEMVs (and the row-paired AWQ one up to 8 rows),
-// the small-batch kernel up to 64 and the pipelined prefill beyond, all in plain group order
-// on the checkpoint layouts; act-order and the shapes those kernels reject run the generic
-// kernel.
+// the small-batch kernel up to 64 and the pipelined prefill beyond, on the checkpoint
+// layouts; act-order as for fp16 (small-batch table, else the group-order prefill route); the
+// shapes those kernels reject run the generic kernel.
 static int plan_bf16(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
-    if (has_gidx) return W4A16_KERNEL_STRIDED;
+    if (has_gidx) {
+        const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus, true);
+        if (sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
+        return act_order_prefill_ok(fmt, M, N, K, G, cus, true) ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
+    }
     const GemvShape gv = gemv_shape(fmt, M, N, K, G, false, /*bf16=*/true);
     if (gv.ok && (size_t)gv.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_GEMV;
     const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus);

@@ -59,13 +59,12 @@ __device__ __forceinline__ half8_t cat8(half2_t a, half2_t b, half2_t c, half2_t
 // on the host where K allows); 0 for the default.
 // E: the element type of x, the scales and the output. With bf16 a weight is
 // RNE_bf16((q - z) * s) (deq2_bf16: exact fp32 product, one rounding) and the MFMA is the
-// bf16 one; act-order stays fp16 (its table holds fp16 zero points).
+// bf16 one; the act-order table then holds (bf16 scale | z << 16).
 template <int FMT, int BM, int CPL, int PF, int GIDX, bool XCD, int SPW, bool RG = false, int WV = 0,
           typename E = half_t>
 __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) skinny_kernel(SkinnyParams p) {
     constexpr bool BF = std::is_same<E, bf16_t>::value;
     typedef typename vec8<E>::type v8_t;
-    static_assert(!BF || !GIDX, "bf16: plain group order");
     static_assert(!RG || !GIDX, "one group per round needs plain group order");
     static_assert(!GIDX || FMT != FMT_AWQ, "act-order is a GPTQ layout");
     static_assert(CPL == 4 || (CPL == 2 && FMT != FMT_AWQ) || (CPL == 8 && FMT == FMT_AWQ),
@@ -82,7 +81,8 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
 
     __shared__ float red[RW][BM][WN + 1];
     __shared__ int flag;
-    // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16), then (GIDX = 2) the g_idx of the
+    // GIDX: [groups][WN] of (scale | fp16(1024 + z) << 16) (bf16: scale | z << 16), then
+    // (GIDX = 2) the g_idx of the
     // workgroup's W * spw * 32 rows
     extern __shared__ __attribute__((aligned(16))) uint32_t gtab[];   // 16-byte table accesses
 
@@ -208,7 +208,7 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
 #pragma unroll
         for (int i = 0; i < 8; ++i) {   // column n0 + 8 b + i: nibble i of its zero word
             const int z = (FMT == FMT_GPTQ_SYM) ? 8 : nib(zw, i) + p.zero_offset;
-            const uint32_t zf = __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
+            const uint32_t zf = BF ? (uint32_t)z : __builtin_bit_cast(uint16_t, (half_t)(1024 + z));
             const uint32_t sw = i < 2 ? sv.x : i < 4 ? sv.y : i < 6 ? sv.z : sv.w;
             e[i] = ((i & 1) ? (sw >> 16) : (sw & 0xFFFFu)) | (zf << 16);
         }
@@ -359,15 +359,29 @@ __global__ void __launch_bounds__(64 * (WV ? WV : skinny_waves(FMT, BM, CPL))) s
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 const uint32_t w = bw[u][c];
-                half2_t pr[4];
+                if constexpr (BF) {
+                    // each half with its own row's scale and zero point, exact fp32 products
+                    uint32_t pr[4];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    // the pair holds rows k_q (low half) and k_{q+4} (high half)
-                    const half2_t s2 = as_h2(perm(t[q + 4][c], t[q][c], 0x05040100u));
-                    const half2_t z2 = as_h2(perm(t[q + 4][c], t[q][c], 0x07060302u));
-                    pr[q] = deq2(nib_pair(w >> (4 * q)), z2, s2);
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t ea = t[q][c], eb = t[q + 4][c];
+                        const float sa = bf16_bits_to_f32(ea & 0xFFFFu), sb = bf16_bits_to_f32(eb & 0xFFFFu);
+                        const uint32_t x = (w >> (4 * q)) & 0x000F000Fu;
+                        pr[q] = pack2(bf16_t{}, __builtin_fmaf((float)(x & 0xFFu), sa, -(float)(ea >> 16) * sa),
+                                      __builtin_fmaf((float)(x >> 16), sb, -(float)(eb >> 16) * sb));
+                    }
+                    bf[c] = __builtin_bit_cast(v8_t, u32x4{pr[0], pr[1], pr[2], pr[3]});
+                } else {
+                    half2_t pr[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        // the pair holds rows k_q (low half) and k_{q+4} (high half)
+                        const half2_t s2 = as_h2(perm(t[q + 4][c], t[q][c], 0x05040100u));
+                        const half2_t z2 = as_h2(perm(t[q + 4][c], t[q][c], 0x07060302u));
+                        pr[q] = deq2(nib_pair(w >> (4 * q)), z2, s2);
+                    }
+                    bf[c] = cat8(pr[0], pr[1], pr[2], pr[3]);
                 }
-                bf[c] = cat8(pr[0], pr[1], pr[2], pr[3]);
             }
         } else {
 #pragma unroll
@@ -541,8 +555,7 @@ static hipError_t launch_xw(const SkinnyParams& p, const SkinnyShape& s, hipStre
     constexpr int PF = FMT == FMT_AWQ ? 3 : WV == 8 ? 2 : 4;
     constexpr int NTH = 64 * (WV ? WV : skinny_waves(FMT, BM, CPL));
     const dim3 grid = XCD ? dim3(s.col_tiles * s.splits) : dim3(s.col_tiles, s.splits);
-    if (p.g_idx && !std::is_same<E, half_t>::value) return hipErrorInvalidValue;   // fp16 only
-    if constexpr (FMT != FMT_AWQ && std::is_same<E, half_t>::value) {
+    if constexpr (FMT != FMT_AWQ) {
         if (p.g_idx) {
             // act-order waves with exactly one ring of steps run without a loop: the loop's
             // ring copies raise the kernel to 186 VGPRs, two waves per SIMD instead of three
@@ -556,11 +569,11 @@ static hipError_t launch_xw(const SkinnyParams& p, const SkinnyShape& s, hipStre
                 return hipGetLastError();
             };
             if (s.gidx_lds) {
-                if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, PF, false, WV>);
-                return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, 0, false, WV>);
+                if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, PF, false, WV, E>);
+                return go(&skinny_kernel<FMT, BM, CPL, PF, 2, XCD, 0, false, WV, E>);
             }
-            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, PF, false, WV>);
-            return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, 0, false, WV>);
+            if (s.steps_per_wave == PF) return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, PF, false, WV, E>);
+            return go(&skinny_kernel<FMT, BM, CPL, PF, 1, XCD, 0, false, WV, E>);
         }
     }
     if constexpr (FMT != FMT_AWQ) {

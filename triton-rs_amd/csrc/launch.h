@@ -172,7 +172,7 @@ constexpr size_t SKINNY_GIDX_MAX_LDS = 64 * 1024;
 
 SkinnyShape skinny_shape(int fmt, int M, int N, int K, int G, int num_cus, bool gidx = false,
                          bool xcd_placement = false);
-// bf16: x, scales and out are bfloat16 (plain group order only)
+// bf16: x, scales and out are bfloat16
 hipError_t launch_skinny(int fmt, const SkinnyParams& p, const SkinnyShape& s, hipStream_t st,
                          bool bf16 = false);
 
