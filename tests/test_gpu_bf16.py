@@ -150,6 +150,28 @@ def test_gemm_bf16_act_order_matches_oracle(torch_cuda, orc, fmt, M, K, N, kerne
     assert_parity(y.float().cpu().numpy()[rows], ref, what=f"bf16 act-order {kernel} M={M}")
 
 
+@pytest.mark.parametrize("fmt", [GPTQ, SYM, AWQ])
+@pytest.mark.parametrize("M,G,kernel", [(1, 32, "gemv"), (1, 64, "gemv"), (1, 256, "gemv"),
+                                        (4, 64, "gemv"), (6, 64, "skinny"), (16, 32, "skinny"),
+                                        (200, 64, "prefill"), (200, 256, "prefill")])
+def test_gemm_bf16_group_sizes(torch_cuda, orc, fmt, M, G, kernel):
+    """Group sizes 32 to 256 on each bf16 kernel (K = 2048, N = 512); 16 sampled rows at
+    M = 200."""
+    torch = torch_cuda
+    P = pkg()
+    K, N = 2048, 512
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=780 + M + G + fmt)
+    assert P.plan(FMT_NAME[fmt], M, N, K, G, bf16=True) == kernel
+    x_bits = bf16_bits(torch, p.x.astype(np.float32))
+    s_bits = bf16_bits(torch, p.scales.astype(np.float32))
+    y = P.gemm(bf16_dev(torch, x_bits), to_dev(p.qweight), bf16_dev(torch, s_bits),
+               None if p.qzeros is None else to_dev(p.qzeros), fmt=FMT_NAME[fmt], group_size=G)
+    torch.cuda.synchronize()
+    rows = np.arange(M) if M <= 16 else np.random.default_rng(G).choice(M, 16, replace=False)
+    _, ref = orc.w4a16_gemm_bf16(fmt, x_bits[rows], p.qweight, s_bits, p.qzeros, K, N, G)
+    assert_parity(y.float().cpu().numpy()[rows], ref, what=f"bf16 {kernel} fmt={fmt} M={M} G={G}")
+
+
 def test_gemm_bf16_act_order_unequal_groups_runs_generic(torch_cuda, orc):
     """Beyond 64 rows a g_idx whose groups do not each hold G rows fails the device-side
     check of the prefill route, and the gated generic kernel runs in bf16."""
