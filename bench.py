@@ -699,6 +699,49 @@ def achievable_refs(torch, dev, stream):
     return out
 
 
+def n_sweep(args) -> int:
+    """The headline kernel (prepared layout, M = 1, K = 4096, AWQ) at several N, timed as the
+    headline is (graph replays, median of 5 batches of 1000 calls, weight sets rotated over at
+    least 700 MB), then t = a + b N by least squares: a is the fixed cost of a call, b the
+    marginal cost per column, and bytes per column / b the marginal streaming rate."""
+    import numpy as np
+    import torch
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+    fmt, M, K, _, G = HEADLINE
+    ns_, ts_ = [], []
+    for N in (int(v) for v in args.n_sweep.split(",")):
+        per_set = algorithmic_bytes(fmt, M, K, N, G)
+        n_sets = max(8, int(700e6 // per_set) + 1)
+        sets = make_weight_sets(torch, fmt, K, N, G, n_sets, dev, seed=zlib.crc32(b"sweep%d" % N))
+        preps = [pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G) for qw, sc, qz in sets]
+        del sets
+        x = torch.randn((M, K), device=dev).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+        ms = time_calls(torch, lambda i: pkg.gemm_prepared(x, preps[i % n_sets], out=out), 2000, 50,
+                        stream, n_sets)[1]
+        ns_.append(N)
+        ts_.append(ms * 1e3)
+        print(f"N={N} strips={N // 16} per_cu={N / 16 / 256:.2f} us={ms * 1e3:.3f} "
+              f"GBps={per_set / (ms * 1e-3) / 1e9:.0f}", flush=True)
+        del preps
+        torch.cuda.empty_cache()
+    if len(ns_) >= 2:
+        n_arr, t_arr = np.array(ns_, dtype=float), np.array(ts_)
+        b, a = np.polyfit(n_arr, t_arr, 1)
+        per_col = algorithmic_bytes(fmt, M, K, 1000, G) / 1000.0   # x and out are per call
+        print(f"fit: t = {a:.3f} us + {b * 1e3:.4f} us per 1000 columns; marginal "
+              f"{per_col / (b * 1e-6) / 1e12:.2f} TB/s; residuals "
+              f"{np.round(t_arr - (a + b * n_arr), 3).tolist()}", flush=True)
+    tiny = torch.zeros(1, dtype=torch.int32, device=dev)
+    print(f"graph-replay floor of a one-element kernel: "
+          f"{time_calls(torch, lambda i: tiny.add_(1), 1000, 10, stream, 1)[1] * 1e3:.2f} us", flush=True)
+    return 0
+
+
 def dequant_then_mm_refs(torch, pkg, dev, stream, gen):
     """The unfused dense path at config 3's shapes: this library's dequantisation of the AWQ
     weights to fp16 [K, N], then torch's fp16 GEMM (hipBLASLt / rocBLAS), per call, against
@@ -746,6 +789,10 @@ def main() -> int:
     ap.add_argument("--headline-only", action="store_true",
                     help="time the headline and exit (no JSON line): for kernel-trace profiles "
                          "whose statistics should cover the cold headline dispatches only")
+    ap.add_argument("--n-sweep", default="",
+                    help="comma-separated N values: time the headline kernel (prepared layout, "
+                         "M=1, K=4096) at each N, fit fixed + per-column cost, and exit (no JSON "
+                         "line): the fixed and marginal cost of the headline call")
     ap.add_argument("--pmc-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--pmc-workload", default="headline", choices=sorted(PMC_WORKLOADS),
                     help="workload of a --pmc-child or --pmc-report run (for counter profiles)")
@@ -765,6 +812,9 @@ def main() -> int:
         return pmc_child(args)
     if args.pmc_report:
         return pmc_report(args)
+
+    if args.n_sweep:
+        return n_sweep(args)
 
     # counter passes run first, in child processes, before this process touches the GPU
     traffic, traffic_detail = (None, {"traffic_note": "skipped (--no-traffic)"})
