@@ -560,7 +560,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int W = blockDim.x >> 6;
-    const int col = lane & 15, h = lane >> 4;
+    const int col = lane & 15;
     const int NS = p.N >> 4, KB = p.K >> 7, M = p.M;
     const int s0 = blockIdx.x * S;
     const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
