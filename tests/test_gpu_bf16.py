@@ -218,16 +218,23 @@ def test_gemm_bf16_exact_inputs_bit_exact(torch_cuda, orc, fmt, M, K, N, G):
     assert np.array_equal(dev_bits(y), want)
 
 
-def test_noalloc_bf16_equals_gemm(torch_cuda):
+@pytest.mark.parametrize("fmt,M,K,N,kernel", [(AWQ, 4, 1024, 512, "gemv"),
+                                               (GPTQ, 16, 4096, 6144, "skinny"),
+                                               (SYM, 256, 8192, 1024, "prefill")])
+def test_noalloc_bf16_equals_gemm(torch_cuda, fmt, M, K, N, kernel):
+    """The allocation-free entry in bf16 runs the same kernels, with their K splits in its
+    fixed scratch area: bit-identical outputs."""
     torch = torch_cuda
     P = pkg()
-    p = Problem(AWQ, M=4, K=1024, N=512, G=128, seed=750)
+    p = Problem(fmt, M=M, K=K, N=N, G=128, seed=750 + M)
+    assert P.plan(FMT_NAME[fmt], M, N, K, 128, bf16=True) == kernel
     x = bf16_dev(torch, bf16_bits(torch, p.x.astype(np.float32)))
     s = bf16_dev(torch, bf16_bits(torch, p.scales.astype(np.float32)))
-    qw, qz = to_dev(p.qweight), to_dev(p.qzeros)
-    y = P.gemm(x, qw, s, qz, fmt="awq")
+    qw = to_dev(p.qweight)
+    qz = None if p.qzeros is None else to_dev(p.qzeros)
+    y = P.gemm(x, qw, s, qz, fmt=FMT_NAME[fmt])
     out = torch.empty_like(y)
-    P.gemm_noalloc(x, qw, s, qz, out, fmt="awq")
+    P.gemm_noalloc(x, qw, s, qz, out, fmt=FMT_NAME[fmt])
     torch.cuda.synchronize()
     assert np.array_equal(dev_bits(out), dev_bits(y))
 
