@@ -462,10 +462,13 @@ def test_act_order_identity_gidx_equals_plain(torch_cuda, M, K, N, G):
 
 
 @pytest.mark.parametrize("fmt,M,K,N,G", [(GPTQ, 100, 512, 256, 128), (SYM, 65, 1024, 384, 64),
-                                         (GPTQ, 300, 2048, 1024, 256), (GPTQ, 130, 4096, 224, 128)])
+                                         (GPTQ, 300, 2048, 1024, 256), (GPTQ, 130, 4096, 224, 128),
+                                         (GPTQ, 200, 6144, 512, 128), (GPTQ, 72, 8192, 1024, 64),
+                                         (GPTQ, 96, 16384, 256, 128), (GPTQ, 80, 1024, 224, 128)])
 def test_act_order_large_m_prefill(torch_cuda, orc, fmt, M, K, N, G):
     """Act-order beyond 64 rows through w4a16_gemm: the group order is computed on the device,
-    then the prefill kernel runs on the repacked rows and the gathered x."""
+    then the prefill kernel runs on the repacked rows and the gathered x (K from 512 to
+    16384, N from 224 to 1024, groups of 64 to 256 rows)."""
     p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1330 + M, act_order=True)
     assert pkg().plan(FMT_NAME[fmt], p.M, p.N, p.K, p.G, has_g_idx=True) == "prefill"
     y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
