@@ -35,19 +35,11 @@ gptq_repack_rows_kernel(const uint32_t* __restrict__ q, const int32_t* __restric
     qout[(size_t)jp * N + n] = w;
 }
 
-// Where output chunk c (columns 8 c .. 8 c + 7) of row m goes: row-major (frag_mt == 0), or
-// the MFMA fragment order of the prepared small-batch kernel (frag_mt = 16-row tiles, K % 128
-// == 0): 16-byte unit ((c / 16 * MT + m / 16) * 4 + c % 4) * 64 + m % 16 + 16 (c % 16 / 4).
-__device__ __forceinline__ size_t gather_dst(int m, int c, int K, int frag_mt) {
-    if (frag_mt == 0) return (size_t)m * (K / 8) + c;
-    return ((size_t)((c >> 4) * frag_mt + (m >> 4)) * 4 + (c & 3)) * 64 + (m & 15) + 16 * ((c >> 2) & 3);
-}
-
 // xout[m, j] = x[m, perm[j]] (perm entries outside [0, K) read column K - 1). Grid
-// (ceil(K / 2048), M), 256 threads x 8 columns. frag_mt > 0: fragment order (K % 8 == 0).
+// (ceil(K / 2048), M), 256 threads x 8 columns.
 __global__ void __launch_bounds__(256)
 gather_columns_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
-                      half_t* __restrict__ xout, int K, int frag_mt) {
+                      half_t* __restrict__ xout, int K) {
     const int j0 = (blockIdx.x * 256 + threadIdx.x) * 8;
     const size_t row = (size_t)blockIdx.y * K;
     if (j0 >= K) return;
@@ -55,8 +47,7 @@ gather_columns_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ 
         half8_t v;
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = x[row + min((uint32_t)perm[j0 + i], (uint32_t)K - 1u)];
-        if (frag_mt) reinterpret_cast<half8_t*>(xout)[gather_dst(blockIdx.y, j0 / 8, K, frag_mt)] = v;
-        else *reinterpret_cast<half8_t*>(xout + row + j0) = v;
+        *reinterpret_cast<half8_t*>(xout + row + j0) = v;
     } else {
         for (int j = j0; j < K; ++j) xout[row + j] = x[row + min((uint32_t)perm[j], (uint32_t)K - 1u)];
     }
@@ -71,7 +62,7 @@ constexpr int GATHER_LDS_MAX_K = 32768;   // 64 KiB of LDS
 
 __global__ void __launch_bounds__(256)
 gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restrict__ perm,
-                          half_t* __restrict__ xout, int K, int per, int frag_mt) {
+                          half_t* __restrict__ xout, int K, int per) {
     extern __shared__ __attribute__((aligned(16))) half_t row_s[];
     const size_t row = (size_t)blockIdx.x * K;
     const int chunks = K / 8;
@@ -79,7 +70,7 @@ gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restric
     for (int c = threadIdx.x; c < chunks; c += 256) reinterpret_cast<u32x4*>(row_s)[c] = src[c];
     __syncthreads();
     const u32x4* pp = reinterpret_cast<const u32x4*>(perm);
-    u32x4* dst = reinterpret_cast<u32x4*>(frag_mt ? xout : xout + row);
+    u32x4* dst = reinterpret_cast<u32x4*>(xout + row);
     const uint32_t last = (uint32_t)K - 1u;
     // this workgroup's share of the row's 8-column output chunks
     const int c_end = min(chunks, ((int)blockIdx.y + 1) * per);
@@ -89,7 +80,7 @@ gather_columns_lds_kernel(const half_t* __restrict__ x, const int32_t* __restric
         half8_t v;
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = row_s[min(idx[i], last)];
-        dst[frag_mt ? gather_dst(blockIdx.x, c, K, frag_mt) : c] = __builtin_bit_cast(u32x4, v);
+        dst[c] = __builtin_bit_cast(u32x4, v);
     }
 }
 
@@ -194,11 +185,8 @@ hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint3
 }
 
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
-                                 hipStream_t st, bool frag) {
+                                 hipStream_t st) {
     (void)hipGetLastError();
-    // fragment order: M <= 64 rows (one launch), K % 128 == 0
-    if (frag && (M > 64 || K % 128)) return hipErrorInvalidValue;
-    const int frag_mt = frag ? (M + 15) / 16 : 0;
     const bool lds_ok = K % 8 == 0 && K <= GATHER_LDS_MAX_K &&
                         reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                         reinterpret_cast<uintptr_t>(perm) % 16 == 0 &&
@@ -214,7 +202,7 @@ hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* x
             const int per = (chunks + share - 1) / share;
             hipLaunchKernelGGL(gather_columns_lds_kernel, dim3(rows, (chunks + per - 1) / per),
                                dim3(256), (size_t)K * sizeof(half_t), st, x + (size_t)m0 * K,
-                               perm, xout + (size_t)m0 * K, K, per, frag_mt);
+                               perm, xout + (size_t)m0 * K, K, per);
         }
         return hipGetLastError();
     }
@@ -222,7 +210,7 @@ hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* x
     for (int m0 = 0; m0 < M; m0 += MAX_ROWS) {
         const int rows = M - m0 < MAX_ROWS ? M - m0 : MAX_ROWS;
         hipLaunchKernelGGL(gather_columns_kernel, dim3((K + 2047) / 2048, rows), dim3(256), 0, st,
-                           x + (size_t)m0 * K, perm, xout + (size_t)m0 * K, K, frag_mt);
+                           x + (size_t)m0 * K, perm, xout + (size_t)m0 * K, K);
     }
     return hipGetLastError();
 }

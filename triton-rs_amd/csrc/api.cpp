@@ -613,19 +613,22 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
                     "x, out and perm must be 16-byte aligned, prepared 256-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     // 2..64 rows (5..64 without act-order, where the rows kernel needs no pass over x): the
-    // small-batch kernel, with x (gathered by perm for act-order) rewritten in MFMA fragment
-    // order first
+    // small-batch kernel, reading x as stored (act-order: x's columns gathered by perm first)
+    // and putting it in MFMA fragment order itself
     const PrepFragShape fs = prep_frag_shape(M, N, K, G);
     if (fs.ok && (perm ? M >= 2 : M >= 5)) {
-        void* xf = nullptr;
-        int rc = stream_buffer(g_gather, st, xfrag_bytes(M, K), 0, "fragment-order activations", &xf);
-        if (rc) return rc;
-        hipError_t e = perm ? launch_gather_columns(static_cast<const half_t*>(x), perm, static_cast<half_t*>(xf),
-                                                    M, K, st, /*frag=*/true)
-                            : launch_xfrag(static_cast<const half_t*>(x), static_cast<half_t*>(xf), M, K, st);
-        if (e != hipSuccess) return hip_fail(e, perm ? "act-order gather launch" : "fragment-order launch");
+        const void* xa = x;
+        hipError_t e = hipSuccess;
+        if (perm) {
+            void* xg = nullptr;
+            int rc = stream_buffer(g_gather, st, (size_t)M * K * sizeof(half_t), 0, "act-order gather buffer", &xg);
+            if (rc) return rc;
+            e = launch_gather_columns(static_cast<const half_t*>(x), perm, static_cast<half_t*>(xg), M, K, st);
+            if (e != hipSuccess) return hip_fail(e, "act-order gather launch");
+            xa = xg;
+        }
         PrepFragParams p{};
-        p.xfrag = static_cast<const half_t*>(xf);
+        p.x = static_cast<const half_t*>(xa);
         p.prep = static_cast<const unsigned char*>(prepared);
         p.out = static_cast<half_t*>(out);
         p.M = M; p.N = N; p.K = K; p.G = G;

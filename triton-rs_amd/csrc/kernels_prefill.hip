@@ -313,6 +313,41 @@ size_t prefill_dma_lds(int bm, int bn) {
 
 constexpr int PF_THREADS = 512;   // 8 waves: 4 along M x 2 along N
 
+// XCD-grouped order of an expert-tile grid. The dispatcher hands workgroup b of a launch to
+// XCD b mod 8, so a grid in the natural order (column tiles fastest) spreads every expert's
+// tile over all eight XCDs, and each XCD's L2 then fetches every expert's activation rows
+// (the down projection moved twice its bytes that way). Here the 1-D grid of
+// gx * round_up(max_tiles, 8) * gz workgroups is dealt out in units of one expert tile's
+// columns, or of 1/c of them: with nt tiles, c = 8 / gcd(nt, 8), so the nt * c units fill
+// the eight XCDs evenly, unit u going to XCD u mod 8 and each XCD taking its units one
+// after another, all column tiles and K splits of a unit together. A unit's activation rows
+// are then fetched into one L2 and reused there by its column tiles. Placement only: the
+// results do not depend on it. Returns false for a workgroup with no unit (it exits).
+__device__ __forceinline__ bool xcd_tile_of_block(int gx, int gz, int max_tiles, int nt,
+                                                  int& bx, int& by, int& bz) {
+    const int L = blockIdx.x;
+    const int gyp = (max_tiles + 7) & ~7;
+    nt = min(nt, max_tiles);
+    if (nt <= 0) return false;
+    const int low = nt & -nt;
+    const int c = 8 / (low < 8 ? low : 8);
+    if (gx % c) {   // units would split a column tile: the natural order over the 1-D grid
+        bx = L % gx;
+        by = (L / gx) % gyp;
+        bz = L / (gx * gyp);
+        return by < nt;
+    }
+    const int cw = gx / c, W = cw * gz;   // column tiles per unit, workgroups per unit
+    const int slot = L >> 3, i = slot / W;
+    if (i >= nt * c / 8) return false;
+    const int u = (L & 7) + 8 * i;
+    by = u / c;
+    const int w = slot - i * W;
+    bz = w / cw;
+    bx = (u - by * c) * cw + (w - bz * cw);
+    return true;
+}
+
 // E: the element type of x, the scales and the output. With bf16 (dense checkpoint layouts)
 // a weight is RNE_bf16((q - z) * s) (deq2_bf16) and the MFMA is the bf16 one.
 template <int FMT, int BM, int BN, bool MOE, typename E = half_t>
@@ -338,26 +373,34 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
     const int lane = t & 63, wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int wm = wave / WGN, wn = wave % WGN;
     const int j = lane & 15, kb = lane >> 4;
-    int m0 = blockIdx.y * BM, rows = BM;
+    const int ksp = max(p.ksplit, 1);
+    // (column tile, row tile, K split) of this workgroup: the grid's own coordinates, or in
+    // the XCD-grouped expert-tile order a 1-D grid dealt out by xcd_tile_of_block
+    int bx = blockIdx.x, by = blockIdx.y, bz = blockIdx.z;
+    if constexpr (MOE) {
+        if (p.tiles && p.xcd_tiles > 0 &&
+            !xcd_tile_of_block(p.N / BN, ksp, p.xcd_tiles, *p.num_tiles, bx, by, bz))
+            return;
+    }
+    int m0 = by * BM, rows = BM;
     (void)rows;
-    const int n0 = blockIdx.x * BN;
+    const int n0 = bx * BN;
     const int NW = p.N >> 3;
     // split K: this workgroup's K stages are [s0, s0 + ns)
-    const int ksp = max(p.ksplit, 1);
     const int ns = p.K / BK / ksp;
-    const int s0 = (int)blockIdx.z * ns;
+    const int s0 = bz * ns;
 
     if constexpr (MOE) {
         int e;
         if (p.tiles) {   // expert tile: rows past its height are masked like padding
-            if ((int)blockIdx.y >= *p.num_tiles) return;
-            const int32_t* td = p.tiles + 4 * blockIdx.y;
+            if (by >= *p.num_tiles) return;
+            const int32_t* td = p.tiles + 4 * by;
             m0 = td[0];
             rows = td[1];
             e = td[2];
         } else {
             if (m0 >= *p.num_post_padded) return;
-            e = p.expert_ids[blockIdx.y];
+            e = p.expert_ids[by];
             if ((unsigned)e >= (unsigned)p.num_experts) return;   // caller data out of range
         }
         p.qweight += (size_t)e * p.qweight_stride;
@@ -698,7 +741,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
         // writes the fp16 tile
         __shared__ int last_flag;
         const size_t MN = (size_t)(MOE ? p.num_pairs : p.M) * p.N;
-        float* mine = p.ws + (size_t)blockIdx.z * MN;
+        float* mine = p.ws + (size_t)bz * MN;
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
@@ -709,7 +752,7 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
                 for (int c = 0; c < CB; ++c) st_partial<SCOPE_DEVICE>(dst + 16 * c, acc[r][c][i]);
             }
-        const int tile = (int)blockIdx.y * (int)gridDim.x + (int)blockIdx.x;
+        const int tile = by * (p.N / BN) + bx;
         if (!splitk_arrive(splitk_counter(p.counters, tile), ksp, &last_flag)) return;
         constexpr int C4 = BN / 4;
         const int nrows = MOE ? rows : min(BM, p.M - m0);
@@ -927,7 +970,11 @@ hipError_t launch_moe_gemm_tiles(int fmt, const PrefillParams& p, int tile_bm, i
     if (p.ksplit > 1 && (!p.ws || !p.counters || (p.K / BK) % p.ksplit ||
                          (size_t)(p.N / bn) * max_tiles > SPLITK_MAX_TILES))
         return hipErrorInvalidValue;
-    return launch_dma_any<true>(fmt, p, tile_bm, bn, dim3(p.N / bn, max_tiles, max(p.ksplit, 1)),
+    PrefillParams q = p;
+    q.xcd_tiles = max_tiles;   // XCD-grouped order (xcd_tile_of_block) over a 1-D grid
+    const int gyp = (max_tiles + 7) & ~7;
+    return launch_dma_any<true>(fmt, q, tile_bm, bn,
+                                dim3((p.N / bn) * gyp * max(p.ksplit, 1)),
                                 prefill_dma_lds(tile_bm, bn), st);
 }
 

@@ -102,6 +102,9 @@ struct PrefillParams {
     // on the stream wrote); otherwise every workgroup returns at once
     const uint32_t* gate;
     uint32_t gate_want;
+    // expert-tile mode: > 0 selects the XCD-grouped workgroup order over a 1-D grid and is
+    // the grid's bound on tiles (set by launch_moe_gemm_tiles)
+    int xcd_tiles;
 };
 
 struct PrefillShape {
@@ -210,9 +213,7 @@ struct DequantParams {
 hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st, bool bf16 = false);
 
 // Act-order in group order (act_order.hip): qout = rows of the GPTQ qweight q [K/8, N] taken
-// in the order perm (row j of qout = row perm[j] of q); xout [M, K] = x[:, perm], or with
-// frag (M <= 64, K % 128 == 0) x[:, perm] in the fragment order of the prepared small-batch
-// kernel (xfrag_bytes(M, K) bytes).
+// in the order perm (row j of qout = row perm[j] of q); xout [M, K] = x[:, perm].
 hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
                                    int N, hipStream_t st);
 // perm (K entries) of the rows in group order, computed on the device from g_idx, and gate[0] =
@@ -221,7 +222,7 @@ hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint3
 hipError_t launch_act_order_perm(const int32_t* g_idx, int32_t* perm, uint32_t* gate, int K, int G,
                                  hipStream_t st);
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
-                                 hipStream_t st, bool frag = false);
+                                 hipStream_t st);
 
 // Prepared layout (prepared.hip): strips of 16 columns, each one contiguous run of
 // prep_strip_bytes(K, G) bytes: the strip's table (per block of 128 rows, R = max(1, 128/G)
@@ -257,7 +258,7 @@ constexpr int PREP_GEMV_MAX_M = 8;
 // M <= 64 on the prepared layout (G % 128 == 0) with the activations in MFMA fragment order
 // (prepared.hip): one workgroup per S strips, its waves over K.
 struct PrepFragParams {
-    const half_t* xfrag;          // x [M, K] in fragment order: (K / 128) * MT * 4 KiB
+    const half_t* x;              // x [M, K], row-major
     const unsigned char* prep;    // prepared weights (fewer than 2^31 bytes)
     half_t* out;                  // [M, N]
     int M, N, K, G;
@@ -273,7 +274,6 @@ struct PrepFragShape {
     size_t lds;   // dynamic LDS bytes
 };
 constexpr int PREP_FRAG_MAX_M = 64;
-inline size_t xfrag_bytes(int M, int K) { return (size_t)(K / 128) * ((M + 15) / 16) * 4096; }
 hipError_t launch_prepare_layout(int fmt, const uint32_t* qweight, const half_t* scales,
                                  const uint32_t* qzeros, void* out, int K, int N, int G,
                                  int zero_offset, hipStream_t st);
@@ -283,7 +283,6 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G);
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st);
 PrepFragShape prep_frag_shape(int M, int N, int K, int G);
 hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
-hipError_t launch_xfrag(const half_t* x, half_t* xf, int M, int K, hipStream_t st);
 
 // ------------------------------------------------------------------ op layer (api.cpp)
 

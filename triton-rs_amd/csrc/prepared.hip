@@ -30,6 +30,7 @@
 // 16 columns: the GEMV needs no split-K hand-off at all.
 #include "device_common.h"
 #include "launch.h"
+#include "lds_dma.h"
 
 namespace w4a16 {
 
@@ -539,23 +540,98 @@ gemv_prep_rows_kernel(PrepParams p) {
     }
 }
 
-// M <= 64 with the activations in MFMA fragment order (xfrag, written by launch_xfrag or by
-// the act-order gather): A operand st of 16-row tile tt of block kb is 1 KiB at
-// ((kb * MT + tt) * 4 + st) KiB, lane l's 16 bytes holding x at row 16 tt + l % 16 and rows
-// 128 kb + 32 (l / 16) + 8 st + [0, 8). A wave's A loads are then whole cache lines, and lanes
-// whose row is >= M load nothing (the tile's padding rows are never read or written).
+// M <= 64 (small batches): A operand st of 16-row tile tt of block kb holds, in lane l, x at
+// row 16 tt + l % 16 and rows 128 kb + 32 (l / 16) + 8 st + [0, 8), the rows the prepared
+// word st of lane l covers on the B side. Rows of a tile past M are zero.
 //
 // One workgroup owns S strips over the whole K range: wave w takes blocks w BPW .. w BPW +
-// BPW - 1 (so no split-K hand-off and no partial sums leave the CU); its table entries,
-// activations and weights run PD blocks ahead of its MFMAs. Per block and strip, B = word st
-// of the lane's 16 bytes as eight fp16 q - z: ((w >> 4 i) & 0x000F000F | 0x64006400) -
-// (1024 + z) is exact; one chain of four MFMAs per 16-row tile gives D = sum_k x_k (q_k - z)
-// over the block, and y += s D. The waves' sums meet in LDS and are added in wave order.
+// BPW - 1 (so no split-K hand-off and no partial sums leave the CU); its table entries and
+// weights run PD blocks ahead of its MFMAs. Per block and strip, B = word st of the lane's
+// 16 bytes as eight fp16 q - z: ((w >> 4 i) & 0x000F000F | 0x64006400) - (1024 + z) is exact;
+// one chain of four MFMAs per 16-row tile gives D = sum_k x_k (q_k - z) over the block, and
+// y += s D. The waves' sums meet in LDS and are added in wave order.
 // Requires G % 128 == 0 and fewer than 2^31 bytes of prepared weights.
-template <int MT, int S, int BPW, int PD>
+//
+// x is read as stored ([M, K], row-major) and put in that order on the way into LDS, so no
+// pass over x runs before the kernel. Per block and 16-row tile a wave issues four
+// LDS-DMA loads of 1 KiB (buffer_load_dwordx4 ... lds: lane i's 16 bytes land at the wave's
+// base + 16 i), load q covering rows 4 q .. 4 q + 3 of the tile: lane i reads row
+// r = 4 q + i / 16, chunk c = (i % 16) ^ r of the block's 256 bytes (chunk c: the row's x at
+// 8 c .. 8 c + 7), so each load is four whole 256-byte row segments and chunk c of row r sits
+// at r * 256 + (c ^ r) * 16 of the tile's 4 KiB. The A operand of step st is chunk
+// 4 (l / 16) + st of row l % 16: one ds_read_b128 per lane, the 16 lanes of a row group at 16
+// distinct positions (no bank conflicts).
+// The x loads go through the compiler's buffer-load-to-LDS builtin, so its own waits for the
+// table and weight loads count them; it does not order LDS reads after them, so the kernel
+// waits for them itself (vmcnt: the loads issued after a block's x loads may still be in
+// flight) before reading a block's x.
+//   XD = 1 (one 16-row tile, every block of the wave loaded up front, PD = BPW): all the x
+//   loads go first, then the table and weight loads; one wait (vmcnt 2 S BPW) precedes the
+//   first LDS read.
+//   XD = 2 (any tile count): R = xd_slots(MT) slots of MT x 4 KiB per wave, x running R
+//   blocks ahead: block j + R's x is loaded into block j's slot as soon as block j's A
+//   operands are in registers (lgkmcnt(0) first), and block j's wait counts the loads issued
+//   after its x loads (xd_after).
+// Slots of x per wave in the streamed XD mode: 4 KiB per tile and slot, 8 waves at most
+constexpr int xd_slots(int MT) { return MT == 1 ? 4 : MT == 2 ? 2 : 1; }
+
+// Streamed XD mode: VMEM loads issued after block j's x loads by the time block j is read.
+// Issue order: the x of blocks 0 .. R - 1, then the table and weight loads (lops each) of
+// blocks 0 .. PD - 1; iteration i then issues the x of block i + R (dops loads) and the
+// table and weights of block i + PD, each while that block exists.
+constexpr int xd_after(int j, int R, int PD, int BPW, int dops, int lops) {
+    int n = 0, i = 0;
+    if (j < R) {
+        n = ((R < BPW ? R : BPW) - 1 - j) * dops + PD * lops;
+    } else {
+        if (j - R + PD < BPW) n = lops;
+        i = j - R + 1;
+    }
+    for (; i < j; ++i) {
+        if (i + R < BPW) n += dops;
+        if (i + PD < BPW) n += lops;
+    }
+    return n < 0 ? 0 : n < 63 ? n : 63;
+}
+
+// s_waitcnt vmcnt(xd_after(j, ...)) for a j that is a constant once the caller's loop is
+// unrolled: the count is the same for every block from R until R + PD blocks before the end,
+// so a few branches (folded away per iteration) cover every j. R, PD <= 4.
+template <int R, int PD, int BPW, int DOPS, int LOPS>
+__device__ __forceinline__ void xd_wait(const int j) {
+    static_assert(R <= 4 && PD <= 4, "xd_wait cases");
+#define W4A16_XDW(jj) wait_vmcnt<xd_after((jj), R, PD, BPW, DOPS, LOPS)>()
+    if (j < R) {
+        switch (j) {
+            case 0: W4A16_XDW(0); break;
+            case 1: W4A16_XDW(1); break;
+            case 2: W4A16_XDW(2); break;
+            default: W4A16_XDW(3); break;
+        }
+    } else if (j < BPW - R - PD) {
+        W4A16_XDW(R);
+    } else {
+        switch (BPW - 1 - j) {
+            case 0: W4A16_XDW(BPW - 1); break;
+            case 1: W4A16_XDW(BPW - 2); break;
+            case 2: W4A16_XDW(BPW - 3); break;
+            case 3: W4A16_XDW(BPW - 4); break;
+            case 4: W4A16_XDW(BPW - 5); break;
+            case 5: W4A16_XDW(BPW - 6); break;
+            case 6: W4A16_XDW(BPW - 7); break;
+            default: W4A16_XDW(BPW - 8); break;
+        }
+    }
+#undef W4A16_XDW
+}
+
+template <int MT, int S, int BPW, int PD, int XD>
 __global__ void __launch_bounds__(512)
 gemm_prep_frag_kernel(PrepFragParams p) {
     static_assert(PD >= 1 && PD <= BPW, "prefetch depth");
+    static_assert(XD == 2 || (XD == 1 && MT == 1 && PD == BPW && 2 * S * BPW <= 63),
+                  "XD 1: one tile, all blocks up front");
+    constexpr int R = XD == 2 ? xd_slots(MT) : 1;   // XD 2: slots of x per wave
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -565,12 +641,14 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     const int s0 = blockIdx.x * S;
     const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
     const uint32_t pbytes = (uint32_t)NS * p.strip_bytes;
-    const uint32_t xbytes = (uint32_t)KB * MT * 4096u;
     const bufrsrc_t pr = make_rsrc(p.prep, pbytes);
-    const bufrsrc_t xr = make_rsrc(p.xfrag, xbytes);
+    const bufrsrc_t xrs = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
+    // XD 1: the wave's x, block j at 4 KiB j; XD 2: its R slots, block j's tile tt at
+    // ((j % R) MT + tt) 4 KiB
+    unsigned char* xw = lds + (size_t)wave * (XD == 1 ? BPW * 4096 : R * MT * 4096);
 
     uint32_t ev[BPW][S];
-    u32x4 av[BPW][MT][4], wv[BPW][S];
+    u32x4 wv[BPW][S];
     auto load = [&](const int j) __attribute__((always_inline)) {
         const int kb = wave * BPW + j;
         const bool kin = kb < KB;
@@ -582,14 +660,6 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             ev[j][s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 2);
         }
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt)
-#pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const uint32_t off = kin && 16 * tt + col < M ? (uint32_t)(((kb * MT + tt) * 4 + st) * 1024 + lane * 16)
-                                                              : xbytes;
-                av[j][tt][st] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
-            }
-#pragma unroll
         for (int s = 0; s < S; ++s) {
             const int strip = s0 + s;
             const uint32_t off = kin && strip < NS
@@ -598,8 +668,39 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             wv[j][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 2));
         }
     };
+    // block j's x (XD): MT tiles of 4 KiB from dst. The loads go through the compiler's
+    // buffer-load-to-LDS builtin, so its own waits for the table and weight loads count them;
+    // it does not order LDS reads after them (the kernel's waits below do), and the empty asm
+    // statements keep the loads in the issue order those waits count.
+    auto dma_x = [&](const int j, unsigned char* dst) __attribute__((always_inline)) {
+        const int kb = wave * BPW + j;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = 4 * q + (lane >> 4), m = 16 * tt + r;
+                const int c = (lane & 15) ^ r;
+                const uint32_t off = kb < KB && m < M ? (uint32_t)(m * p.K + kb * 128 + 8 * c) * 2u : DMA_OOB;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    xrs, (__attribute__((address_space(3))) void*)(dst + tt * 4096 + q * 1024), 16, (int)off, 0, 0, 0);
+            }
+        asm volatile("" ::: "memory");
+    };
+    if constexpr (XD == 1) {
+#pragma unroll
+        for (int j = 0; j < BPW; ++j) dma_x(j, xw + j * 4096);
+    }
+    if constexpr (XD == 2) {
+#pragma unroll
+        for (int j = 0; j < (R < BPW ? R : BPW); ++j) dma_x(j, xw + j * MT * 4096);
+    }
 #pragma unroll
     for (int j = 0; j < PD; ++j) load(j);
+    if constexpr (XD == 1) {
+        wait_vmcnt<2 * S * BPW>();          // the x loads, issued before every other load
+        asm volatile("" ::: "memory");      // the LDS reads below stay after the wait
+    }
 
     float acc[S][MT][4];
 #pragma unroll
@@ -610,7 +711,30 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             for (int i = 0; i < 4; ++i) acc[s][tt][i] = 0.f;
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
+        u32x4 A[MT][4];
+        const int r = lane & 15, h = lane >> 4;
+        if constexpr (XD == 2) {
+            // block j's x loads are done once only the loads issued after them remain
+            xd_wait<R, PD, BPW, 4 * MT, 2 * S>(j);
+            asm volatile("" ::: "memory");   // the LDS reads below stay after the wait
+            const int slot = j % R;
+#pragma unroll
+            for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+                for (int st = 0; st < 4; ++st)
+                    A[tt][st] = *reinterpret_cast<const u32x4*>(xw + (slot * MT + tt) * 4096 + r * 256 +
+                                                                (((4 * h + st) ^ r) << 4));
+            if (j + R < BPW) {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the slot's reads are done
+                dma_x(j + R, xw + slot * MT * 4096);
+            }
+        }
         if (j + PD < BPW) load(j + PD);
+        if constexpr (XD == 1) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st)
+                A[0][st] = *reinterpret_cast<const u32x4*>(xw + j * 4096 + r * 256 + (((4 * h + st) ^ r) << 4));
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const uint32_t e = ev[j][s];
@@ -629,7 +753,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
                 float4_t d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st)
-                    d = mfma16x16x32(__builtin_bit_cast(half8_t, av[j][tt][st]), B[st], d);
+                    d = mfma16x16x32(__builtin_bit_cast(half8_t, A[tt][st]), B[st], d);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[s][tt][i] = __builtin_fmaf(sc, d[i], acc[s][tt][i]);
             }
@@ -638,6 +762,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
 
     // ---- the waves' sums, added in wave order; lane l of tile tt holds rows 16 tt + 4 (l / 16)
     // + i of column l % 16
+    __syncthreads();   // the sums overwrite other waves' x
     float4_t* red = reinterpret_cast<float4_t*>(lds);
 #pragma unroll
     for (int s = 0; s < S; ++s)
@@ -654,24 +779,6 @@ gemm_prep_frag_kernel(PrepFragParams p) {
         for (int w = 0; w < W; ++w) a += rf[w * S * MT * 256 + o];
         p.out[(size_t)m * p.N + strip * 16 + (l & 15)] = (half_t)a;
     }
-}
-
-// x [M, K] -> fragment order (see gemm_prep_frag_kernel): grid (K / 128, MT), 256 threads;
-// thread t writes lane t % 64 of step t / 64. Rows past M are left unwritten.
-__global__ void __launch_bounds__(256)
-xfrag_kernel(const half_t* __restrict__ x, half_t* __restrict__ xf, int M, int K) {
-    const int kb = blockIdx.x, tt = blockIdx.y, MT = gridDim.y;
-    const int t = threadIdx.x, lane = t & 63, st = t >> 6;
-    const int m = 16 * tt + (lane & 15);
-    if (m >= M) return;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(x + (size_t)m * K + kb * 128 + 32 * (lane >> 4) + 8 * st);
-    *reinterpret_cast<u32x4*>(xf + ((size_t)((kb * MT + tt) * 4 + st) * 64 + lane) * 8) = v;
-}
-
-hipError_t launch_xfrag(const half_t* x, half_t* xf, int M, int K, hipStream_t st) {
-    (void)hipGetLastError();
-    hipLaunchKernelGGL(xfrag_kernel, dim3(K / 128, (M + 15) / 16), dim3(256), 0, st, x, xf, M, K);
-    return hipGetLastError();
 }
 
 PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
@@ -728,7 +835,12 @@ PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
     for (int c = s.mt <= 2 && s.bpw <= 16 ? 4 : 2; c > 1; c /= 2)
         if (NS / c >= 192) { s.s = c; break; }
     s.pd = s.mt == 1 ? (s.bpw == 4 ? 4 : 2) : s.mt == 2 ? 2 : 1;
-    s.lds = (size_t)s.waves * s.s * s.mt * 1024;
+    // LDS: the waves' x (one 16-row tile and 4 blocks per wave: all of it, 16 KiB per wave;
+    // else xd_slots(mt) slots of 4 KiB per tile, at most 128 KiB for 8 waves), later reused
+    // for the waves' sums (1 KiB per wave, strip and tile)
+    const size_t xl = (size_t)s.waves * (s.mt == 1 && s.bpw == 4 ? 4 : xd_slots(s.mt) * s.mt) * 4096;
+    const size_t sums = (size_t)s.waves * s.s * s.mt * 1024;
+    s.lds = xl > sums ? xl : sums;
     s.ok = true;
     return s;
 }
@@ -737,12 +849,15 @@ template <int MT, int S>
 static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
     constexpr int PD1 = MT == 1 ? 2 : MT == 2 ? 2 : 1;   // pd for 8 or more blocks per wave
     const dim3 grid((p.N / 16 + S - 1) / S), block(64 * s.waves);
-    switch (s.bpw) {
-        case 4: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 4, MT == 1 ? 4 : PD1>), grid, block, s.lds, st, p); break;
-        case 8: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 8, PD1>), grid, block, s.lds, st, p); break;
-        case 16: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 16, PD1>), grid, block, s.lds, st, p); break;
-        case 32:   // 4 strips over 32 blocks would spill
-            if constexpr (S <= 2) { hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 32, PD1>), grid, block, s.lds, st, p); break; }
+    switch (s.bpw) {   // XD 1 with one tile and 4 blocks per wave, else XD 2
+        case 4:
+            if constexpr (MT == 1) hipLaunchKernelGGL((gemm_prep_frag_kernel<1, S, 4, 4, 1>), grid, block, s.lds, st, p);
+            else hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 4, MT == 2 ? 2 : 1, 2>), grid, block, s.lds, st, p);
+            break;
+        case 8: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 8, PD1, 2>), grid, block, s.lds, st, p); break;
+        case 16: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 16, PD1, 2>), grid, block, s.lds, st, p); break;
+        case 32:   // 4 strips over 32 blocks would not fit the registers
+            if constexpr (S <= 2) { hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 32, PD1, 2>), grid, block, s.lds, st, p); break; }
             return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
