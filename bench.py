@@ -6,9 +6,11 @@ cannot hold them. The weights are given as AWQ checkpoints and rewritten once ea
 prepared layout (w4a16_prepare_layout: the load-time step, timed on its own and reported);
 one step = one w4a16_gemm_prepared call through the C ABI. The same workload on the
 checkpoint layout as stored (w4a16_gemm) is reported beside it in extra.checkpoint_layout. The timed region is
-exactly --steps calls, replayed from HIP graphs so that host launch cost does not gate the
-GPU, with one untimed replay enqueued just ahead of the start event so that the GPU is busy
-when the timed work is launched. `value` is algorithmic GB/s (bytes of qweight + scales +
+exactly --steps calls, with untimed calls (HIP graph replays) enqueued just ahead of the start
+event so that the GPU is busy while the host enqueues the timed work: up to DIRECT_MAX_STEPS
+steps are launched directly behind about 1000 such calls (a graph replay has a fixed cost of
+its own, ~8 us, that a short region would carry), more steps are replayed from HIP graphs so
+that host launch cost does not gate the GPU. `value` is algorithmic GB/s (bytes of qweight + scales +
 qzeros + x + out, each counted once) over that region, measured with HIP events on the
 launch stream; the median of five further batches of 1000 calls is reported beside it.
 (Act-order lines in "extra" also count the int32 g_idx, or the prepared path's permutation.)
@@ -45,6 +47,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP16_DENSE_PEAK_TFLOPS = 2516.6  # MI355X fp16 dense MFMA
 GRAPH_CALLS = 100
+# the headline's timed region up to this many steps is launched directly (behind ~1000 untimed
+# graph-replayed calls) instead of as graph replays: one replay of a 20-call graph took 144 us
+# against 20 x 6.78 us for the same calls inside longer graphs (~8.5 us per replay), direct
+# launches 7.03 us per call
+DIRECT_MAX_STEPS = 100
 PMC_WARM, PMC_MEASURED = 20, 40
 COPY_ELEMS = 128 * 1024 * 1024   # int32 elements streamed by the calibration kernel (512 MiB)
 
@@ -106,30 +113,52 @@ def _timed_replays(torch, graphs, reps, stream, lead=None):
     return start.elapsed_time(stop)
 
 
+def _timed_direct(torch, fn, steps, stream, lead):
+    """ms for `steps` direct calls fn(0 .. steps-1), enqueued behind the untimed graph replays
+    `lead` (no synchronisation in between), which keep the GPU busy while the host enqueues
+    the timed calls."""
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for g in lead:
+            g.replay()
+        start.record(stream)
+        for i in range(steps):
+            fn(i)
+        stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop)
+
+
 def time_calls(torch, fn, steps, warmup, stream, n_sets, batches=5, batch_calls=1000,
-               graph_calls=GRAPH_CALLS, n_graphs=10):
+               graph_calls=GRAPH_CALLS, n_graphs=10, exact_direct=False):
     """Per-call ms of fn(i) (call i uses weight set i % n_sets) replayed from HIP graphs.
 
     Returns (ms_exact, ms_median, batch_ms, wall_s): ms_exact from exactly `steps` calls
-    (graphs of C = the largest divisor of steps up to graph_calls calls), ms_median the median
-    over `batches` further batches of about `batch_calls` calls (graphs of graph_calls)."""
+    (with exact_direct and at most DIRECT_MAX_STEPS steps: launched directly behind the batch
+    graphs' replays; else graphs of C = the largest divisor of steps up to graph_calls calls),
+    ms_median the median over `batches` further batches of about `batch_calls` calls (graphs
+    of graph_calls)."""
     with torch.cuda.stream(stream):
         for i in range(max(warmup, n_sets)):
             fn(i)
     stream.synchronize()
+    direct = exact_direct and steps <= DIRECT_MAX_STEPS
     c = max(d for d in range(1, min(graph_calls, steps) + 1) if steps % d == 0)
-    g_exact = _capture(torch, fn, c, max(1, min(steps // c, n_graphs)), stream)
-    g_batch = g_exact if c == graph_calls else _capture(torch, fn, graph_calls, n_graphs, stream)
+    g_exact = [] if direct else _capture(torch, fn, c, max(1, min(steps // c, n_graphs)), stream)
+    g_batch = g_exact if c == graph_calls and not direct else _capture(torch, fn, graph_calls, n_graphs, stream)
     with torch.cuda.stream(stream):
         for g in g_exact + g_batch:
             g.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    # a short timed region (the driver's 20 steps fit one graph) is preceded by the batch
-    # graphs, about 1000 calls of other graph instances (a relaunch of an instance still in
-    # flight is not queued behind it), so the host has enqueued it before the GPU gets there
-    lead = g_batch if g_batch is not g_exact else None
-    ms_exact = _timed_replays(torch, g_exact, steps // c, stream, lead=lead) / steps
+    if direct:
+        ms_exact = _timed_direct(torch, fn, steps, stream, lead=g_batch) / steps
+    else:
+        # a short graph-timed region is preceded by the batch graphs, about 1000 calls of
+        # other graph instances (a relaunch of an instance still in flight is not queued
+        # behind it), so the host has enqueued it before the GPU gets there
+        lead = g_batch if g_batch is not g_exact else None
+        ms_exact = _timed_replays(torch, g_exact, steps // c, stream, lead=lead) / steps
     wall = time.perf_counter() - t0
     reps = max(1, batch_calls // graph_calls)
     per = []
@@ -870,7 +899,7 @@ def main() -> int:
 
     # timed region: exactly args.steps calls; then 5 further batches of 1000 for the median
     ms, ms_med, batch_ms, wall = time_calls(torch, headline_call, args.steps, args.warmup, stream,
-                                            n_sets, batches=5, batch_calls=1000)
+                                            n_sets, batches=5, batch_calls=1000, exact_direct=True)
     if args.headline_only:
         progress(f"headline only: {ms * 1e3:.3f} us/call exact, {ms_med * 1e3:.3f} median")
         return 0
@@ -905,9 +934,11 @@ def main() -> int:
                    "kernel": "prepared/gemv (gemv_prep_mfma_kernel)", "weight_sets_rotated": n_sets,
                    "rotated_footprint_MB": round(n_sets * pkg.prepared_bytes(K, N, G) / 1e6, 1),
                    "prepare_once_us": round(prepare_us, 1),
-                   "timing": f"HIP events on the launch stream around exactly {args.steps} calls "
-                             f"replayed from HIP graphs, one untimed replay enqueued ahead of the "
-                             f"start event"},
+                   "timing": (f"HIP events on the launch stream around exactly {args.steps} calls "
+                              + (f"launched directly, enqueued behind {GRAPH_CALLS * 10} untimed calls "
+                                 f"replayed from HIP graphs" if args.steps <= DIRECT_MAX_STEPS else
+                                 f"replayed from HIP graphs, untimed replays enqueued ahead of the "
+                                 f"start event"))},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": nbytes, **traffic_detail},
