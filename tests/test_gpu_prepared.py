@@ -177,6 +177,11 @@ def test_gemm_prepared_prefill_exact_arithmetic(torch_cuda, orc):
     (AWQ, 63, 128 * 70, 256, 256),      # 16 blocks per wave, group of 2 blocks
     (GPTQ, 5, 32768, 64, 128),          # 32 blocks per wave, 8 waves
     (SYM, 12, 128, 16, 128),            # one block, one strip
+    # x streamed through the waves' LDS slots: 2 row tiles with 8 blocks per wave; one tile
+    # with a last wave of 5 blocks (3 past K); all of x up front with a last wave of 1 block;
+    # 4 rows (the rows GEMV's range) where a wave takes 4 blocks
+    (GPTQ, 24, 8192, 512, 128), (AWQ, 9, 128 * 37, 128, 128), (SYM, 10, 128 * 13, 96, 128),
+    (GPTQ, 4, 2048, 320, 128),
 ])
 def test_gemm_prepared_small_batch_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
     P = pkg()
@@ -195,7 +200,8 @@ def test_gemm_prepared_small_batch_matches_oracle(torch_cuda, orc, fmt, M, K, N,
 @pytest.mark.parametrize("M", [2, 7, 16, 32, 64])
 def test_act_order_then_prepared_small_batch(torch_cuda, orc, M):
     """Config 2 (GPTQ act-order, K=4096 -> N=6144) through the group-order repack and the
-    prepared layout: x is gathered straight into the small-batch kernel's operand order."""
+    prepared layout: x's columns are gathered by the permutation, then the small-batch kernel
+    reads the gathered rows (with a permutation it serves every M from 2)."""
     P = pkg()
     K, N = 4096, 6144
     p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED0002 + M, act_order=True)

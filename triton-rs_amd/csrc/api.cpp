@@ -612,11 +612,13 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
         return fail(W4A16_ERR_INVALID_ARG,
                     "x, out and perm must be 16-byte aligned, prepared 256-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    // 2..64 rows (5..64 without act-order, where the rows kernel needs no pass over x): the
-    // small-batch kernel, reading x as stored (act-order: x's columns gathered by perm first)
-    // and putting it in MFMA fragment order itself
+    // 2..64 rows (5..64 without act-order, or 4 where a wave takes 4 blocks, K <= 4096; below
+    // that the rows GEMV is as fast or faster: AWQ M = 4 4096 -> 14336 9.13 -> 8.73 us, 14336
+    // -> 4096 9.45 -> 9.80 us, M = 3 8.63 -> 8.69 us): the small-batch kernel, reading x as
+    // stored (act-order: x's columns gathered by perm first) and putting it in MFMA fragment
+    // order itself
     const PrepFragShape fs = prep_frag_shape(M, N, K, G);
-    if (fs.ok && (perm ? M >= 2 : M >= 5)) {
+    if (fs.ok && (perm ? M >= 2 : M >= 5 || (M == 4 && fs.bpw == 4))) {
         const void* xa = x;
         hipError_t e = hipSuccess;
         if (perm) {
