@@ -305,6 +305,31 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
                       : plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
     if (g_idx && kernel == W4A16_KERNEL_PREFILL && !src.may_allocate) kernel = W4A16_KERNEL_STRIDED;
+    // plain-order GPTQ small batches beyond 16 rows (or 9..16 with 64-column workgroups): the
+    // direct-x small-batch kernel on the checkpoint as stored (one workgroup over all of K for
+    // its columns: no split-K hand-off, no scratch). Same-box A/B against the split-K kernel,
+    // K=4096 -> N=6144: M = 32 / 48 / 64 11.12 / 14.62 / 15.38 -> 10.18 / 13.12 / 14.67 us;
+    // M = 16 on N = 14336 (4 columns per lane) 13.42 -> 12.42 us; 14336 -> 4096 M = 32
+    // 26.17 -> 25.86 us. Up to 16 rows with 32-column workgroups it was slower (M = 9 / 16
+    // 7.55 / 8.35 -> 8.25 / 8.45 us, 8192 x 8192 M = 16 13.49 -> 14.35 us): its workgroups
+    // read 128-byte pieces of K / 8 packed rows N * 4 bytes apart, where the prepared layout
+    // streams whole strips (6.05 us at config 2's M = 16); 16- and 64-column workgroups were
+    // slower still.
+    if (kernel == W4A16_KERNEL_SKINNY && !bf16 && !g_idx && fmt != W4A16_FMT_AWQ && M > 8) {
+        const PrepFragShape fs = ck_frag_shape(fmt, M, N, K, G);
+        if (fs.ok && (M > 16 || fs.s == 4)) {
+            PrepFragParams p{};
+            p.x = static_cast<const half_t*>(x);
+            p.qweight = static_cast<const uint32_t*>(qweight);
+            p.scales = static_cast<const half_t*>(scales);
+            p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+            p.zero_offset = zero_offset;
+            p.out = static_cast<half_t*>(out);
+            p.M = M; p.N = N; p.K = K; p.G = G;
+            hipError_t e = launch_ck_frag(fmt, p, fs, st);
+            return e == hipSuccess ? W4A16_OK : hip_fail(e, "small-batch launch");
+        }
+    }
     // the placement probe allocates: sources that must not allocate use what is cached
     const bool xcd = src.may_probe ? xcd_placement(st) : xcd_placement_cached();
     auto scratch_for = [&](size_t tiles, size_t partial_bytes, Scratch* sc) -> int {

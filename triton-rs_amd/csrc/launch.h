@@ -259,6 +259,12 @@ constexpr int PREP_GEMV_MAX_M = 8;
 // (prepared.hip): one workgroup per S strips, its waves over K.
 struct PrepFragParams {
     const half_t* x;              // x [M, K], row-major
+    // checkpoint source (launch_ck_frag): GPTQ qweight [K/8, N], scales [K/G, N], qzeros
+    // [K/G, N/8] (GPTQ_SYM: unused), zero = nibble + zero_offset
+    const uint32_t* qweight;
+    const half_t* scales;
+    const uint32_t* qzeros;
+    int zero_offset;
     const unsigned char* prep;    // prepared weights (fewer than 2^31 bytes)
     half_t* out;                  // [M, N]
     int M, N, K, G;
@@ -283,6 +289,9 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G);
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st);
 PrepFragShape prep_frag_shape(int M, int N, int K, int G);
 hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
+// The small-batch kernel on a GPTQ / GPTQ_SYM checkpoint as stored (no split-K, no scratch)
+PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G);
+hipError_t launch_ck_frag(int fmt, const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
 
 // ------------------------------------------------------------------ op layer (api.cpp)
 

@@ -625,50 +625,124 @@ __device__ __forceinline__ void xd_wait(const int j) {
 #undef W4A16_XDW
 }
 
-template <int MT, int S, int BPW, int PD, int XD>
+// Weight sources of the small-batch kernel: the prepared layout, or a GPTQ checkpoint as stored
+// (qweight [K/8, N], scales [K/G, N], qzeros [K/G, N/8]; GPTQ_SYM: zero 8). For the checkpoint
+// a workgroup owns 16 S consecutive columns and lane l of sub-block s holds column
+// n0 + S (l % 16) + s (the MFMA's column order is free as long as the output follows it):
+// a lane loads S consecutive words of each packed row (16 lanes: 64 S contiguous bytes of the
+// row), its S scales in one load and its zero word in one. Word st of a lane's block is
+// packed row 16 kb + 4 (l / 16) + st, i.e. rows 128 kb + 32 (l / 16) + 8 st + [0, 8), the
+// rows the A operand of step st holds; GPTQ packs row 8 r + i in nibble i, so the pair
+// (i, i + 1) = ((w >> 4 i) & 0xF, (w >> 4 i + 4) & 0xF) becomes the fp16 pair
+// (1024 + q_i, 1024 + q_i+1) with one shift each and two v_and_or_b32. The checkpoint kernel
+// then forms each weight as the reference does, W16 = RNE_f16((q - z) s) (v_pk_add_f16 of
+// -(1024 + z), exact, then v_pk_mul_f16), and the MFMA chain accumulates x W16 in fp32; the
+// prepared kernel scales each block's sum of x (q - z) in fp32 instead.
+constexpr int SRC_PREP = 0, SRC_GPTQ = 1, SRC_GPTQ_SYM = 2;
+
+__device__ __forceinline__ uint32_t gptq_pair(uint32_t w, int i) {   // i even, constant
+    const uint32_t x = w >> (4 * i);
+    return (x & 0xFu) | ((x << 12) & 0xF0000u) | 0x64006400u;
+}
+
+template <int S> struct ck_words;
+template <> struct ck_words<1> { typedef uint32_t type; };
+template <> struct ck_words<2> { typedef u32x2 type; };
+template <> struct ck_words<4> { typedef u32x4 type; };
+
+// S consecutive 32-bit words at byte offset off; ck_load<0>: one 16-bit value
+template <int S>
+__device__ __forceinline__ typename ck_words<S ? S : 1>::type ck_load(bufrsrc_t r, uint32_t off) {
+    if constexpr (S == 0) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 2);
+    else if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 2);
+    else if constexpr (S == 2) return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 2));
+    else return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
+template <int S>
+__device__ __forceinline__ uint32_t ck_word(const typename ck_words<S>::type& v, int s) {
+    if constexpr (S == 1) return v;
+    else return v[s];
+}
+
+template <int MT, int S, int BPW, int PD, int XD, int SRC = SRC_PREP>
 __global__ void __launch_bounds__(512)
 gemm_prep_frag_kernel(PrepFragParams p) {
+    constexpr bool CK = SRC != SRC_PREP;
+    // loads per block besides x: the table entries and weights of S strips (prepared); four
+    // words, the scales and the zero word (checkpoint)
+    constexpr int LOPS = CK ? (SRC == SRC_GPTQ ? 6 : 5) : 2 * S;
     static_assert(PD >= 1 && PD <= BPW, "prefetch depth");
-    static_assert(XD == 2 || (XD == 1 && MT == 1 && PD == BPW && 2 * S * BPW <= 63),
+    static_assert(XD == 2 || (XD == 1 && MT == 1 && PD == BPW && LOPS * BPW <= 63),
                   "XD 1: one tile, all blocks up front");
+    static_assert(!CK || S == 1 || S == 2 || S == 4, "checkpoint: 1, 2 or 4 columns per lane");
     constexpr int R = XD == 2 ? xd_slots(MT) : 1;   // XD 2: slots of x per wave
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int W = blockDim.x >> 6;
-    const int col = lane & 15;
+    const int col = lane & 15, h = lane >> 4;
     const int NS = p.N >> 4, KB = p.K >> 7, M = p.M;
-    const int s0 = blockIdx.x * S;
-    const uint32_t tbytes = prep_table_words(p.K, p.G) * 4u;
-    const uint32_t pbytes = (uint32_t)NS * p.strip_bytes;
-    const bufrsrc_t pr = make_rsrc(p.prep, pbytes);
+    const int s0 = blockIdx.x * S;             // prepared: first strip
+    const int n0 = blockIdx.x * 16 * S;        // checkpoint: first column
+    const int nc = n0 + S * col;               // checkpoint: the lane's first column
+    const uint32_t tbytes = CK ? 0u : prep_table_words(p.K, p.G) * 4u;
+    const uint32_t pbytes = CK ? 0u : (uint32_t)NS * p.strip_bytes;
+    const bufrsrc_t pr = make_rsrc(CK ? nullptr : p.prep, pbytes);
+    const uint32_t qbytes = CK ? (uint32_t)(p.K / 8) * (uint32_t)p.N * 4u : 0u;
+    const uint32_t sbytes = CK ? (uint32_t)(p.K / p.G) * (uint32_t)p.N * 2u : 0u;
+    const uint32_t zbytes = SRC == SRC_GPTQ ? (uint32_t)(p.K / p.G) * (uint32_t)(p.N / 8) * 4u : 0u;
+    const bufrsrc_t qr = make_rsrc(CK ? p.qweight : nullptr, qbytes);
+    const bufrsrc_t sr = make_rsrc(CK ? p.scales : nullptr, sbytes);
+    const bufrsrc_t zr = make_rsrc(SRC == SRC_GPTQ ? p.qzeros : nullptr, zbytes);
+    const int bpg = CK ? p.G / 128 : 1;        // checkpoint: blocks per group (G % 128 == 0)
     const bufrsrc_t xrs = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
     // XD 1: the wave's x, block j at 4 KiB j; XD 2: its R slots, block j's tile tt at
     // ((j % R) MT + tt) 4 KiB
     unsigned char* xw = lds + (size_t)wave * (XD == 1 ? BPW * 4096 : R * MT * 4096);
+    (void)pr; (void)qr; (void)sr; (void)zr; (void)bpg; (void)nc; (void)s0; (void)n0; (void)tbytes;
 
+    // prepared: ev = table entries, wv = 16-byte lane chunks (one per strip); checkpoint:
+    // ev[j][0] = the zero word, cs = the lane's S scales (raw), cw = word st of every column
     uint32_t ev[BPW][S];
-    u32x4 wv[BPW][S];
+    u32x4 wv[CK ? 1 : BPW][S];
+    typename ck_words<CK ? S : 1>::type cw[CK ? BPW : 1][4];
+    typename ck_words<CK ? (S + 1) / 2 : 1>::type cs[CK ? BPW : 1];   // S = 1: one 16-bit load
+    (void)wv; (void)cw; (void)cs;
     auto load = [&](const int j) __attribute__((always_inline)) {
         const int kb = wave * BPW + j;
         const bool kin = kb < KB;
+        if constexpr (CK) {
+            const int g = kb / bpg;
+            const uint32_t so = kin ? (uint32_t)(g * p.N + nc) * 2u : sbytes;
+            cs[j] = ck_load<S / 2>(sr, so);
+            if constexpr (SRC == SRC_GPTQ)
+                ev[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    zr, kin ? (uint32_t)(g * (p.N >> 3) + (nc >> 3)) * 4u : zbytes, 0, 2);
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int strip = s0 + s;
-            const uint32_t off = kin && strip < NS ? (uint32_t)strip * p.strip_bytes + (uint32_t)(kb * 16 + col) * 4u
-                                                   : pbytes;
-            ev[j][s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 2);
-        }
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t off = kin ? ((uint32_t)(16 * kb + 4 * h + st) * (uint32_t)p.N + (uint32_t)nc) * 4u
+                                         : qbytes;
+                cw[j][st] = ck_load<S>(qr, off);
+            }
+        } else {
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-            const int strip = s0 + s;
-            const uint32_t off = kin && strip < NS
-                                     ? (uint32_t)strip * p.strip_bytes + tbytes + (uint32_t)kb * 1024u + (uint32_t)lane * 16u
-                                     : pbytes;
-            wv[j][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 2));
+            for (int s = 0; s < S; ++s) {
+                const int strip = s0 + s;
+                const uint32_t off = kin && strip < NS ? (uint32_t)strip * p.strip_bytes + (uint32_t)(kb * 16 + col) * 4u
+                                                       : pbytes;
+                ev[j][s] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, 2);
+            }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int strip = s0 + s;
+                const uint32_t off = kin && strip < NS
+                                         ? (uint32_t)strip * p.strip_bytes + tbytes + (uint32_t)kb * 1024u + (uint32_t)lane * 16u
+                                         : pbytes;
+                wv[j][s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, 2));
+            }
         }
     };
-    // block j's x (XD): MT tiles of 4 KiB from dst. The loads go through the compiler's
+    // block j's x: MT tiles of 4 KiB from dst. The loads go through the compiler's
     // buffer-load-to-LDS builtin, so its own waits for the table and weight loads count them;
     // it does not order LDS reads after them (the kernel's waits below do), and the empty asm
     // statements keep the loads in the issue order those waits count.
@@ -698,7 +772,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
 #pragma unroll
     for (int j = 0; j < PD; ++j) load(j);
     if constexpr (XD == 1) {
-        wait_vmcnt<2 * S * BPW>();          // the x loads, issued before every other load
+        wait_vmcnt<LOPS * BPW>();           // the x loads, issued before every other load
         asm volatile("" ::: "memory");      // the LDS reads below stay after the wait
     }
 
@@ -712,10 +786,10 @@ gemm_prep_frag_kernel(PrepFragParams p) {
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
         u32x4 A[MT][4];
-        const int r = lane & 15, h = lane >> 4;
+        const int r = lane & 15;
         if constexpr (XD == 2) {
             // block j's x loads are done once only the loads issued after them remain
-            xd_wait<R, PD, BPW, 4 * MT, 2 * S>(j);
+            xd_wait<R, PD, BPW, 4 * MT, LOPS>(j);
             asm volatile("" ::: "memory");   // the LDS reads below stay after the wait
             const int slot = j % R;
 #pragma unroll
@@ -737,31 +811,54 @@ gemm_prep_frag_kernel(PrepFragParams p) {
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-            const uint32_t e = ev[j][s];
-            // -(1024 + z) as an fp16 pair (z <= 31: exact, bit pattern)
-            const half2_t ze = as_h2(((0x6400u + (e >> 16)) * 0x10001u) | 0x80008000u);
+            // the (scale, zero) of sub-block s and -(1024 + z) as an fp16 pair (exact bits)
+            uint32_t zq;
+            float sc;
+            if constexpr (CK) {
+                const uint32_t sw = ck_word<(S + 1) / 2>(cs[j], s >> 1);
+                sc = (float)__builtin_bit_cast(half_t, (uint16_t)(sw >> (16 * (s & 1))));
+                zq = SRC == SRC_GPTQ ? ((ev[j][0] >> (4 * ((nc + s) & 7))) & 0xFu) + (uint32_t)p.zero_offset : 8u;
+            } else {
+                const uint32_t e = ev[j][s];
+                sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
+                zq = e >> 16;
+            }
+            const half2_t ze = as_h2(((0x6400u + zq) * 0x10001u) | 0x80008000u);
             half8_t B[4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                const uint32_t q = wv[j][s][st];
-                B[st] = __builtin_bit_cast(half8_t, u32x4{as_u32(nib_pair(q) + ze), as_u32(nib_pair(q >> 4) + ze),
-                                                          as_u32(nib_pair(q >> 8) + ze), as_u32(nib_pair(q >> 12) + ze)});
+                if constexpr (CK) {
+                    // W16 = RNE_f16((q - z) s) per weight, as the reference dequantises
+                    // (w4a16_gptq_gemm_typed.rs:246-260): q - z exact, one rounded multiply
+                    const uint32_t q = ck_word<S>(cw[j][st], s);
+                    const half2_t s2 = {(half_t)sc, (half_t)sc};
+                    B[st] = __builtin_bit_cast(half8_t, u32x4{as_u32((as_h2(gptq_pair(q, 0)) + ze) * s2),
+                                                              as_u32((as_h2(gptq_pair(q, 2)) + ze) * s2),
+                                                              as_u32((as_h2(gptq_pair(q, 4)) + ze) * s2),
+                                                              as_u32((as_h2(gptq_pair(q, 6)) + ze) * s2)});
+                } else {
+                    const uint32_t q = wv[j][s][st];
+                    B[st] = __builtin_bit_cast(half8_t, u32x4{as_u32(nib_pair(q) + ze), as_u32(nib_pair(q >> 4) + ze),
+                                                              as_u32(nib_pair(q >> 8) + ze), as_u32(nib_pair(q >> 12) + ze)});
+                }
             }
-            const float sc = (float)__builtin_bit_cast(half_t, (uint16_t)e);
 #pragma unroll
             for (int tt = 0; tt < MT; ++tt) {
-                float4_t d = {0.f, 0.f, 0.f, 0.f};
+                // checkpoint: the dot of x and W16 accumulates in the chain itself; prepared:
+                // the block's sum of x (q - z), scaled in fp32
+                float4_t d = CK ? float4_t{acc[s][tt][0], acc[s][tt][1], acc[s][tt][2], acc[s][tt][3]}
+                                : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st)
                     d = mfma16x16x32(__builtin_bit_cast(half8_t, A[tt][st]), B[st], d);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[s][tt][i] = __builtin_fmaf(sc, d[i], acc[s][tt][i]);
+                for (int i = 0; i < 4; ++i) acc[s][tt][i] = CK ? d[i] : __builtin_fmaf(sc, d[i], acc[s][tt][i]);
             }
         }
     }
 
     // ---- the waves' sums, added in wave order; lane l of tile tt holds rows 16 tt + 4 (l / 16)
-    // + i of column l % 16
+    // + i of column l % 16 of sub-block s
     __syncthreads();   // the sums overwrite other waves' x
     float4_t* red = reinterpret_cast<float4_t*>(lds);
 #pragma unroll
@@ -773,11 +870,18 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     const float* rf = reinterpret_cast<const float*>(lds);
     for (int o = t; o < S * MT * 256; o += blockDim.x) {
         const int i = o & 3, l = (o >> 2) & 63, rest = o >> 8, tt = rest % MT, s = rest / MT;
-        const int m = 16 * tt + 4 * (l >> 4) + i, strip = s0 + s;
-        if (m >= M || strip >= NS) continue;
+        const int m = 16 * tt + 4 * (l >> 4) + i;
+        if (m >= M) continue;
+        int n;
+        if constexpr (CK) {
+            n = n0 + S * (l & 15) + s;
+        } else {
+            if (s0 + s >= NS) continue;
+            n = (s0 + s) * 16 + (l & 15);
+        }
         float a = 0.f;
         for (int w = 0; w < W; ++w) a += rf[w * S * MT * 256 + o];
-        p.out[(size_t)m * p.N + strip * 16 + (l & 15)] = (half_t)a;
+        p.out[(size_t)m * p.N + n] = (half_t)a;
     }
 }
 
@@ -822,18 +926,12 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G) {
 // the registers leave less room) that still gives 192 workgroups (K=4096 -> N=6144: S = 2, 192 workgroups,
 // 6.1 us at M = 16 against 7.5 with S = 1; N=14336: S = 4); loads in flight: the whole queue
 // at 16 rows when it is 4 blocks, else 2 blocks, then 1 (measured over PD = 1, 2, 4, BPW).
-PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
-    PrepFragShape s{};
-    if (M < 1 || M > PREP_FRAG_MAX_M || N % 16 || K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
-        return s;
-    if (prep_total_bytes(K, N, G) >= ((size_t)1 << 31)) return s;
-    const int NS = N / 16, KB = K / 128;
-    s.mt = (M + 15) / 16;
+// Blocks per wave, waves, prefetch depth and LDS of the small-batch kernel for s.mt tiles,
+// s.s strips (or columns per lane) and K / 128 = KB blocks.
+static void frag_common(PrepFragShape& s, int KB) {
     s.bpw = KB <= 32 ? 4 : KB <= 64 ? 8 : KB <= 128 ? 16 : 32;
     s.waves = (KB + s.bpw - 1) / s.bpw;
-    s.s = 1;
-    for (int c = s.mt <= 2 && s.bpw <= 16 ? 4 : 2; c > 1; c /= 2)
-        if (NS / c >= 192) { s.s = c; break; }
+
     s.pd = s.mt == 1 ? (s.bpw == 4 ? 4 : 2) : s.mt == 2 ? 2 : 1;
     // LDS: the waves' x (one 16-row tile and 4 blocks per wave: all of it, 16 KiB per wave;
     // else xd_slots(mt) slots of 4 KiB per tile, at most 128 KiB for 8 waves), later reused
@@ -842,49 +940,112 @@ PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
     const size_t sums = (size_t)s.waves * s.s * s.mt * 1024;
     s.lds = xl > sums ? xl : sums;
     s.ok = true;
+}
+
+PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
+    PrepFragShape s{};
+    if (M < 1 || M > PREP_FRAG_MAX_M || N % 16 || K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
+        return s;
+    if (prep_total_bytes(K, N, G) >= ((size_t)1 << 31)) return s;
+    const int NS = N / 16, KB = K / 128;
+    s.mt = (M + 15) / 16;
+    s.s = 1;
+    const int bpw = KB <= 32 ? 4 : KB <= 64 ? 8 : KB <= 128 ? 16 : 32;
+    for (int c = s.mt <= 2 && bpw <= 16 ? 4 : 2; c > 1; c /= 2)
+        if (NS / c >= 192) { s.s = c; break; }
+    frag_common(s, KB);
     return s;
 }
 
-template <int MT, int S>
-static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+// Checkpoint instances that fit the registers (the others spill: their block loop, with the
+// GPTQ unpacking, is not unrolled); fewer columns per lane are tried first
+constexpr bool ck_frag_fits(int mt, int s, int bpw) {
+    return bpw == 4 || (bpw == 8 && mt * s <= 6) || (bpw == 16 && mt * s <= 2) || (bpw == 32 && mt * s == 1);
+}
+
+// The same kernel on a GPTQ / GPTQ_SYM checkpoint as stored: 16 s columns per workgroup, s
+// columns per lane (N a multiple of 16 s), G a multiple of 128, fewer than 2^31 bytes per
+// tensor.
+PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G) {
+    PrepFragShape s{};
+    if ((fmt != FMT_GPTQ && fmt != FMT_GPTQ_SYM) || M < 1 || M > PREP_FRAG_MAX_M || N % 16 ||
+        K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
+        return s;
+    if ((size_t)K / 8 * N * 4 >= ((size_t)1 << 31) || (size_t)K / G * N * 2 >= ((size_t)1 << 31))
+        return s;
+    const int KB = K / 128;
+    s.mt = (M + 15) / 16;
+    s.s = 1;
+    const int bpw = KB <= 32 ? 4 : KB <= 64 ? 8 : KB <= 128 ? 16 : 32;
+    for (int c = s.mt <= 2 && bpw <= 16 ? 4 : 2; c > 1; c /= 2)
+        if (N % (16 * c) == 0 && N / (16 * c) >= 192) { s.s = c; break; }
+    while (s.s > 1 && !ck_frag_fits(s.mt, s.s, bpw)) s.s /= 2;
+    if (!ck_frag_fits(s.mt, s.s, bpw)) return s;
+    frag_common(s, KB);
+    return s;
+}
+
+template <int MT, int S, int BPW, int SRC>
+static void launch_frag_inst(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
     constexpr int PD1 = MT == 1 ? 2 : MT == 2 ? 2 : 1;   // pd for 8 or more blocks per wave
     const dim3 grid((p.N / 16 + S - 1) / S), block(64 * s.waves);
-    switch (s.bpw) {   // XD 1 with one tile and 4 blocks per wave, else XD 2
-        case 4:
-            if constexpr (MT == 1) hipLaunchKernelGGL((gemm_prep_frag_kernel<1, S, 4, 4, 1>), grid, block, s.lds, st, p);
-            else hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 4, MT == 2 ? 2 : 1, 2>), grid, block, s.lds, st, p);
-            break;
-        case 8: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 8, PD1, 2>), grid, block, s.lds, st, p); break;
-        case 16: hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 16, PD1, 2>), grid, block, s.lds, st, p); break;
-        case 32:   // 4 strips over 32 blocks would not fit the registers
-            if constexpr (S <= 2) { hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 32, PD1, 2>), grid, block, s.lds, st, p); break; }
-            return hipErrorInvalidValue;
+    // XD 1 with one tile and 4 blocks per wave, else XD 2
+    if constexpr (BPW == 4 && MT == 1) hipLaunchKernelGGL((gemm_prep_frag_kernel<1, S, 4, 4, 1, SRC>), grid, block, s.lds, st, p);
+    else if constexpr (BPW == 4) hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, 4, MT == 2 ? 2 : 1, 2, SRC>), grid, block, s.lds, st, p);
+    else hipLaunchKernelGGL((gemm_prep_frag_kernel<MT, S, BPW, PD1, 2, SRC>), grid, block, s.lds, st, p);
+}
+
+template <int MT, int S, int SRC>
+static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    // instances that would not fit the registers: 4 strips over 32 blocks (prepared), and
+    // the checkpoint ones ck_frag_fits excludes
+    auto fits = [](int bpw) { return SRC == SRC_PREP ? !(S == 4 && bpw == 32) : ck_frag_fits(MT, S, bpw); };
+    if (!fits(s.bpw)) return hipErrorInvalidValue;
+    switch (s.bpw) {
+        case 4: launch_frag_inst<MT, S, 4, SRC>(p, s, st); break;
+        case 8: if constexpr (SRC == SRC_PREP || ck_frag_fits(MT, S, 8)) { launch_frag_inst<MT, S, 8, SRC>(p, s, st); break; }
+                return hipErrorInvalidValue;
+        case 16: if constexpr (SRC == SRC_PREP || ck_frag_fits(MT, S, 16)) { launch_frag_inst<MT, S, 16, SRC>(p, s, st); break; }
+                 return hipErrorInvalidValue;
+        case 32: if constexpr ((SRC == SRC_PREP && S <= 2) || ck_frag_fits(MT, S, 32)) { launch_frag_inst<MT, S, 32, SRC>(p, s, st); break; }
+                 return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-template <int MT>
+template <int MT, int SRC>
 static hipError_t launch_prep_frag_m(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
     switch (s.s) {
-        case 1: return launch_prep_frag_ms<MT, 1>(p, s, st);
-        case 2: return launch_prep_frag_ms<MT, 2>(p, s, st);
-        case 4: if constexpr (MT <= 2) return launch_prep_frag_ms<MT, 4>(p, s, st);
+        case 1: return launch_prep_frag_ms<MT, 1, SRC>(p, s, st);
+        case 2: return launch_prep_frag_ms<MT, 2, SRC>(p, s, st);
+        case 4: if constexpr (MT <= 2) return launch_prep_frag_ms<MT, 4, SRC>(p, s, st);
                 [[fallthrough]];
         default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+template <int SRC>
+static hipError_t launch_frag_src(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
     (void)hipGetLastError();
     if (!s.ok || s.pd != (s.mt == 1 ? (s.bpw == 4 ? 4 : 2) : s.mt == 2 ? 2 : 1)) return hipErrorInvalidValue;
     switch (s.mt) {
-        case 1: return launch_prep_frag_m<1>(p, s, st);
-        case 2: return launch_prep_frag_m<2>(p, s, st);
-        case 3: return launch_prep_frag_m<3>(p, s, st);
-        case 4: return launch_prep_frag_m<4>(p, s, st);
+        case 1: return launch_prep_frag_m<1, SRC>(p, s, st);
+        case 2: return launch_prep_frag_m<2, SRC>(p, s, st);
+        case 3: return launch_prep_frag_m<3, SRC>(p, s, st);
+        case 4: return launch_prep_frag_m<4, SRC>(p, s, st);
         default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    return launch_frag_src<SRC_PREP>(p, s, st);
+}
+
+hipError_t launch_ck_frag(int fmt, const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    if (fmt == FMT_GPTQ) return launch_frag_src<SRC_GPTQ>(p, s, st);
+    if (fmt == FMT_GPTQ_SYM) return launch_frag_src<SRC_GPTQ_SYM>(p, s, st);
+    return hipErrorInvalidValue;
 }
 
 template <int BPW>
