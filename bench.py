@@ -411,7 +411,7 @@ def pmc_report(args) -> int:
         table = _rocprof_pass(rocprof, counters, args.pmc_workload, args.sets, outdir)
         kern = {}
         for name, cs in table.items():
-            if "w4a16::" not in name:
+            if "w4a16" not in name:   # demangled or mangled (_ZN5w4a16...) names
                 continue
             kern[name] = {c: round(sum(v[-PMC_MEASURED:]) / len(v[-PMC_MEASURED:]), 1)
                           for c, v in cs.items()}
