@@ -174,9 +174,9 @@ W4A16_API int w4a16_gemm_act_order(void* stream, int fmt, const void* x, const v
  *   returned; x's columns are then gathered by it first (as w4a16_gemm_act_order does, into a
  *   per-(device, stream) buffer the library keeps). M = 1 runs a GEMV with one workgroup per
  *   strip over all of K (no split-K, no scratch). With group_size a multiple of 128, 5..64 rows
- *   (2..64 with perm) run a small-batch kernel, one workgroup per 1, 2 or 4 strips over all of
- *   K (no split-K), after one pass that rewrites x (gathered by perm) into the kernel's
- *   operand order in that same buffer.
+ *   (4 where K <= 4096; 2..64 with perm) run a small-batch kernel, one workgroup per 1, 2 or
+ *   4 strips over all of K (no split-K), which reads x (gathered by perm) as stored and puts
+ *   it in the matrix cores' operand order itself.
  * w4a16_dequant_prepared: W16 as fp16 [K, N] (transposed = 0) or [N, K] (= 1), bit-exact. */
 W4A16_API size_t w4a16_prepared_bytes(int32_t K, int32_t N, int32_t group_size);
 W4A16_API int w4a16_prepare_layout(void* stream, int fmt, const void* qweight, const void* scales,
