@@ -678,10 +678,18 @@ __global__ void __launch_bounds__(PF_THREADS) prefill_dma_kernel(PrefillParams p
 #pragma unroll
             for (int c = 0; c < CB; ++c)
                 if (RV > 0) bf[c] = *reinterpret_cast<const v8_t*>(B + boff[c] + ks * 4 * 256 * 8);
+            // checkpoint formats, tiles 224 or 256 wide: the wave's MFMA burst at raised
+            // priority, so that the SIMD's other wave, dequantising or reading LDS, does not
+            // hold up its issue (same-box A/B: config 3 4096->14336 / 14336->4096 228-231 ->
+            // 221-222 us, the MoE layer 0.571 -> 0.559 ms; 256 x 128 tiles, with a third of
+            // the MFMAs per burst, 1.5-3 % slower; with the prepared B stage 1-5 % slower)
+            constexpr bool PRIO = FMT != FMT_PREP && BN >= 224;
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int r = 0; r < RV; ++r)
 #pragma unroll
                 for (int c = 0; c < CB; ++c) acc[r][c] = mfma16x16x32(af[r], bf[c], acc[r][c]);
+            if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int c = ks * DQC / 2; c < (ks + 1) * DQC / 2; ++c) col[c] = dq_col(d, c);
             // place the dequantisation arithmetic between the MFMAs: 1 MFMA, 2 VALU
