@@ -305,9 +305,15 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
                       : plan(fmt, M, N, K, G, g_idx != nullptr, cus);
     if (!vec_ok) kernel = W4A16_KERNEL_STRIDED;
     if (g_idx && kernel == W4A16_KERNEL_PREFILL && !src.may_allocate) kernel = W4A16_KERNEL_STRIDED;
-    // plain-order GPTQ small batches beyond 16 rows (or 9..16 with 64-column workgroups): the
-    // direct-x small-batch kernel on the checkpoint as stored (one workgroup over all of K for
-    // its columns: no split-K hand-off, no scratch). Same-box A/B against the split-K kernel,
+    // GPTQ small batches beyond 16 rows (plain order also 9..16 with 64-column workgroups;
+    // act-order also any M >= 2 with groups under 128 rows): the direct-x small-batch kernel on
+    // the checkpoint as stored (one workgroup over all of K for its columns: no split-K
+    // hand-off, no scratch; act-order through a per-workgroup (scale, zero) table). Act-order,
+    // same-box A/B against the split-K kernel's table path, K=4096 -> N=6144: M = 32 / 48 / 64
+    // 12.30 / 16.34 / 17.03 -> 11.35 / 13.26 / 14.79 us; G = 32 M = 16 / 64 16.81 / 17.45 ->
+    // 11.40 / 15.26 us; up to 16 rows at G = 128 slower (M = 2 / 8 / 16 7.95 / 9.15 / 9.77 ->
+    // 10.40 / 10.50 / 10.84 us: its per-row table reads, ~4 bytes of LDS per weight, fall on
+    // 192 workgroups). Plain order, same-box A/B against the split-K kernel,
     // K=4096 -> N=6144: M = 32 / 48 / 64 11.12 / 14.62 / 15.38 -> 10.18 / 13.12 / 14.67 us;
     // M = 16 on N = 14336 (4 columns per lane) 13.42 -> 12.42 us; 14336 -> 4096 M = 32
     // 26.17 -> 25.86 us. Up to 16 rows with 32-column workgroups it was slower (M = 9 / 16
@@ -315,10 +321,11 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     // read 128-byte pieces of K / 8 packed rows N * 4 bytes apart, where the prepared layout
     // streams whole strips (6.05 us at config 2's M = 16); 16- and 64-column workgroups were
     // slower still.
-    if (kernel == W4A16_KERNEL_SKINNY && !bf16 && !g_idx && fmt != W4A16_FMT_AWQ && M > 8) {
-        const PrepFragShape fs = ck_frag_shape(fmt, M, N, K, G);
-        if (fs.ok && (M > 16 || fs.s == 4)) {
+    if (kernel == W4A16_KERNEL_SKINNY && !bf16 && fmt != W4A16_FMT_AWQ && (g_idx ? M >= 2 : M > 8)) {
+        const PrepFragShape fs = ck_frag_shape(fmt, M, N, K, G, g_idx != nullptr);
+        if (fs.ok && (g_idx ? M > 16 || G < 128 : M > 16 || fs.s == 4)) {
             PrepFragParams p{};
+            p.g_idx = g_idx;
             p.x = static_cast<const half_t*>(x);
             p.qweight = static_cast<const uint32_t*>(qweight);
             p.scales = static_cast<const half_t*>(scales);

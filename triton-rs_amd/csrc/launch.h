@@ -265,6 +265,7 @@ struct PrepFragParams {
     const half_t* scales;
     const uint32_t* qzeros;
     int zero_offset;
+    const int32_t* g_idx;         // checkpoint, act-order (nullable): each row's group
     const unsigned char* prep;    // prepared weights (fewer than 2^31 bytes)
     half_t* out;                  // [M, N]
     int M, N, K, G;
@@ -289,8 +290,9 @@ PrepGemvShape prep_gemv_shape(int M, int N, int K, int G);
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st);
 PrepFragShape prep_frag_shape(int M, int N, int K, int G);
 hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
-// The small-batch kernel on a GPTQ / GPTQ_SYM checkpoint as stored (no split-K, no scratch)
-PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G);
+// The small-batch kernel on a GPTQ / GPTQ_SYM checkpoint as stored (no split-K, no scratch);
+// act: with g_idx (any group size, K <= 4096, a table of at most 4096 entries)
+PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G, bool act = false);
 hipError_t launch_ck_frag(int fmt, const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
 
 // ------------------------------------------------------------------ op layer (api.cpp)

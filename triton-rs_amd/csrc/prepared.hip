@@ -638,7 +638,18 @@ __device__ __forceinline__ void xd_wait(const int j) {
 // then forms each weight as the reference does, W16 = RNE_f16((q - z) s) (v_pk_add_f16 of
 // -(1024 + z), exact, then v_pk_mul_f16), and the MFMA chain accumulates x W16 in fp32; the
 // prepared kernel scales each block's sum of x (q - z) in fp32 instead.
-constexpr int SRC_PREP = 0, SRC_GPTQ = 1, SRC_GPTQ_SYM = 2;
+//
+// Act-order (SRC_GPTQ_ACT, SRC_SYM_ACT: g_idx gives each row's group): the workgroup first
+// builds an LDS table of (scale | fp16(1024 + z) << 16) for every group and each of its 16 S
+// columns, and the rows' table offsets (clamp(g_idx, 0, K/G - 1) * 16 S) for all of K; the
+// loads for both are issued ahead of x and the weights, so they land first. A lane's B
+// operand of step st then takes, per row pair, its two entries per column: v_perm_b32
+// assembles the pairs (1024 + z0, 1024 + z1) and (s0, s1), and W16 = RNE_f16((q - z) s)
+// as before (the weights stay bit-exact; any group size).
+constexpr int SRC_PREP = 0, SRC_GPTQ = 1, SRC_GPTQ_SYM = 2, SRC_GPTQ_ACT = 3, SRC_SYM_ACT = 4;
+// act-order: table entries per thread (4 columns of one group per pass, ACT_TI passes) and
+// g_idx rows per thread (two 16-byte loads): at most 4096 entries and K <= 4096
+constexpr int ACT_TI = 2, ACT_MAX_ENTRIES = 4 * 512 * ACT_TI, ACT_MAX_K = 8 * 512;
 
 __device__ __forceinline__ uint32_t gptq_pair(uint32_t w, int i) {   // i even, constant
     const uint32_t x = w >> (4 * i);
@@ -668,9 +679,11 @@ template <int MT, int S, int BPW, int PD, int XD, int SRC = SRC_PREP>
 __global__ void __launch_bounds__(512)
 gemm_prep_frag_kernel(PrepFragParams p) {
     constexpr bool CK = SRC != SRC_PREP;
+    constexpr bool ACT = SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT;
+    constexpr bool ZQ = SRC == SRC_GPTQ || SRC == SRC_GPTQ_ACT;    // zero points from qzeros
     // loads per block besides x: the table entries and weights of S strips (prepared); four
-    // words, the scales and the zero word (checkpoint)
-    constexpr int LOPS = CK ? (SRC == SRC_GPTQ ? 6 : 5) : 2 * S;
+    // words, the scales and the zero word (checkpoint); four words (act-order)
+    constexpr int LOPS = ACT ? 4 : CK ? (SRC == SRC_GPTQ ? 6 : 5) : 2 * S;
     static_assert(PD >= 1 && PD <= BPW, "prefetch depth");
     static_assert(XD == 2 || (XD == 1 && MT == 1 && PD == BPW && LOPS * BPW <= 63),
                   "XD 1: one tile, all blocks up front");
@@ -690,16 +703,45 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     const bufrsrc_t pr = make_rsrc(CK ? nullptr : p.prep, pbytes);
     const uint32_t qbytes = CK ? (uint32_t)(p.K / 8) * (uint32_t)p.N * 4u : 0u;
     const uint32_t sbytes = CK ? (uint32_t)(p.K / p.G) * (uint32_t)p.N * 2u : 0u;
-    const uint32_t zbytes = SRC == SRC_GPTQ ? (uint32_t)(p.K / p.G) * (uint32_t)(p.N / 8) * 4u : 0u;
+    const uint32_t zbytes = ZQ ? (uint32_t)(p.K / p.G) * (uint32_t)(p.N / 8) * 4u : 0u;
     const bufrsrc_t qr = make_rsrc(CK ? p.qweight : nullptr, qbytes);
     const bufrsrc_t sr = make_rsrc(CK ? p.scales : nullptr, sbytes);
-    const bufrsrc_t zr = make_rsrc(SRC == SRC_GPTQ ? p.qzeros : nullptr, zbytes);
-    const int bpg = CK ? p.G / 128 : 1;        // checkpoint: blocks per group (G % 128 == 0)
+    const bufrsrc_t zr = make_rsrc(ZQ ? p.qzeros : nullptr, zbytes);
+    const int bpg = CK && p.G >= 128 ? p.G / 128 : 1;   // checkpoint: blocks per group (plain order: G % 128 == 0)
     const bufrsrc_t xrs = make_rsrc(p.x, (uint32_t)M * (uint32_t)p.K * 2u);
     // XD 1: the wave's x, block j at 4 KiB j; XD 2: its R slots, block j's tile tt at
     // ((j % R) MT + tt) 4 KiB
     unsigned char* xw = lds + (size_t)wave * (XD == 1 ? BPW * 4096 : R * MT * 4096);
     (void)pr; (void)qr; (void)sr; (void)zr; (void)bpg; (void)nc; (void)s0; (void)n0; (void)tbytes;
+
+    // act-order: the table [K/G][16 S] and the rows' offsets into it [K], after the waves' x
+    constexpr int WN = 16 * S;
+    const int NG = p.K / p.G;
+    uint32_t* tab = reinterpret_cast<uint32_t*>(lds + (size_t)W * (XD == 1 ? BPW * 4096 : R * MT * 4096));
+    int* gof = reinterpret_cast<int*>(tab + (ACT ? NG * WN : 0));
+    (void)tab; (void)gof;
+    u32x2 tsv[ACT ? ACT_TI : 1];
+    uint32_t tzv[ACT ? ACT_TI : 1];
+    u32x4 giv[ACT ? 2 : 1];
+    (void)tsv; (void)tzv; (void)giv;
+    if constexpr (ACT) {
+        // issued first: pass i of thread t covers columns 4 q .. 4 q + 3 of group g,
+        // u = t + 512 i = g (WN / 4) + q; then g_idx rows 8 t .. 8 t + 7
+        const bufrsrc_t gr = make_rsrc(p.g_idx, (uint32_t)p.K * 4u);
+#pragma unroll
+        for (int i = 0; i < ACT_TI; ++i) {
+            const int u = t + 512 * i, g = u / (WN / 4), q = u - g * (WN / 4);
+            const bool in = g < NG;
+            tsv[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                sr, in ? (uint32_t)(g * p.N + n0 + 4 * q) * 2u : sbytes, 0, 0));
+            if constexpr (ZQ)
+                tzv[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                    zr, in ? (uint32_t)(g * (p.N >> 3) + ((n0 + 4 * q) >> 3)) * 4u : zbytes, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            giv[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(gr, (uint32_t)(8 * t + 4 * i) * 4u, 0, 0));
+    }
 
     // prepared: ev = table entries, wv = 16-byte lane chunks (one per strip); checkpoint:
     // ev[j][0] = the zero word, cs = the lane's S scales (raw), cw = word st of every column
@@ -714,7 +756,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
         if constexpr (CK) {
             const int g = kb / bpg;
             const uint32_t so = kin ? (uint32_t)(g * p.N + nc) * 2u : sbytes;
-            cs[j] = ck_load<S / 2>(sr, so);
+            if constexpr (!ACT) cs[j] = ck_load<S / 2>(sr, so);
             if constexpr (SRC == SRC_GPTQ)
                 ev[j][0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
                     zr, kin ? (uint32_t)(g * (p.N >> 3) + (nc >> 3)) * 4u : zbytes, 0, 2);
@@ -771,10 +813,49 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     }
 #pragma unroll
     for (int j = 0; j < PD; ++j) load(j);
+    if constexpr (ACT) {
+        // the act-order table and offsets into LDS (their loads were issued first), then one
+        // barrier; the x and weight loads stay in flight
+#pragma unroll
+        for (int i = 0; i < ACT_TI; ++i) {
+            const int u = t + 512 * i, g = u / (WN / 4), q = u - g * (WN / 4);
+            if (g < NG) {
+                uint32_t e[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const uint32_t sb = (c & 1 ? tsv[i][c >> 1] >> 16 : tsv[i][c >> 1]) & 0xFFFFu;
+                    const uint32_t z = ZQ ? ((tzv[i] >> (4 * ((n0 + 4 * q + c) & 7))) & 0xFu) + (uint32_t)p.zero_offset
+                                          : 8u;
+                    e[c] = sb | ((0x6400u + z) << 16);
+                }
+                *reinterpret_cast<u32x4*>(tab + g * WN + 4 * q) = u32x4{e[0], e[1], e[2], e[3]};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            u32x4 o;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c] = (uint32_t)(min(max((int)giv[i][c], 0), NG - 1) * WN);
+            if (8 * t + 4 * i < p.K) *reinterpret_cast<u32x4*>(gof + 8 * t + 4 * i) = o;
+        }
+        __syncthreads();
+    }
     if constexpr (XD == 1) {
         wait_vmcnt<LOPS * BPW>();           // the x loads, issued before every other load
         asm volatile("" ::: "memory");      // the LDS reads below stay after the wait
     }
+
+    // act-order: the lane's 32 row offsets of block j (rows 128 kb + 32 h + [0, 32))
+    u32x4 gq[ACT ? 8 : 1];
+    (void)gq;
+    auto read_gq = [&](const int j) __attribute__((always_inline)) {
+        if constexpr (ACT) {
+            const int* go = gof + min(wave * BPW + j, KB - 1) * 128 + 32 * h;   // blocks past K add zero x
+#pragma unroll
+            for (int i = 0; i < 8; ++i) gq[i] = *reinterpret_cast<const u32x4*>(go + 4 * i);
+        }
+    };
+    read_gq(0);
 
     float acc[S][MT][4];
 #pragma unroll
@@ -809,12 +890,28 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             for (int st = 0; st < 4; ++st)
                 A[0][st] = *reinterpret_cast<const u32x4*>(xw + j * 4096 + r * 256 + (((4 * h + st) ^ r) << 4));
         }
+        // act-order: the table entries of the lane's 32 rows, S columns each, through the row
+        // offsets read one block ahead (gq), so that no entry read waits on an offset read
+        typename ck_words<ACT ? S : 1>::type ent[ACT ? 4 : 1][ACT ? 8 : 1];
+        (void)ent;
+        if constexpr (ACT) {
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t o[8] = {gq[2 * st].x, gq[2 * st].y, gq[2 * st].z, gq[2 * st].w,
+                                       gq[2 * st + 1].x, gq[2 * st + 1].y, gq[2 * st + 1].z, gq[2 * st + 1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    ent[st][e] = *reinterpret_cast<const typename ck_words<S>::type*>(tab + o[e] + S * col);
+            }
+            if (j + 1 < BPW) read_gq(j + 1);
+        }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             // the (scale, zero) of sub-block s and -(1024 + z) as an fp16 pair (exact bits)
-            uint32_t zq;
-            float sc;
-            if constexpr (CK) {
+            uint32_t zq = 0;
+            float sc = 0.f;
+            if constexpr (ACT) {
+            } else if constexpr (CK) {
                 const uint32_t sw = ck_word<(S + 1) / 2>(cs[j], s >> 1);
                 sc = (float)__builtin_bit_cast(half_t, (uint16_t)(sw >> (16 * (s & 1))));
                 zq = SRC == SRC_GPTQ ? ((ev[j][0] >> (4 * ((nc + s) & 7))) & 0xFu) + (uint32_t)p.zero_offset : 8u;
@@ -827,7 +924,19 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             half8_t B[4];
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
-                if constexpr (CK) {
+                if constexpr (ACT) {
+                    // per row pair: (1024 + z0, 1024 + z1) and (s0, s1) from the two entries
+                    const uint32_t q = ck_word<S>(cw[j][st], s);
+                    uint32_t wp[4];
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp) {
+                        const uint32_t e0 = ck_word<S>(ent[st][2 * pp], s), e1 = ck_word<S>(ent[st][2 * pp + 1], s);
+                        const half2_t zz = as_h2(perm(e1, e0, 0x07060302u));
+                        const half2_t ss = as_h2(perm(e1, e0, 0x05040100u));
+                        wp[pp] = as_u32((as_h2(gptq_pair(q, 2 * pp)) - zz) * ss);
+                    }
+                    B[st] = __builtin_bit_cast(half8_t, u32x4{wp[0], wp[1], wp[2], wp[3]});
+                } else if constexpr (CK) {
                     // W16 = RNE_f16((q - z) s) per weight, as the reference dequantises
                     // (w4a16_gptq_gemm_typed.rs:246-260): q - z exact, one rounded multiply
                     const uint32_t q = ck_word<S>(cw[j][st], s);
@@ -966,11 +1075,12 @@ constexpr bool ck_frag_fits(int mt, int s, int bpw) {
 // The same kernel on a GPTQ / GPTQ_SYM checkpoint as stored: 16 s columns per workgroup, s
 // columns per lane (N a multiple of 16 s), G a multiple of 128, fewer than 2^31 bytes per
 // tensor.
-PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G) {
+PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G, bool act) {
     PrepFragShape s{};
     if ((fmt != FMT_GPTQ && fmt != FMT_GPTQ_SYM) || M < 1 || M > PREP_FRAG_MAX_M || N % 16 ||
-        K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
+        K % 128 || G < 1 || K % G || K > PREP_MAX_K || (!act && (G < 128 || G % 128)))
         return s;
+    if (act && (K > ACT_MAX_K || G % 8)) return s;
     if ((size_t)K / 8 * N * 4 >= ((size_t)1 << 31) || (size_t)K / G * N * 2 >= ((size_t)1 << 31))
         return s;
     const int KB = K / 128;
@@ -981,7 +1091,16 @@ PrepFragShape ck_frag_shape(int fmt, int M, int N, int K, int G) {
         if (N % (16 * c) == 0 && N / (16 * c) >= 192) { s.s = c; break; }
     while (s.s > 1 && !ck_frag_fits(s.mt, s.s, bpw)) s.s /= 2;
     if (!ck_frag_fits(s.mt, s.s, bpw)) return s;
+    if (act) {   // the table (4 columns of a group per thread and pass) and the row offsets
+        if (s.mt == 2 && s.s == 4) s.s = 2;   // that instance would spill
+        while (s.s > 1 && (size_t)(K / G) * 16 * s.s > (size_t)ACT_MAX_ENTRIES) s.s /= 2;
+        if ((size_t)(K / G) * 16 * s.s > (size_t)ACT_MAX_ENTRIES || (16 * s.s) % 4) return s;
+    }
     frag_common(s, KB);
+    if (act) {
+        s.lds += (size_t)(K / G) * 16 * s.s * 4 + (size_t)K * 4;
+        if (s.lds > 160 * 1024) s.ok = false;
+    }
     return s;
 }
 
@@ -1001,6 +1120,11 @@ static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragSha
     // the checkpoint ones ck_frag_fits excludes
     auto fits = [](int bpw) { return SRC == SRC_PREP ? !(S == 4 && bpw == 32) : ck_frag_fits(MT, S, bpw); };
     if (!fits(s.bpw)) return hipErrorInvalidValue;
+    if constexpr (SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT) {   // K <= 4096: 4 blocks per wave
+        if (s.bpw != 4) return hipErrorInvalidValue;
+        launch_frag_inst<MT, S, 4, SRC>(p, s, st);
+        return hipGetLastError();
+    } else {
     switch (s.bpw) {
         case 4: launch_frag_inst<MT, S, 4, SRC>(p, s, st); break;
         case 8: if constexpr (SRC == SRC_PREP || ck_frag_fits(MT, S, 8)) { launch_frag_inst<MT, S, 8, SRC>(p, s, st); break; }
@@ -1012,6 +1136,7 @@ static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragSha
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+    }
 }
 
 template <int MT, int SRC>
@@ -1043,6 +1168,11 @@ hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hip
 }
 
 hipError_t launch_ck_frag(int fmt, const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
+    if (p.g_idx) {
+        if (fmt == FMT_GPTQ) return launch_frag_src<SRC_GPTQ_ACT>(p, s, st);
+        if (fmt == FMT_GPTQ_SYM) return launch_frag_src<SRC_SYM_ACT>(p, s, st);
+        return hipErrorInvalidValue;
+    }
     if (fmt == FMT_GPTQ) return launch_frag_src<SRC_GPTQ>(p, s, st);
     if (fmt == FMT_GPTQ_SYM) return launch_frag_src<SRC_GPTQ_SYM>(p, s, st);
     return hipErrorInvalidValue;
