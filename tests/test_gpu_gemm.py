@@ -434,9 +434,12 @@ def test_act_order_config2_full_size(torch_cuda, orc, M):
 @pytest.mark.parametrize("fmt,M,K,N,G,zo", [(SYM, 8, 2048, 512, 128, 1), (GPTQ, 1, 1024, 256, 64, 0),
                                             (GPTQ, 40, 1408, 640, 128, 1), (GPTQ, 5, 512, 64, 32, 1),
                                             (GPTQ, 16, 8192, 256, 32, 1), (SYM, 32, 2048, 512, 32, 1),
-                                            (GPTQ, 33, 16384, 3072, 256, 0)])
+                                            (GPTQ, 33, 16384, 3072, 256, 0),
+                                            (GPTQ, 16, 4096, 6144, 32, 1), (SYM, 3, 2048, 512, 64, 1)])
 def test_act_order_shapes(torch_cuda, orc, fmt, M, K, N, G, zo):
-    """Act-order over formats, zero offsets, group sizes, strip widths and split counts.
+    """Act-order over formats, zero offsets, group sizes, strip widths and split counts; the
+    direct-x kernel's (scale, zero) table at its largest (K=4096, G=32, N=6144: 128 groups x
+    32 columns) and from 3 rows with G=64.
     K=8192 with G=32 fills the LDS budget with the group table (256 groups), so g_idx is
     read from global memory per step and the table is built after the weight stream is
     issued; the other shapes stage the workgroup's g_idx slice in LDS, K=16384 over two
@@ -519,12 +522,12 @@ def test_act_order_large_m_unequal_groups_runs_generic(torch_cuda, orc):
     assert_parity(y, _oracle(orc, p, g_idx=g_idx), what="act-order unequal groups")
 
 
-@pytest.mark.parametrize("M", [16, 80])
+@pytest.mark.parametrize("M", [16, 40, 80])
 def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc, M):
     """The device cannot report a bad g_idx without a host round trip; entries outside
-    [0, K/G) are clamped into the scale table (the oracle, which rejects them, is given the
-    clamped index). Beyond 64 rows the group-order check sees them and the generic kernel
-    runs."""
+    [0, K/G) are clamped into the scale table (the split-K kernel at 16 rows, the direct-x
+    kernel's table offsets at 40; the oracle, which rejects them, is given the clamped
+    index). Beyond 64 rows the group-order check sees them and the generic kernel runs."""
     p = Problem(GPTQ, M=M, K=1024, N=256, G=128, seed=1340, act_order=True)
     bad = p.g_idx.copy()
     bad[3], bad[700] = 99, -5
