@@ -227,8 +227,8 @@ def test_prepared_kernels_isa(tmp_path):
         assert "v_mfma" not in b and "v_dot2" in b and "atomic" not in b, n
     fr = {n: b for n, b in k.items() if "gemm_prep_frag_kernel" in n}
     assert len(fr) >= 20
-    for n, b in fr.items():
-        assert "v_mfma_f32_16x16x32_f16" in b and "v_and_or_b32" in b, n
+    for n, b in fr.items():   # the nibble pairs by v_and_or_b32, or v_or3_b32 after a mask
+        assert "v_mfma_f32_16x16x32_f16" in b and ("v_and_or_b32" in b or "v_or3_b32" in b), n
         assert "atomic" not in b and "scratch_" not in b and "buffer_store" not in b, n
 
 

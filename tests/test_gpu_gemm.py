@@ -522,6 +522,43 @@ def test_act_order_large_m_unequal_groups_runs_generic(torch_cuda, orc):
     assert_parity(y, _oracle(orc, p, g_idx=g_idx), what="act-order unequal groups")
 
 
+def test_act_order_large_m_order_kept_between_calls(torch_cuda, orc):
+    """Beyond 64 rows the group order computed from g_idx stays on the stream's buffers and is
+    reused while g_idx, K and G are unchanged. One stream, calls that change g_idx (another
+    order; two rows of different groups swapped; one row moved to another group, so the groups
+    are unequal) and then G with the same g_idx (8 groups of 128 rows: valid for G = 128,
+    unequal for G = 64), each against the oracle; a repeated g_idx gives its first call's bits."""
+    K, N, M = 1024, 256, 96
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=1337, act_order=True)
+    p64 = Problem(GPTQ, M=M, K=K, N=N, G=64, seed=1338)
+    p64.x = p.x
+    rng = np.random.default_rng(1337)
+    a = p.g_idx
+    b = (np.arange(K) // 128)[rng.permutation(K)].astype(np.int32)
+    i = 0
+    j = int(np.nonzero(a != a[i])[0][0])
+    swapped = a.copy()
+    swapped[[i, j]] = a[[j, i]]
+    unequal = a.copy()
+    unequal[i] = a[j]
+    c = (np.arange(K) // 128).astype(np.int32)[::-1].copy()
+    first = _run_gemm(torch_cuda, p, g_idx=a)
+    assert_parity(first, _oracle(orc, p, g_idx=a), what="g_idx a")
+    again = _run_gemm(torch_cuda, p, g_idx=a)
+    assert np.array_equal(first.view(np.uint16), again.view(np.uint16)), "repeated g_idx differs"
+    for name, g in (("b", b), ("two rows swapped", swapped), ("unequal groups", unequal)):
+        y = _run_gemm(torch_cuda, p, g_idx=g)
+        assert_parity(y, _oracle(orc, p, g_idx=g), what=f"g_idx {name}")
+    y = _run_gemm(torch_cuda, p, g_idx=a)
+    assert np.array_equal(first.view(np.uint16), y.view(np.uint16)), "g_idx a after others"
+    y = _run_gemm(torch_cuda, p, g_idx=c)
+    assert_parity(y, _oracle(orc, p, g_idx=c), what="g_idx c, G=128")
+    y = _run_gemm(torch_cuda, p64, g_idx=c)
+    assert_parity(y, _oracle(orc, p64, g_idx=c), what="g_idx c, G=64 (unequal groups)")
+    y = _run_gemm(torch_cuda, p, g_idx=a)
+    assert np.array_equal(first.view(np.uint16), y.view(np.uint16)), "g_idx a after G=64"
+
+
 @pytest.mark.parametrize("M", [16, 40, 80])
 def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc, M):
     """The device cannot report a bad g_idx without a host round trip; entries outside

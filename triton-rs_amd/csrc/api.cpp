@@ -424,7 +424,8 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
 
     // act-order beyond the small-batch kernel's rows: per call, the group order of the rows is
     // computed on the device (perm, and a gate word that is 1 when every group holds exactly G
-    // rows), the packed rows are repacked into it and x's columns gathered by it, then the
+    // rows; kept from the stream's previous call when g_idx, K and G are the same), the packed
+    // rows are repacked into it and x's columns gathered by it (one launch), then the
     // prefill kernel runs on them when the gate is 1 and the generic kernel on the checkpoint
     // when it is 0 (each reads the gate and returns at once when it is not the one wanted).
     // Without the per-stream buffers (allocation-free entry) the generic kernel alone runs.
@@ -433,15 +434,19 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
         const size_t perm_bytes = ((size_t)K * 4 + 255) & ~(size_t)255;
         void* ws = nullptr;
         void* xg = nullptr;
-        rc = stream_buffer(g_actorder, st, perm_bytes + 256 + (size_t)K / 8 * N * 4, 0, "act-order repack buffer", &ws);
+        // [header 256 B: gate word, then the order's memo (valid, K, G); cleared when the
+        //  buffer is allocated][perm][copy of the g_idx perm was computed from][repacked rows]
+        rc = stream_buffer(g_actorder, st, 256 + 2 * perm_bytes + (size_t)K / 8 * N * 4, 256, "act-order repack buffer", &ws);
         if (!rc) rc = stream_buffer(g_gather, st, (size_t)M * K * sizeof(half_t), 0, "act-order gather buffer", &xg);
         if (rc) return rc;
-        int32_t* perm = static_cast<int32_t*>(ws);
-        uint32_t* gw = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + perm_bytes);
-        uint32_t* qout = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + perm_bytes + 256);
-        hipError_t e = launch_act_order_perm(g_idx, perm, gw, K, G, st);
-        if (e == hipSuccess) e = launch_gptq_repack_rows(static_cast<const uint32_t*>(qweight), perm, qout, K, N, st);
-        if (e == hipSuccess) e = launch_gather_columns(static_cast<const half_t*>(x), perm, static_cast<half_t*>(xg), M, K, st);
+        uint32_t* gw = static_cast<uint32_t*>(ws);
+        int32_t* perm = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + 256);
+        int32_t* gcopy = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + 256 + perm_bytes);
+        uint32_t* qout = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + 256 + 2 * perm_bytes);
+        hipError_t e = launch_act_order_perm(g_idx, perm, gw, gcopy, K, G, st);
+        if (e == hipSuccess)
+            e = launch_act_order_stage(static_cast<const uint32_t*>(qweight), perm, qout,
+                                       static_cast<const half_t*>(x), static_cast<half_t*>(xg), M, K, N, st);
         if (e != hipSuccess) return hip_fail(e, "act-order group order launch");
         if ((rc = run_prefill(xg, qout, gw))) return rc;
         gate = gw;

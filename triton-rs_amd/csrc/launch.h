@@ -216,11 +216,18 @@ hipError_t launch_dequant(int fmt, const DequantParams& p, hipStream_t st, bool 
 // in the order perm (row j of qout = row perm[j] of q); xout [M, K] = x[:, perm].
 hipError_t launch_gptq_repack_rows(const uint32_t* q, const int32_t* perm, uint32_t* qout, int K,
                                    int N, hipStream_t st);
-// perm (K entries) of the rows in group order, computed on the device from g_idx, and gate[0] =
-// 1 when every group holds exactly G rows, else 0 (perm then the identity). K <= 32768,
-// K / G <= 1024.
-hipError_t launch_act_order_perm(const int32_t* g_idx, int32_t* perm, uint32_t* gate, int K, int G,
-                                 hipStream_t st);
+// perm (K entries) of the rows in group order, computed on the device from g_idx, and hdr[0]
+// (the gate word) = 1 when every group holds exactly G rows, else 0 (perm then the identity).
+// hdr[1..3] (16 bytes, zero when first used) and gcopy (K entries) keep what the result was
+// computed from, so that a call with the same g_idx, K and G returns after the compare.
+// K <= 32768, K / G <= 1024.
+hipError_t launch_act_order_perm(const int32_t* g_idx, int32_t* perm, uint32_t* hdr, int32_t* gcopy,
+                                 int K, int G, hipStream_t st);
+// launch_gptq_repack_rows and launch_gather_columns in one launch (the two passes side by side)
+// where K % 32 == 0, K <= 32768 and x, perm, xout are 16-byte aligned; else the two launches.
+hipError_t launch_act_order_stage(const uint32_t* q, const int32_t* perm, uint32_t* qout,
+                                  const half_t* x, half_t* xout, int M, int K, int N,
+                                  hipStream_t st);
 hipError_t launch_gather_columns(const half_t* x, const int32_t* perm, half_t* xout, int M, int K,
                                  hipStream_t st);
 

@@ -1144,7 +1144,9 @@ static hipError_t launch_prep_frag_m(const PrepFragParams& p, const PrepFragShap
     switch (s.s) {
         case 1: return launch_prep_frag_ms<MT, 1, SRC>(p, s, st);
         case 2: return launch_prep_frag_ms<MT, 2, SRC>(p, s, st);
-        case 4: if constexpr (MT <= 2) return launch_prep_frag_ms<MT, 4, SRC>(p, s, st);
+        // act-order at 2 row tiles: 2 strips (ck_frag_shape), 4 would spill
+        case 4: if constexpr (MT == 1 || (MT == 2 && SRC != SRC_GPTQ_ACT && SRC != SRC_SYM_ACT))
+                    return launch_prep_frag_ms<MT, 4, SRC>(p, s, st);
                 [[fallthrough]];
         default: return hipErrorInvalidValue;
     }
