@@ -562,6 +562,27 @@ def extras(torch, pkg, dev, stream, args):
         preplayout_case(f"c2_gptq_actorder_preplayout_m{M}_k4096_n6144", M, 40, 500)
     preplayout_case("c2_gptq_actorder_preplayout_m2048_k4096_n6144", 2048, 2, 200)
 
+    # config 2's act-order layer prepared as stored (w4a16_prepare_layout on the checkpoint, rows
+    # in their own order): per call, w4a16_gemm_prepared_gidx with g_idx (no repack, no gather)
+    def prepstored_case(tag, M, n_sets, calls):
+        K, N, G = 4096, 6144, 128
+        sets = make_weight_sets(torch, "gptq", K, N, G, n_sets, dev, seed=zlib.crc32(tag.encode()))
+        preps = [pkg.prepare_layout(qw, sc, qz, fmt="gptq", group_size=G, zero_offset=1)
+                 for qw, sc, qz in sets]
+        del sets
+        x = torch.randn((M, K), device=dev, generator=gen).half()
+        out = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+        def fn(i):
+            pkg.gemm_prepared(x, preps[i % n_sets], g_idx=g_idx, out=out)
+        ms = time_calls(torch, fn, GRAPH_CALLS, 10, stream, n_sets, batch_calls=calls,
+                        n_graphs=min(10, max(1, 1000 // GRAPH_CALLS)))[1]
+        record(tag, "gptq", M, K, N, G, ms, "prepared+g_idx/small-batch", act_order=True)
+        del preps
+
+    for M in (16, 32, 64):
+        prepstored_case(f"c2_gptq_actorder_prepstored_m{M}_k4096_n6144", M, 40, 500)
+
     gemm_case("c3_awq_m2048_k4096_n14336", "awq", 2048, 4096, 14336, 128, 2, 300)
     gemm_case("c3_awq_m2048_k14336_n4096", "awq", 2048, 14336, 4096, 128, 2, 300)
     # the same workloads with bfloat16 activations, scales and output

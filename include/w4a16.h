@@ -188,6 +188,19 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
                                   int32_t K, int32_t group_size);
 W4A16_API int w4a16_dequant_prepared(void* stream, const void* prepared, void* out, int32_t K,
                                      int32_t N, int32_t group_size, int transposed);
+/* w4a16_gemm_prepared_gidx: out[M, N] = x[M, K] @ W16 for an act-order (desc_act) GPTQ
+ * checkpoint prepared as stored (w4a16_prepare_layout on its qweight, scales and qzeros, rows
+ * in their own order): g_idx [K] gives row k's group, read from the strips' tables (their
+ * rows hold every group's scale and zero point). No counterpart in the reference, whose GEMM
+ * takes group k / group_size (w4a16_gptq_gemm_typed.rs:221); it spares an act-order layer the
+ * group-order repack (w4a16_prepare_act_order) and the per-call gather of x's columns. Up to
+ * 64 rows with K <= 4096 a small-batch kernel reading x as stored, one workgroup per 1, 2 or
+ * 4 strips over all of K; other shapes the generic kernel. g_idx entries outside
+ * [0, K / group_size) are clamped. Same alignment as w4a16_gemm_prepared, g_idx 16-byte
+ * aligned. */
+W4A16_API int w4a16_gemm_prepared_gidx(void* stream, const void* x, const void* prepared,
+                                       const int32_t* g_idx, void* out, int32_t M, int32_t N,
+                                       int32_t K, int32_t group_size);
 
 /* Which kernel w4a16_gemm would run for this problem (no GPU access). */
 W4A16_API int w4a16_gemm_plan(int fmt, int32_t M, int32_t N, int32_t K, int32_t group_size,

@@ -235,3 +235,52 @@ def test_gemm_prepared_small_batch_exact_arithmetic(torch_cuda, orc):
         ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
                              g_idx=p.g_idx if act else None, zero_offset=p.zero_offset)
         assert np.array_equal(y.view(np.uint16), ref.view(np.uint16)), (NAME[fmt], M, act)
+
+
+@pytest.mark.parametrize("fmt,M,K,N,G", [
+    (GPTQ, 16, 4096, 6144, 128), (GPTQ, 64, 4096, 6144, 128),   # config 2, as stored + g_idx
+    (GPTQ, 1, 2048, 512, 128), (GPTQ, 7, 1024, 6160, 128), (SYM, 40, 2048, 1024, 128),
+    (GPTQ, 24, 1024, 512, 32), (SYM, 9, 512, 2048, 64), (GPTQ, 33, 4096, 256, 256),
+    (GPTQ, 100, 1024, 256, 128), (GPTQ, 5, 8192, 128, 128),     # generic kernel: M > 64, K > 4096
+])
+def test_gemm_prepared_gidx_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
+    """An act-order checkpoint prepared as stored (rows in their own order) with g_idx
+    (w4a16_gemm_prepared_gidx): the small-batch kernel's (scale, zero) table filled from the
+    strips' tables, or the generic kernel reading each group's table row; against the oracle's
+    act-order GEMM on the checkpoint."""
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=0x5EED0300 + M + K, act_order=True)
+    y = P.gemm_prepared(to_dev(p.x), _prep(P, p), g_idx=to_dev(p.g_idx)).cpu().numpy()
+    ref = orc.w4a16_gemm(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, G, g_idx=p.g_idx,
+                         zero_offset=p.zero_offset, want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"prepared g_idx {NAME[fmt]} M={M} K={K} N={N} G={G}")
+
+
+@pytest.mark.parametrize("fmt,M,G", [(GPTQ, 32, 128), (GPTQ, 64, 128), (SYM, 48, 128), (GPTQ, 40, 64)])
+def test_gemm_prepared_gidx_equals_checkpoint_route(torch_cuda, fmt, M, G):
+    """Beyond 16 rows w4a16_gemm runs the same small-batch kernel on the checkpoint as stored
+    (K = 4096 over 8 waves of 4 blocks, the same W16 per weight and the same MFMA chain): on
+    the prepared strips with g_idx the output is bit for bit the checkpoint call's."""
+    P = pkg()
+    K, N = 4096, 6144
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=0x5EED0310 + M, act_order=True)
+    g_idx = to_dev(p.g_idx)
+    y = P.gemm_prepared(to_dev(p.x), _prep(P, p), g_idx=g_idx).cpu().numpy()
+    assert P.plan(NAME[fmt], M, N, K, G, has_g_idx=True) == "skinny"
+    ck = P.gemm(to_dev(p.x), to_dev(p.qweight), to_dev(p.scales),
+                None if p.qzeros is None else to_dev(p.qzeros), fmt=NAME[fmt], group_size=G,
+                g_idx=g_idx, zero_offset=p.zero_offset).cpu().numpy()
+    assert np.array_equal(y.view(np.uint16), ck.view(np.uint16))
+
+
+def test_gemm_prepared_gidx_clamps_and_unequal_groups(torch_cuda, orc):
+    """g_idx entries outside [0, K/G) are clamped into the table (as w4a16_gemm does), and
+    groups of unequal size need nothing else: each row reads its own group's entry."""
+    P = pkg()
+    p = Problem(GPTQ, M=20, K=1024, N=512, G=128, seed=0x5EED0320, act_order=True)
+    bad = p.g_idx.copy()
+    bad[3], bad[700], bad[10] = 99, -5, bad[11]
+    y = P.gemm_prepared(to_dev(p.x), _prep(P, p), g_idx=to_dev(bad)).cpu().numpy()
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, p.K, p.N, p.G,
+                         g_idx=np.clip(bad, 0, p.K // p.G - 1).astype(np.int32), want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what="prepared g_idx clamped / unequal")

@@ -71,7 +71,7 @@ EXPORTED = (
     "w4a16_last_error", "w4a16_version", "w4a16_init", "w4a16_gemm", "w4a16_gemm_noalloc",
     "w4a16_gemm_noalloc_scratch_bytes", "w4a16_gemm_plan", "w4a16_prepare_act_order",
     "w4a16_gemm_act_order", "w4a16_prepared_bytes", "w4a16_prepare_layout",
-    "w4a16_gemm_prepared", "w4a16_dequant_prepared",
+    "w4a16_gemm_prepared", "w4a16_dequant_prepared", "w4a16_gemm_prepared_gidx",
     "w4a16_typed_plan",
     "w4a16_gptq_gemm_typed", "awq_gemm_int4_typed", "dequant_int4_to_fp16",
     "dequant_int4_sym_to_fp16", "w4a16_dequant", "w4a16_moe_route", "w4a16_moe_align",
@@ -108,6 +108,7 @@ def lib() -> ctypes.CDLL:
         L.w4a16_prepared_bytes.argtypes = [_I, _I, _I]
         L.w4a16_prepare_layout.argtypes = [_P, _I, _P, _P, _P, _I, _I, _I, _I, _P, _Z]
         L.w4a16_gemm_prepared.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
+        L.w4a16_gemm_prepared_gidx.argtypes = [_P, _P, _P, _P, _P, _I, _I, _I, _I]
         L.w4a16_dequant_prepared.argtypes = [_P, _P, _P, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc.argtypes = [_P, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I]
         L.w4a16_gemm_noalloc_scratch_bytes.restype = ctypes.c_size_t
@@ -350,18 +351,30 @@ def prepare_layout(qweight, scales, qzeros, fmt="awq", group_size: int = 128,
 
 
 def gemm_prepared(x: torch.Tensor, w: PreparedWeights, perm: torch.Tensor | None = None,
-                  out: torch.Tensor | None = None) -> torch.Tensor:
+                  out: torch.Tensor | None = None, g_idx: torch.Tensor | None = None) -> torch.Tensor:
     """out[M, N] = x[M, K] @ W16 from prepared weights (perm: an act-order checkpoint repacked
-    by prepare_act_order before prepare_layout; x's columns are gathered by it first)."""
+    by prepare_act_order before prepare_layout; x's columns are gathered by it first. g_idx:
+    an act-order checkpoint prepared as stored, g_idx[k] the group of row k
+    (w4a16_gemm_prepared_gidx))."""
     _require(x, "x", _HALF)
+    if perm is not None and g_idx is not None:
+        raise InvalidArgument("give perm (group-order repack) or g_idx (rows as stored), not both")
     if perm is not None:
         _require(perm, "perm", _INT32, x.device)
+    if g_idx is not None:
+        _require(g_idx, "g_idx", _INT32, x.device)
+        if g_idx.dim() != 1 or g_idx.numel() != w.K or not g_idx.is_contiguous():
+            raise InvalidArgument(f"g_idx must be a contiguous int32 vector of K={w.K} entries")
     if x.dim() != 2 or not x.is_contiguous():
         raise InvalidArgument("x must be a contiguous 2-D tensor")
     M, K = x.shape
     if K != w.K:
         raise InvalidArgument(f"x has K={K}, the prepared weights K={w.K}")
     out = _gemm_out(out, M, w.N, x.device)
+    if g_idx is not None:
+        check(lib().w4a16_gemm_prepared_gidx(_stream(x), _ptr(x), _ptr(w.buffer), _ptr(g_idx),
+                                             _ptr(out), M, w.N, K, w.group_size))
+        return out
     check(lib().w4a16_gemm_prepared(_stream(x), _ptr(x), _ptr(w.buffer), _ptr(perm), _ptr(out),
                                     M, w.N, K, w.group_size))
     return out

@@ -740,6 +740,46 @@ W4A16_API int w4a16_gemm_prepared(void* stream, const void* x, const void* prepa
     return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared strided gemm launch");
 }
 
+W4A16_API int w4a16_gemm_prepared_gidx(void* stream, const void* x, const void* prepared,
+                                       const int32_t* g_idx, void* out, int32_t M, int32_t N,
+                                       int32_t K, int32_t G) {
+    if (int rc = check_prep_shape(K, N, G)) return rc;
+    if (!x || !prepared || !g_idx || !out) return fail(W4A16_ERR_INVALID_ARG, "null pointer argument");
+    if (M < 1) return fail(W4A16_ERR_INVALID_ARG, "M (%d) must be positive", M);
+    if (!aligned(x, 16) || !aligned(prepared, 256) || !aligned(out, 16) || !aligned(g_idx, 16))
+        return fail(W4A16_ERR_INVALID_ARG,
+                    "x, out and g_idx must be 16-byte aligned, prepared 256-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // up to 64 rows (K <= 4096): the small-batch kernel with the per-workgroup (scale, zero)
+    // table filled from the strips' own tables and indexed through g_idx; x read as stored
+    const PrepFragShape fs = prep_frag_shape(M, N, K, G, /*act=*/true);
+    if (fs.ok) {
+        PrepFragParams p{};
+        p.x = static_cast<const half_t*>(x);
+        p.prep = static_cast<const unsigned char*>(prepared);
+        p.g_idx = g_idx;
+        p.out = static_cast<half_t*>(out);
+        p.M = M; p.N = N; p.K = K; p.G = G;
+        p.strip_bytes = (uint32_t)prep_strip_bytes(K, G);
+        hipError_t e = launch_prep_frag(p, fs, st);
+        return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared act-order small-batch launch");
+    }
+    // any other shape: the generic kernel, each element's (scale, zero) from its group's row
+    // of the strip's table
+    StridedParams p{};
+    p.a = static_cast<const half_t*>(x);
+    p.qweight = static_cast<const uint32_t*>(prepared);
+    p.g_idx = g_idx;
+    p.c = static_cast<half_t*>(out);
+    p.m = M; p.n = N; p.k = K; p.group_size = G;
+    p.stride_am = K; p.stride_ak = 1;
+    p.stride_qwk = (int)(prep_strip_bytes(K, G) / 4);
+    p.stride_qwn = (int)prep_table_words(K, G);
+    p.stride_cm = N; p.stride_cn = 1;
+    hipError_t e = launch_strided_gemm(FMT_PREP, p, st);
+    return e == hipSuccess ? W4A16_OK : hip_fail(e, "prepared act-order strided gemm launch");
+}
+
 // The reference kernels' parameter lists with arbitrary strides. A call whose tensors are
 // the dense row-major layouts of the checkpoint formats (the usual case: a linear layer's
 // weights and activations) is the same problem w4a16_gemm solves, and goes through its

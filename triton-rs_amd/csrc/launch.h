@@ -295,7 +295,9 @@ hipError_t launch_prep_dequant(const void* prep, half_t* out, int K, int N, int 
                                hipStream_t st);
 PrepGemvShape prep_gemv_shape(int M, int N, int K, int G);
 hipError_t launch_prep_gemv(const PrepParams& p, const PrepGemvShape& s, hipStream_t st);
-PrepFragShape prep_frag_shape(int M, int N, int K, int G);
+// act: rows in the checkpoint's own order with p.g_idx (any group size of the layout,
+// K <= 4096, a table of at most 4096 entries)
+PrepFragShape prep_frag_shape(int M, int N, int K, int G, bool act = false);
 hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st);
 // The small-batch kernel on a GPTQ / GPTQ_SYM checkpoint as stored (no split-K, no scratch);
 // act: with g_idx (any group size, K <= 4096, a table of at most 4096 entries)

@@ -646,7 +646,16 @@ __device__ __forceinline__ void xd_wait(const int j) {
 // operand of step st then takes, per row pair, its two entries per column: v_perm_b32
 // assembles the pairs (1024 + z0, 1024 + z1) and (s0, s1), and W16 = RNE_f16((q - z) s)
 // as before (the weights stay bit-exact; any group size).
-constexpr int SRC_PREP = 0, SRC_GPTQ = 1, SRC_GPTQ_SYM = 2, SRC_GPTQ_ACT = 3, SRC_SYM_ACT = 4;
+//
+// Prepared act-order (SRC_PREP_ACT): the prepared layout of an act-order checkpoint as stored
+// (rows in their own order, g_idx gives each row's group). The strip's inline table holds every
+// group's (scale, full zero point) already (table row g (G / 128) for G >= 128, row g for G =
+// 32 or 64), so the workgroup's LDS table is filled from it, and the B operand is formed per
+// row pair as for the checkpoint (W16 = RNE_f16((q - z) s), accumulated in the MFMA chain)
+// from the prepared words (row pair (2 i, 2 i + 1) in nibble slots i and i + 4). The lane's S
+// strips sit at table positions S col + s, so its S entries are one read as for the checkpoint.
+constexpr int SRC_PREP = 0, SRC_GPTQ = 1, SRC_GPTQ_SYM = 2, SRC_GPTQ_ACT = 3, SRC_SYM_ACT = 4,
+              SRC_PREP_ACT = 5;
 // act-order: table entries per thread (4 columns of one group per pass, ACT_TI passes) and
 // g_idx rows per thread (two 16-byte loads): at most 4096 entries and K <= 4096
 constexpr int ACT_TI = 2, ACT_MAX_ENTRIES = 4 * 512 * ACT_TI, ACT_MAX_K = 8 * 512;
@@ -678,12 +687,15 @@ __device__ __forceinline__ uint32_t ck_word(const typename ck_words<S>::type& v,
 template <int MT, int S, int BPW, int PD, int XD, int SRC = SRC_PREP>
 __global__ void __launch_bounds__(512)
 gemm_prep_frag_kernel(PrepFragParams p) {
-    constexpr bool CK = SRC != SRC_PREP;
-    constexpr bool ACT = SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT;
+    constexpr bool PA = SRC == SRC_PREP_ACT;   // prepared strips with g_idx
+    constexpr bool CK = SRC != SRC_PREP && !PA;   // checkpoint tensors as stored
+    constexpr bool ACT = SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT || PA;
+    constexpr bool W16 = CK || ACT;   // W16 formed per weight, accumulated in the MFMA chain
     constexpr bool ZQ = SRC == SRC_GPTQ || SRC == SRC_GPTQ_ACT;    // zero points from qzeros
     // loads per block besides x: the table entries and weights of S strips (prepared); four
-    // words, the scales and the zero word (checkpoint); four words (act-order)
-    constexpr int LOPS = ACT ? 4 : CK ? (SRC == SRC_GPTQ ? 6 : 5) : 2 * S;
+    // words, the scales and the zero word (checkpoint); four words (act-order); the weights of
+    // S strips (prepared act-order)
+    constexpr int LOPS = PA ? S : ACT ? 4 : CK ? (SRC == SRC_GPTQ ? 6 : 5) : 2 * S;
     static_assert(PD >= 1 && PD <= BPW, "prefetch depth");
     static_assert(XD == 2 || (XD == 1 && MT == 1 && PD == BPW && LOPS * BPW <= 63),
                   "XD 1: one tile, all blocks up front");
@@ -722,21 +734,34 @@ gemm_prep_frag_kernel(PrepFragParams p) {
     (void)tab; (void)gof;
     u32x2 tsv[ACT ? ACT_TI : 1];
     uint32_t tzv[ACT ? ACT_TI : 1];
+    uint32_t pev[PA ? ACT_TI : 1][PA ? 4 : 1];
     u32x4 giv[ACT ? 2 : 1];
-    (void)tsv; (void)tzv; (void)giv;
+    (void)tsv; (void)tzv; (void)pev; (void)giv;
     if constexpr (ACT) {
-        // issued first: pass i of thread t covers columns 4 q .. 4 q + 3 of group g,
-        // u = t + 512 i = g (WN / 4) + q; then g_idx rows 8 t .. 8 t + 7
+        // issued first: pass i of thread t covers table positions 4 q .. 4 q + 3 of group g,
+        // u = t + 512 i = g (WN / 4) + q (checkpoint: columns n0 + 4 q + c; prepared: position
+        // S col + s = strip s0 + s, column col); then g_idx rows 8 t .. 8 t + 7
         const bufrsrc_t gr = make_rsrc(p.g_idx, (uint32_t)p.K * 4u);
+        const int trows = p.G >= 128 ? p.G / 128 : 1;   // prepared: table rows per group step
 #pragma unroll
         for (int i = 0; i < ACT_TI; ++i) {
             const int u = t + 512 * i, g = u / (WN / 4), q = u - g * (WN / 4);
             const bool in = g < NG;
-            tsv[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
-                sr, in ? (uint32_t)(g * p.N + n0 + 4 * q) * 2u : sbytes, 0, 0));
-            if constexpr (ZQ)
-                tzv[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                    zr, in ? (uint32_t)(g * (p.N >> 3) + ((n0 + 4 * q) >> 3)) * 4u : zbytes, 0, 0);
+            if constexpr (PA) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int pos = 4 * q + c, strip = s0 + pos % S, cl = pos / S;
+                    pev[i][c] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                        pr, in && strip < NS ? (uint32_t)strip * p.strip_bytes + (uint32_t)(g * trows * 16 + cl) * 4u
+                                             : pbytes, 0, 0);
+                }
+            } else {
+                tsv[i] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+                    sr, in ? (uint32_t)(g * p.N + n0 + 4 * q) * 2u : sbytes, 0, 0));
+                if constexpr (ZQ)
+                    tzv[i] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                        zr, in ? (uint32_t)(g * (p.N >> 3) + ((n0 + 4 * q) >> 3)) * 4u : zbytes, 0, 0);
+            }
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -769,6 +794,7 @@ gemm_prep_frag_kernel(PrepFragParams p) {
         } else {
 #pragma unroll
             for (int s = 0; s < S; ++s) {
+                if constexpr (PA) break;   // the entries come from the LDS table
                 const int strip = s0 + s;
                 const uint32_t off = kin && strip < NS ? (uint32_t)strip * p.strip_bytes + (uint32_t)(kb * 16 + col) * 4u
                                                        : pbytes;
@@ -823,6 +849,10 @@ gemm_prep_frag_kernel(PrepFragParams p) {
                 uint32_t e[4];
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
+                    if constexpr (PA) {   // prepared entry: scale | full zero point << 16
+                        e[c] = (pev[i][c] & 0xFFFFu) | ((0x6400u + (pev[i][c] >> 16)) << 16);
+                        continue;
+                    }
                     const uint32_t sb = (c & 1 ? tsv[i][c >> 1] >> 16 : tsv[i][c >> 1]) & 0xFFFFu;
                     const uint32_t z = ZQ ? ((tzv[i] >> (4 * ((n0 + 4 * q + c) & 7))) & 0xFu) + (uint32_t)p.zero_offset
                                           : 8u;
@@ -926,14 +956,17 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             for (int st = 0; st < 4; ++st) {
                 if constexpr (ACT) {
                     // per row pair: (1024 + z0, 1024 + z1) and (s0, s1) from the two entries
-                    const uint32_t q = ck_word<S>(cw[j][st], s);
+                    uint32_t q;
+                    if constexpr (PA) q = wv[j][s][st];
+                    else q = ck_word<S>(cw[j][st], s);
                     uint32_t wp[4];
 #pragma unroll
                     for (int pp = 0; pp < 4; ++pp) {
                         const uint32_t e0 = ck_word<S>(ent[st][2 * pp], s), e1 = ck_word<S>(ent[st][2 * pp + 1], s);
                         const half2_t zz = as_h2(perm(e1, e0, 0x07060302u));
                         const half2_t ss = as_h2(perm(e1, e0, 0x05040100u));
-                        wp[pp] = as_u32((as_h2(gptq_pair(q, 2 * pp)) - zz) * ss);
+                        const half2_t qp = PA ? nib_pair(q >> (4 * pp)) : as_h2(gptq_pair(q, 2 * pp));
+                        wp[pp] = as_u32((qp - zz) * ss);
                     }
                     B[st] = __builtin_bit_cast(half8_t, u32x4{wp[0], wp[1], wp[2], wp[3]});
                 } else if constexpr (CK) {
@@ -955,13 +988,13 @@ gemm_prep_frag_kernel(PrepFragParams p) {
             for (int tt = 0; tt < MT; ++tt) {
                 // checkpoint: the dot of x and W16 accumulates in the chain itself; prepared:
                 // the block's sum of x (q - z), scaled in fp32
-                float4_t d = CK ? float4_t{acc[s][tt][0], acc[s][tt][1], acc[s][tt][2], acc[s][tt][3]}
-                                : float4_t{0.f, 0.f, 0.f, 0.f};
+                float4_t d = W16 ? float4_t{acc[s][tt][0], acc[s][tt][1], acc[s][tt][2], acc[s][tt][3]}
+                                 : float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int st = 0; st < 4; ++st)
                     d = mfma16x16x32(__builtin_bit_cast(half8_t, A[tt][st]), B[st], d);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) acc[s][tt][i] = CK ? d[i] : __builtin_fmaf(sc, d[i], acc[s][tt][i]);
+                for (int i = 0; i < 4; ++i) acc[s][tt][i] = W16 ? d[i] : __builtin_fmaf(sc, d[i], acc[s][tt][i]);
             }
         }
     }
@@ -1051,10 +1084,13 @@ static void frag_common(PrepFragShape& s, int KB) {
     s.ok = true;
 }
 
-PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
+PrepFragShape prep_frag_shape(int M, int N, int K, int G, bool act) {
     PrepFragShape s{};
-    if (M < 1 || M > PREP_FRAG_MAX_M || N % 16 || K % 128 || G < 128 || G % 128 || K % G || K > PREP_MAX_K)
+    if (M < 1 || M > PREP_FRAG_MAX_M || N % 16 || K % 128 || K % G || K > PREP_MAX_K)
         return s;
+    // plain: G a multiple of 128 (one table entry per block); act-order: any group size of
+    // the layout, K within the table's row offsets
+    if (act ? (K > ACT_MAX_K || !prep_group_ok(G)) : (G < 128 || G % 128)) return s;
     if (prep_total_bytes(K, N, G) >= ((size_t)1 << 31)) return s;
     const int NS = N / 16, KB = K / 128;
     s.mt = (M + 15) / 16;
@@ -1062,7 +1098,16 @@ PrepFragShape prep_frag_shape(int M, int N, int K, int G) {
     const int bpw = KB <= 32 ? 4 : KB <= 64 ? 8 : KB <= 128 ? 16 : 32;
     for (int c = s.mt <= 2 && bpw <= 16 ? 4 : 2; c > 1; c /= 2)
         if (NS / c >= 192) { s.s = c; break; }
+    if (act) {   // as ck_frag_shape: the table of 16 s entries per group
+        if (s.mt == 2 && s.s == 4) s.s = 2;
+        while (s.s > 1 && (size_t)(K / G) * 16 * s.s > (size_t)ACT_MAX_ENTRIES) s.s /= 2;
+        if ((size_t)(K / G) * 16 * s.s > (size_t)ACT_MAX_ENTRIES) return s;
+    }
     frag_common(s, KB);
+    if (act) {
+        s.lds += (size_t)(K / G) * 16 * s.s * 4 + (size_t)K * 4;
+        if (s.lds > 160 * 1024) s.ok = false;
+    }
     return s;
 }
 
@@ -1120,7 +1165,7 @@ static hipError_t launch_prep_frag_ms(const PrepFragParams& p, const PrepFragSha
     // the checkpoint ones ck_frag_fits excludes
     auto fits = [](int bpw) { return SRC == SRC_PREP ? !(S == 4 && bpw == 32) : ck_frag_fits(MT, S, bpw); };
     if (!fits(s.bpw)) return hipErrorInvalidValue;
-    if constexpr (SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT) {   // K <= 4096: 4 blocks per wave
+    if constexpr (SRC == SRC_GPTQ_ACT || SRC == SRC_SYM_ACT || SRC == SRC_PREP_ACT) {   // K <= 4096: 4 blocks per wave
         if (s.bpw != 4) return hipErrorInvalidValue;
         launch_frag_inst<MT, S, 4, SRC>(p, s, st);
         return hipGetLastError();
@@ -1145,7 +1190,7 @@ static hipError_t launch_prep_frag_m(const PrepFragParams& p, const PrepFragShap
         case 1: return launch_prep_frag_ms<MT, 1, SRC>(p, s, st);
         case 2: return launch_prep_frag_ms<MT, 2, SRC>(p, s, st);
         // act-order at 2 row tiles: 2 strips (ck_frag_shape), 4 would spill
-        case 4: if constexpr (MT == 1 || (MT == 2 && SRC != SRC_GPTQ_ACT && SRC != SRC_SYM_ACT))
+        case 4: if constexpr (MT == 1 || (MT == 2 && SRC != SRC_GPTQ_ACT && SRC != SRC_SYM_ACT && SRC != SRC_PREP_ACT))
                     return launch_prep_frag_ms<MT, 4, SRC>(p, s, st);
                 [[fallthrough]];
         default: return hipErrorInvalidValue;
@@ -1166,7 +1211,7 @@ static hipError_t launch_frag_src(const PrepFragParams& p, const PrepFragShape& 
 }
 
 hipError_t launch_prep_frag(const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {
-    return launch_frag_src<SRC_PREP>(p, s, st);
+    return p.g_idx ? launch_frag_src<SRC_PREP_ACT>(p, s, st) : launch_frag_src<SRC_PREP>(p, s, st);
 }
 
 hipError_t launch_ck_frag(int fmt, const PrepFragParams& p, const PrepFragShape& s, hipStream_t st) {

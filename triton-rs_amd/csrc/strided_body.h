@@ -79,7 +79,12 @@ __device__ __forceinline__ void strided_gemm_body(const StridedParams& p) {
                         word = strip[p.stride_qwn + kb * 256 + (col + 16 * ((kk >> 5) & 3)) * 4 + ((kk >> 3) & 3)];
                         const int R = p.group_size < 128 ? 128 / p.group_size : 1;
                         const int r = p.group_size < 128 ? (kk & 127) / p.group_size : 0;
-                        const uint32_t e = strip[(kb * R + r) * 16 + col];
+                        // act-order (rows in the checkpoint's order): group g's entry is table
+                        // row g (G / 128) for G >= 128, row g for G = 32, 64
+                        const int ga = p.g_idx ? min(max(p.g_idx[kk], 0), (p.k - 1) / p.group_size) : 0;
+                        const int trow = p.g_idx ? ga * (p.group_size >= 128 ? p.group_size / 128 : 1)
+                                                 : kb * R + r;
+                        const uint32_t e = strip[trow * 16 + col];
                         const E s = (E)(float)__builtin_bit_cast(half_t, (uint16_t)e);
                         v = dequant1(nib(word, prep_slot(kk & 7)), (int)(e >> 16), s);
                         bv[i] = v;
