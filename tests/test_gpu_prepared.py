@@ -214,6 +214,22 @@ def test_act_order_then_prepared_small_batch(torch_cuda, orc, M):
     assert_parity(y, ref.astype(np.float64), what=f"act-order prepared M={M}")
 
 
+@pytest.mark.parametrize("M,K,N", [(5, 1152, 192), (16, 2048, 6160), (11, 4096, 512)])
+def test_act_order_then_prepared_uneven_shapes(torch_cuda, orc, M, K, N):
+    """The group-order repack, the prepared layout and the per-call gather at shapes the
+    config-2 cases miss: K = 1152 leaves the small-batch kernel's last wave one block of four,
+    N = 6160 an odd strip count; against the oracle's act-order GEMM on the checkpoint."""
+    P = pkg()
+    p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=0x5EED0330 + M + K, act_order=True)
+    qout, perm = P.prepare_act_order(to_dev(p.qweight), to_dev(p.g_idx), group_size=128)
+    w = P.prepare_layout(qout, to_dev(p.scales), to_dev(p.qzeros), fmt="gptq", group_size=128,
+                         zero_offset=1)
+    y = P.gemm_prepared(to_dev(p.x), w, perm=perm).cpu().numpy()
+    ref = orc.w4a16_gemm(GPTQ, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, g_idx=p.g_idx,
+                         want_f32=True)[1]
+    assert_parity(y, ref.astype(np.float64), what=f"act-order prepared M={M} K={K} N={N}")
+
+
 def test_gemm_prepared_small_batch_exact_arithmetic(torch_cuda, orc):
     """Exactly representable products and sums through the small-batch kernel (every row-tile
     count, with and without act-order): the oracle's bits."""
