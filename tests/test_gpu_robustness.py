@@ -396,3 +396,63 @@ def test_silu_mul_any_shape(torch_cuda, orc, rows, inter, total_cut, offset):
     ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
     assert np.all(np.abs(got[:total] - ref[:total]) <= ulp[:total] + 1e-7)
     assert np.all(got[total:] == -7.0)               # nothing written past `total`
+
+
+def test_captured_graph_of_act_order_prefill_route(torch_cuda, orc):
+    """The act-order route beyond 64 rows under graph capture: two layers with different g_idx
+    on one stream (the group order kept on the stream's buffers changes on every call) and one
+    whose groups are unequal (the generic kernel runs). Three replays, with eager calls on the
+    stream in between, each give the eager outputs bit for bit; then one layer's g_idx is
+    rewritten in place and the next replay follows the new order (its output equals an eager
+    call with it, and the oracle)."""
+    torch = torch_cuda
+    P = pkg()
+    s = torch.cuda.Stream()
+    K, N, M, G = 1024, 256, 128, 128
+    pa = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3130, act_order=True)
+    pb = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3131, act_order=True)
+    pc = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3132)
+    assert P.plan("gptq", M, N, K, G, has_g_idx=True) == "prefill"
+    gc = np.random.default_rng(3132).integers(0, K // G, K).astype(np.int32)
+    layers = []
+    for p, gi in ((pa, pa.g_idx), (pb, pb.g_idx), (pc, gc)):
+        args = [to_dev(v) for v in (p.x, p.qweight, p.scales, p.qzeros)]
+        layers.append((args, to_dev(gi), torch.empty((M, N), dtype=torch.float16, device="cuda:0")))
+
+    def run(i):
+        (x, qw, sc, qz), gi, out = layers[i]
+        P.gemm(x, qw, sc, qz, fmt="gptq", group_size=G, g_idx=gi, out=out)
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):                        # eager: sizes the stream's buffers
+        for i in range(3):
+            run(i)
+    s.synchronize()
+    eager = [o.cpu().numpy().copy() for _, _, o in layers]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(3):
+            run(i)
+    for rep in range(3):
+        for _, _, o in layers:
+            o.zero_()
+        torch.cuda.synchronize()
+        with torch.cuda.stream(s):
+            run(1)                                    # eager act-order work between replays
+            g.replay()
+        s.synchronize()
+        for i, (_, _, o) in enumerate(layers):
+            assert np.array_equal(o.cpu().numpy().view(np.uint16), eager[i].view(np.uint16)), (rep, i)
+    new = (np.arange(K) // G)[np.random.default_rng(3133).permutation(K)].astype(np.int32)
+    with torch.cuda.stream(s):
+        layers[0][1].copy_(torch.from_numpy(new).to("cuda:0"))
+        g.replay()
+    s.synchronize()
+    replayed = layers[0][2].cpu().numpy().copy()
+    with torch.cuda.stream(s):
+        run(0)
+    s.synchronize()
+    assert np.array_equal(replayed.view(np.uint16), layers[0][2].cpu().numpy().view(np.uint16))
+    ref = orc.w4a16_gemm(GPTQ, pa.x, pa.qweight, pa.scales, pa.qzeros, K, N, G, g_idx=new,
+                         want_f32=True)[1]
+    assert_parity(replayed, ref, what="replay after g_idx rewritten")
