@@ -270,6 +270,11 @@ PMC_WORKLOADS = {
     "prep_c2_m64": ("gptq", 64, 4096, 6144, 128, True),
     # act-order beyond 64 rows through w4a16_gemm (group order computed per call)
     "c2_m2048": ("gptq", 2048, 4096, 6144, 128, True),
+    # act-order on the prepared layout of the checkpoint as stored, g_idx per row
+    # (w4a16_gemm_prepared_gidx)
+    "prepstored_c2_m16": ("gptq", 16, 4096, 6144, 128, True),
+    "prepstored_c2_m32": ("gptq", 32, 4096, 6144, 128, True),
+    "prepstored_c2_m64": ("gptq", 64, 4096, 6144, 128, True),
 }
 
 
@@ -321,7 +326,16 @@ def pmc_child(args) -> int:
         g_idx = c2_g_idx(torch, dev, K, G) if act_order else None
         x = torch.randn((M, K), device=dev).half()
         out = torch.empty((M, N), dtype=torch.float16, device=dev)
-        if args.pmc_workload.startswith("prep_"):
+        if args.pmc_workload.startswith("prepstored_"):
+            prep = [pkg.prepare_layout(qw, sc, qz, fmt=fmt, group_size=G, zero_offset=1)
+                    for qw, sc, qz in sets]
+            del sets
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+            for i in range(PMC_WARM + PMC_MEASURED):
+                pkg.gemm_prepared(x, prep[i % len(prep)], g_idx=g_idx, out=out)
+            sets = prep
+        elif args.pmc_workload.startswith("prep_"):
             perm = None
             if act_order:   # group order once, then the layout of the repacked rows
                 prep = []
