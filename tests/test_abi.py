@@ -441,3 +441,32 @@ def test_gemm_prepared_argument_errors(M, N, K, G, code, needle):
                                      ctypes.c_void_p(2 << 20), M, N, K, G)
     assert rc == code
     assert needle in P.lib().w4a16_last_error().decode()
+
+
+@pytest.mark.parametrize("M,N,K,G,gi,code,needle", [
+    (0, 4096, 4096, 128, 3 << 20, 1, "M (0)"),
+    (1, 4100, 4096, 128, 3 << 20, 2, "N % 16"),
+    (1, 4096, 3072, 48, 3 << 20, 2, "group_size"),
+    (16, 4096, 4096, 128, None, 1, "null pointer"),
+    (16, 4096, 4096, 128, (3 << 20) + 4, 1, "g_idx must be 16-byte aligned"),
+])
+def test_gemm_prepared_gidx_argument_errors(M, N, K, G, gi, code, needle):
+    """w4a16_gemm_prepared_gidx checks its shape, pointers and alignment before any HIP call."""
+    P = pkg()
+    rc = P.lib().w4a16_gemm_prepared_gidx(None, ctypes.c_void_p(1 << 20), ctypes.c_void_p(1 << 30),
+                                          None if gi is None else ctypes.c_void_p(gi),
+                                          ctypes.c_void_p(2 << 20), M, N, K, G)
+    assert rc == code
+    assert needle in P.lib().w4a16_last_error().decode()
+
+
+def test_gemm_prepared_python_refuses_perm_with_g_idx():
+    """gemm_prepared takes either the group-order permutation or g_idx, never both (checked
+    before any device access)."""
+    import torch
+    P = pkg()
+    w = P.PreparedWeights(torch.empty(0, dtype=torch.uint8), 4096, 4096, 128)
+    x = torch.empty((4, 4096), dtype=torch.float16)
+    i = torch.empty(4096, dtype=torch.int32)
+    with pytest.raises(P.InvalidArgument, match="not both"):
+        P.gemm_prepared(x, w, perm=i, g_idx=i)

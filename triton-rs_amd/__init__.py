@@ -356,9 +356,9 @@ def gemm_prepared(x: torch.Tensor, w: PreparedWeights, perm: torch.Tensor | None
     by prepare_act_order before prepare_layout; x's columns are gathered by it first. g_idx:
     an act-order checkpoint prepared as stored, g_idx[k] the group of row k
     (w4a16_gemm_prepared_gidx))."""
-    _require(x, "x", _HALF)
     if perm is not None and g_idx is not None:
         raise InvalidArgument("give perm (group-order repack) or g_idx (rows as stored), not both")
+    _require(x, "x", _HALF)
     if perm is not None:
         _require(perm, "perm", _INT32, x.device)
     if g_idx is not None:
