@@ -375,11 +375,12 @@ def test_prefill_256_row_tiles(torch_cuda, orc, fmt, M, K, N, G):
 
 @pytest.mark.parametrize("fmt", [AWQ, GPTQ, SYM])
 @pytest.mark.parametrize("M,K,N", [(512, 2048, 4096), (700, 1024, 2048), (2048, 1024, 4096),
-                                   (1024, 14336, 4096)])
+                                   (1024, 14336, 4096), (128, 14336, 4096), (200, 8192, 2048)])
 def test_prefill_split_k(torch_cuda, orc, fmt, M, K, N):
     """Few 256-row tiles: K split over workgroups (256 x 128 tiles in 4 and 2 splits, 256 x 128
-    unsplit, 256 x 256 in 4 splits), the last split of a tile summing the fp32 partials in
-    split order (a row tail included); repeated calls are bit-identical."""
+    unsplit, 256 x 256 in 4 splits, 8 splits where each keeps 16 stages of K), the last split
+    of a tile summing the fp32 partials in split order (a row tail included); repeated calls
+    are bit-identical."""
     P = pkg()
     p = Problem(fmt, M=M, K=K, N=N, G=128, seed=2500 + M + fmt)
     assert P.plan(FMT_NAME[fmt], M, N, K, 128) == "prefill"
@@ -387,7 +388,7 @@ def test_prefill_split_k(torch_cuda, orc, fmt, M, K, N):
     y2 = _run_gemm(torch_cuda, p)
     assert np.array_equal(y.view(np.uint16), y2.view(np.uint16))
     rows = np.random.default_rng(6).choice(M, 16, replace=False).astype(np.int32)
-    rows[:3] = [0, 255, M - 1]
+    rows[:3] = [0, min(255, M - 1), M - 1]
     ref = orc.w4a16_gemm_rows(fmt, p.x, p.qweight, p.scales, p.qzeros, K, N, 128, rows)
     assert_parity(y[rows], ref.astype(np.float64), what=f"prefill split-K fmt={fmt} M={M} N={N}")
     assert np.all(np.isfinite(y))

@@ -817,7 +817,10 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int
         // that 224 does not divide: N = 6144, K = 4096, M = 1024 / 2048 / 4096: 78.9 / 113.7 /
         // 229.6 us with 256 x 256 (2 splits / 1 / 1) against 68.0 / 102.4 / 203.1 us (the 192
         // workgroups of 256 x 256 at M = 2048 leave 64 CUs idle). A split keeps at least 8
-        // stages of K. Ties go to larger tiles and fewer splits.
+        // stages of K, and 16 for 8 splits (the last workgroup of a tile sums 8 partials
+        // alone): AWQ 14336 -> 4096 at M = 128 / 256 70.1 / 79.9 -> 52.2 / 70.5 us with 8
+        // splits; GPTQ 4096 -> 6144 at M = 96 with 8 splits of 8 stages 38.2 us against 27.6
+        // with 4. Ties go to larger tiles and fewer splits.
         double best = -1.0;
         for (int bm : {256, 128}) {
             for (int bn : {256, 224, 192, 128}) {
@@ -825,8 +828,9 @@ PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int
                 if ((bn == 128 || bn == 192) && bm != 256) continue;   // 128/192-wide tiles only with 256 rows
                 const double e = bm == 128 ? 1.35 : bn == 128 ? 1.15 : bn == 192 ? 1.2 : 1.0;
                 const long long tiles = (long long)(N / bn) * ((M + bm - 1) / bm);
-                for (int ks = 1; ks <= 4; ks *= 2) {
-                    if (ks > 1 && (bm != 256 || ks > max_ksplit || (K / BK) % ks || K / BK / ks < 8))
+                for (int ks = 1; ks <= 8; ks *= 2) {
+                    if (ks > 1 && (bm != 256 || ks > max_ksplit || (K / BK) % ks ||
+                                   K / BK / ks < (ks == 8 ? 16 : 8)))
                         break;
                     const long long rounds = (tiles * ks + num_cus - 1) / num_cus;
                     const double cost = (double)rounds * bm * bn * e * ((double)K / ks) +

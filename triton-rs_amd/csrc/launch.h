@@ -118,7 +118,7 @@ struct PrefillShape {
 size_t prefill_dma_lds(int bm, int bn);
 
 // max_ksplit caps the K split (1: never split, so no scratch is needed).
-PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int max_ksplit = 4);
+PrefillShape prefill_shape(int fmt, int M, int N, int K, int G, int num_cus, int max_ksplit = 8);
 // bf16: x, scales and out are bfloat16 (pipelined kernel, dense checkpoint layouts only)
 hipError_t launch_prefill(int fmt, const PrefillParams& p, const PrefillShape& s, hipStream_t st,
                           bool bf16 = false);
