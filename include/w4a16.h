@@ -118,8 +118,9 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
  * fp32 partials) lives in a fixed device array of w4a16_gemm_noalloc_scratch_bytes() bytes
  * (8 MiB: at most 1024 split-K tiles and 6.9 MiB of partials), one per device, held until the
  * process ends; the call itself allocates nothing. A call whose planned kernel would need
- * more than that runs a kernel that needs no scratch instead (the prefill kernel without a K
- * split, or the generic kernel), and act-order beyond 64 rows runs the generic kernel (the
+ * more than that runs the prefill kernel with the largest K split whose partials fit (down
+ * to none, which needs no scratch), or the generic kernel, and act-order beyond 64 rows runs
+ * the generic kernel (the
  * repacked rows would not fit), so such results may differ from w4a16_gemm's in the last bits.
  * All calls on one device share its array: calls that overlap in time on one device (other
  * streams or threads) race and must be serialised by the caller. The device's array is set

@@ -351,7 +351,8 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     };
     // A fixed scratch area (w4a16_gemm_noalloc) may be too small for the split-K partials of
     // the planned GEMV or small-batch kernel (e.g. AWQ M = 8 on a 70B-class MLP: 7 MiB): such
-    // a call takes the prefill kernel without a K split instead, which needs no scratch.
+    // a call takes the prefill kernel instead, with the largest K split whose partials fit
+    // (run_prefill), down to none, which needs no scratch.
     auto scratch_fits = [&](size_t tiles, size_t partial_bytes) {
         return tiles <= src.max_tiles && partial_bytes <= src.max_partial_bytes;
     };
@@ -395,10 +396,12 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
 
     // the prefill kernel on (xp, qwp) with the call's scales and zeros; gate as PrefillParams
     auto run_prefill = [&](const void* xp, const void* qwp, const uint32_t* gate) -> int {
+        // a fixed scratch area too small for the planned split's partials: the best plan with
+        // at most half the splits, down to none (no scratch at all)
         PrefillShape s = prefill_shape(fmt, M, N, K, G, cus);
-        if (s.ksplit > 1 && ((size_t)s.ksplit * M * N * sizeof(float) > src.max_partial_bytes ||
-                             (size_t)s.col_tiles * s.row_tiles > src.max_tiles))
-            s = prefill_shape(fmt, M, N, K, G, cus, 1);   // no K split: no scratch at all
+        while (s.ksplit > 1 && ((size_t)s.ksplit * M * N * sizeof(float) > src.max_partial_bytes ||
+                                (size_t)s.col_tiles * s.row_tiles > src.max_tiles))
+            s = prefill_shape(fmt, M, N, K, G, cus, s.ksplit / 2);
         PrefillParams p{};
         p.x = static_cast<const half_t*>(xp);
         p.qweight = static_cast<const uint32_t*>(qwp);
