@@ -125,6 +125,7 @@ def test_act_order_then_prepared(torch_cuda, orc, M, K, N):
     (AWQ, 9, 1024, 512, 128), (GPTQ, 16, 2048, 768, 128), (AWQ, 64, 4096, 1024, 64),
     (SYM, 100, 1024, 256, 256), (GPTQ, 300, 2048, 4096, 128),    # prefill tiles, K split
     (AWQ, 130, 1024, 224, 128),                                  # 224-column tiles
+    (AWQ, 128, 14336, 4096, 128),                                # K split in 8
     (GPTQ, 40, 512, 48, 32), (AWQ, 12, 16384 + 128, 32, 128),    # generic kernel (G = 32, K)
 ])
 def test_gemm_prepared_large_m_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
