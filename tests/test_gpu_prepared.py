@@ -258,6 +258,7 @@ def test_gemm_prepared_small_batch_exact_arithmetic(torch_cuda, orc):
     (GPTQ, 16, 4096, 6144, 128), (GPTQ, 64, 4096, 6144, 128),   # config 2, as stored + g_idx
     (GPTQ, 1, 2048, 512, 128), (GPTQ, 7, 1024, 6160, 128), (SYM, 40, 2048, 1024, 128),
     (GPTQ, 24, 1024, 512, 32), (SYM, 9, 512, 2048, 64), (GPTQ, 33, 4096, 256, 256),
+    (GPTQ, 16, 4096, 6144, 32), (GPTQ, 48, 4096, 6144, 32),    # the largest table: 4096 entries
     (GPTQ, 100, 1024, 256, 128), (GPTQ, 5, 8192, 128, 128),     # generic kernel: M > 64, K > 4096
 ])
 def test_gemm_prepared_gidx_matches_oracle(torch_cuda, orc, fmt, M, K, N, G):
