@@ -102,7 +102,8 @@ W4A16_API int w4a16_init(int32_t device);
  * captured call stays valid for the life of the process. Growing the workspace is not
  * possible under stream capture: make one call of the largest size before capturing, or
  * the call fails with W4A16_ERR_UNSUPPORTED. Concurrent calls on different streams are
- * safe. With g_idx beyond 64 rows (GPTQ formats, K <= 32768, K / group_size <= 1024) each
+ * safe. With g_idx from 65 to 128 rows (GPTQ formats, K <= 4096) the small-batch kernel runs
+ * in two row chunks; beyond that (K <= 32768, K / group_size <= 1024) each
  * call also computes the group order of the rows on the device, repacks the rows and gathers
  * x into per-(device, stream) buffers (grown like the workspace) and runs the prefill
  * kernel on them; when g_idx's groups do not each hold exactly group_size rows (or an entry
@@ -119,8 +120,8 @@ W4A16_API int w4a16_gemm(void* stream, int fmt, const void* x, const void* qweig
  * (8 MiB: at most 1024 split-K tiles and 6.9 MiB of partials), one per device, held until the
  * process ends; the call itself allocates nothing. A call whose planned kernel would need
  * more than that runs the prefill kernel with the largest K split whose partials fit (down
- * to none, which needs no scratch), or the generic kernel, and act-order beyond 64 rows runs
- * the generic kernel (the
+ * to none, which needs no scratch), or the generic kernel, and act-order beyond the
+ * small-batch kernel's rows (and its row chunks) runs the generic kernel (the
  * repacked rows would not fit), so such results may differ from w4a16_gemm's in the last bits.
  * All calls on one device share its array: calls that overlap in time on one device (other
  * streams or threads) race and must be serialised by the caller. The device's array is set

@@ -474,20 +474,39 @@ def test_act_order_identity_gidx_equals_plain(torch_cuda, orc, M, K, N, G):
         assert_parity(ident, ref, what="identity g_idx")
 
 
-@pytest.mark.parametrize("fmt,M,K,N,G", [(GPTQ, 100, 512, 256, 128), (SYM, 65, 1024, 384, 64),
+@pytest.mark.parametrize("fmt,M,K,N,G", [(GPTQ, 160, 512, 256, 128), (SYM, 129, 1024, 384, 64),
                                          (GPTQ, 300, 2048, 1024, 256), (GPTQ, 130, 4096, 224, 128),
                                          (GPTQ, 200, 6144, 512, 128), (GPTQ, 72, 8192, 1024, 64),
-                                         (GPTQ, 96, 16384, 256, 128), (GPTQ, 80, 1024, 224, 128)])
+                                         (GPTQ, 96, 16384, 256, 128), (GPTQ, 150, 1024, 224, 128)])
 def test_act_order_large_m_prefill(torch_cuda, orc, fmt, M, K, N, G):
-    """Act-order beyond 64 rows through w4a16_gemm: the group order is computed on the device,
-    then the prefill kernel runs on the repacked rows and the gathered x (K from 512 to
-    16384, N from 224 to 1024, groups of 64 to 256 rows)."""
+    """Act-order beyond 128 rows (or K beyond 4096) through w4a16_gemm: the group order is
+    computed on the device, then the prefill kernel runs on the repacked rows and the gathered
+    x (K from 512 to 16384, N from 224 to 1024, groups of 64 to 256 rows)."""
     p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1330 + M, act_order=True)
     assert pkg().plan(FMT_NAME[fmt], p.M, p.N, p.K, p.G, has_g_idx=True) == "prefill"
     y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
     y2 = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
     assert np.array_equal(y.view(np.uint16), y2.view(np.uint16)), "repeated calls differ"
     assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"act-order prefill M={M}")
+
+
+@pytest.mark.parametrize("fmt,M,K,N,G", [(GPTQ, 96, 4096, 6144, 128), (GPTQ, 128, 4096, 6144, 128),
+                                         (GPTQ, 65, 1024, 512, 128), (SYM, 100, 2048, 1024, 64),
+                                         (GPTQ, 77, 4096, 6144, 32)])
+def test_act_order_row_chunks(torch_cuda, orc, fmt, M, K, N, G):
+    """Act-order from 65 to 128 rows (K <= 4096): the direct-x small-batch kernel in two row
+    chunks, 64 and M - 64, each through its (scale, zero) table; against the oracle, and the
+    first 64 rows bit for bit a 64-row call's (each row's sum is its own)."""
+    P = pkg()
+    p = Problem(fmt, M=M, K=K, N=N, G=G, seed=1390 + M + G, act_order=True)
+    assert P.plan(FMT_NAME[fmt], M, N, K, G, has_g_idx=True) == "skinny"
+    y = _run_gemm(torch_cuda, p, g_idx=p.g_idx)
+    assert_parity(y, _oracle(orc, p, g_idx=p.g_idx), what=f"act-order row chunks M={M}")
+    q = Problem(fmt, M=64, K=K, N=N, G=G, seed=1390 + M + G, act_order=True)
+    q.x = p.x[:64].copy()
+    q.qweight, q.scales, q.qzeros, q.g_idx = p.qweight, p.scales, p.qzeros, p.g_idx
+    y64 = _run_gemm(torch_cuda, q, g_idx=q.g_idx)
+    assert np.array_equal(y[:64].view(np.uint16), y64.view(np.uint16))
 
 
 def test_act_order_config2_prefill_size(torch_cuda, orc):
@@ -516,7 +535,8 @@ def test_act_order_large_m_unequal_groups_runs_generic(torch_cuda, orc):
     """A g_idx whose groups do not each hold G rows cannot be put in group order for the
     prefill kernel: the device-side check leaves the generic kernel to run, which reads g_idx
     per row (same results as the oracle)."""
-    p = Problem(GPTQ, M=96, K=1024, N=256, G=128, seed=1336)
+    p = Problem(GPTQ, M=160, K=1024, N=256, G=128, seed=1336)
+    assert pkg().plan("gptq", p.M, p.N, p.K, p.G, has_g_idx=True) == "prefill"
     g_idx = np.random.default_rng(1336).integers(0, p.K // p.G, p.K).astype(np.int32)
     g_idx[:5] = 0
     y = _run_gemm(torch_cuda, p, g_idx=g_idx)
@@ -529,8 +549,9 @@ def test_act_order_large_m_order_kept_between_calls(torch_cuda, orc):
     order; two rows of different groups swapped; one row moved to another group, so the groups
     are unequal) and then G with the same g_idx (8 groups of 128 rows: valid for G = 128,
     unequal for G = 64), each against the oracle; a repeated g_idx gives its first call's bits."""
-    K, N, M = 1024, 256, 96
+    K, N, M = 1024, 256, 160
     p = Problem(GPTQ, M=M, K=K, N=N, G=128, seed=1337, act_order=True)
+    assert pkg().plan("gptq", M, N, K, 128, has_g_idx=True) == "prefill"
     p64 = Problem(GPTQ, M=M, K=K, N=N, G=64, seed=1338)
     p64.x = p.x
     rng = np.random.default_rng(1337)
@@ -560,12 +581,13 @@ def test_act_order_large_m_order_kept_between_calls(torch_cuda, orc):
     assert np.array_equal(first.view(np.uint16), y.view(np.uint16)), "g_idx a after G=64"
 
 
-@pytest.mark.parametrize("M", [16, 40, 80])
+@pytest.mark.parametrize("M", [16, 40, 80, 160])
 def test_act_order_out_of_range_gidx_is_clamped(torch_cuda, orc, M):
     """The device cannot report a bad g_idx without a host round trip; entries outside
     [0, K/G) are clamped into the scale table (the split-K kernel at 16 rows, the direct-x
-    kernel's table offsets at 40; the oracle, which rejects them, is given the clamped
-    index). Beyond 64 rows the group-order check sees them and the generic kernel runs."""
+    kernel's table offsets at 40 and, in two row chunks, at 80; the oracle, which rejects
+    them, is given the clamped index). Beyond 128 rows the group-order check sees them and the
+    generic kernel runs."""
     p = Problem(GPTQ, M=M, K=1024, N=256, G=128, seed=1340, act_order=True)
     bad = p.g_idx.copy()
     bad[3], bad[700] = 99, -5

@@ -408,7 +408,7 @@ def test_captured_graph_of_act_order_prefill_route(torch_cuda, orc):
     torch = torch_cuda
     P = pkg()
     s = torch.cuda.Stream()
-    K, N, M, G = 1024, 256, 128, 128
+    K, N, M, G = 1024, 256, 160, 128
     pa = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3130, act_order=True)
     pb = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3131, act_order=True)
     pc = Problem(GPTQ, M=M, K=K, N=N, G=G, seed=3132)

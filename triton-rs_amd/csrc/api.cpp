@@ -193,10 +193,21 @@ static bool act_order_prefill_ok(int fmt, int M, int N, int K, int G, int cus, b
     return ps.ok && (!bf16 || ps.dma);   // bf16 runs the pipelined prefill only
 }
 
+// Act-order from 65 to 128 rows: the direct-x small-batch kernel on the checkpoint as stored
+// (per-workgroup (scale, zero) table, no scratch) over two row chunks, 64 and M - 64. Each
+// chunk reads all the weights, which at these sizes costs less than the group-order route's
+// per-call staging (order, repack and gather, ~15 us at K = 4096, N = 6144, where M = 96 /
+// 128 took 42.3 / 44.8 us through the route).
+static bool act_order_chunks_ok(int fmt, int M, int N, int K, int G) {
+    return M > 64 && M <= 128 && ck_frag_shape(fmt, 64, N, K, G, true).ok &&
+           ck_frag_shape(fmt, M - 64, N, K, G, true).ok;
+}
+
 static int plan(int fmt, int M, int N, int K, int G, bool has_gidx, int cus = DEFAULT_CUS) {
     if (has_gidx) {
         const SkinnyShape sk = skinny_shape(fmt, M, N, K, G, cus, true);
         if (sk.ok && (size_t)sk.col_tiles <= SPLITK_MAX_TILES) return W4A16_KERNEL_SKINNY;
+        if (act_order_chunks_ok(fmt, M, N, K, G)) return W4A16_KERNEL_SKINNY;
         return act_order_prefill_ok(fmt, M, N, K, G, cus) ? W4A16_KERNEL_PREFILL : W4A16_KERNEL_STRIDED;
     }
     const GemvShape gv = gemv_shape(fmt, M, N, K, G, false);
@@ -321,6 +332,24 @@ int gemm_impl(void* stream, int fmt, const void* x, const void* qweight, const v
     // read 128-byte pieces of K / 8 packed rows N * 4 bytes apart, where the prepared layout
     // streams whole strips (6.05 us at config 2's M = 16); 16- and 64-column workgroups were
     // slower still.
+    if (kernel == W4A16_KERNEL_SKINNY && g_idx && !bf16 && M > 64) {   // act_order_chunks_ok
+        for (int m0 = 0; m0 < M; m0 += 64) {
+            const int rows = M - m0 < 64 ? M - m0 : 64;
+            const PrepFragShape fs = ck_frag_shape(fmt, rows, N, K, G, true);
+            PrepFragParams p{};
+            p.g_idx = g_idx;
+            p.x = static_cast<const half_t*>(x) + (size_t)m0 * K;
+            p.qweight = static_cast<const uint32_t*>(qweight);
+            p.scales = static_cast<const half_t*>(scales);
+            p.qzeros = fmt == W4A16_FMT_GPTQ_SYM ? nullptr : static_cast<const uint32_t*>(qzeros);
+            p.zero_offset = zero_offset;
+            p.out = static_cast<half_t*>(out) + (size_t)m0 * N;
+            p.M = rows; p.N = N; p.K = K; p.G = G;
+            hipError_t e = launch_ck_frag(fmt, p, fs, st);
+            if (e != hipSuccess) return hip_fail(e, "small-batch launch");
+        }
+        return W4A16_OK;
+    }
     if (kernel == W4A16_KERNEL_SKINNY && !bf16 && fmt != W4A16_FMT_AWQ && (g_idx ? M >= 2 : M > 8)) {
         const PrepFragShape fs = ck_frag_shape(fmt, M, N, K, G, g_idx != nullptr);
         if (fs.ok && (g_idx ? M > 16 || G < 128 : M > 16 || fs.s == 4)) {
