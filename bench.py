@@ -526,6 +526,9 @@ def extras(torch, pkg, dev, stream, args):
     # device per call, rows repacked, x gathered, then the prefill kernel)
     gemm_case("c2_gptq_actorder_m2048_k4096_n6144", "gptq", 2048, 4096, 6144, 128, 2, 200, g_idx=g_idx)
     gemm_case("c2_gptq_m2048_k4096_n6144_no_gidx", "gptq", 2048, 4096, 6144, 128, 2, 200)
+    # between the two: 128 rows (act-order: the small-batch kernel in two row chunks)
+    gemm_case("c2_gptq_actorder_m128_k4096_n6144", "gptq", 128, 4096, 6144, 128, 8, 300, g_idx=g_idx)
+    gemm_case("c2_gptq_m128_k4096_n6144_no_gidx", "gptq", 128, 4096, 6144, 128, 8, 300)
 
     # config 2's act-order layer through the one-time group-order repack: gather + plain kernel
     def prepared_case(tag, M, n_sets, calls):
