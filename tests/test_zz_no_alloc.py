@@ -43,6 +43,7 @@ PAIRS = [
     ((GPTQ, 4, 4096, 6144, False), (SYM, 1, 2048, 1024, False)),     # GPTQ GEMV
     ((AWQ, 8, 4096, 14336, False), (AWQ, 6, 2048, 1024, False)),     # matrix-core GEMV, counter
     ((GPTQ, 64, 4096, 6144, True), (GPTQ, 16, 1024, 768, True)),     # small batch, act-order
+    ((GPTQ, 96, 4096, 6144, True), (GPTQ, 70, 1024, 768, True)),     # act-order in row chunks
     ((AWQ, 512, 2048, 4096, False), (GPTQ, 300, 640, 384, False)),   # prefill (K split > scratch)
 ]
 
@@ -57,7 +58,7 @@ def test_noalloc_matches_w4a16_gemm(torch_cuda, orc, pair):
         assert rc_na == P.OK, P.lib().w4a16_last_error()
         rc, y = _call(P, torch, "w4a16_gemm", p, p.g_idx)
         assert rc == P.OK
-        same_plan = not (M > 64 and P.plan(FMT_NAME[fmt], M, N, K, 128) == "prefill")
+        same_plan = not (M > 64 and P.plan(FMT_NAME[fmt], M, N, K, 128, has_g_idx=act) == "prefill")
         if same_plan:
             # same kernels, same deterministic split-K order: the same bits
             assert np.array_equal(y_na.view(np.uint16), y.view(np.uint16)), (fmt, M, K, N)
