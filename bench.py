@@ -268,7 +268,9 @@ PMC_WORKLOADS = {
     "prep_c2_plain_m64": ("gptq", 64, 4096, 6144, 128, False),
     "prep_c2_m16": ("gptq", 16, 4096, 6144, 128, True),
     "prep_c2_m64": ("gptq", 64, 4096, 6144, 128, True),
-    # act-order beyond 64 rows through w4a16_gemm (group order computed per call)
+    # act-order beyond 64 rows through w4a16_gemm: 128 rows (small-batch kernel in two row
+    # chunks) and 2048 (group order computed per call, then the prefill kernel)
+    "c2_m128": ("gptq", 128, 4096, 6144, 128, True),
     "c2_m2048": ("gptq", 2048, 4096, 6144, 128, True),
     # act-order on the prepared layout of the checkpoint as stored, g_idx per row
     # (w4a16_gemm_prepared_gidx)
