@@ -78,7 +78,7 @@ def test_noalloc_matches_w4a16_gemm(torch_cuda, orc, pair):
 
 
 @pytest.mark.parametrize("K,N", [(16384, 16384), (8192, 28672), (28672, 8192)])
-def test_noalloc_beyond_its_scratch_runs_without_split_k(torch_cuda, orc, K, N):
+def test_noalloc_beyond_its_scratch_runs_a_smaller_split(torch_cuda, orc, K, N):
     """AWQ M=8 whose split-K partials exceed the 6.9 MiB the fixed array holds (K=16384 ->
     N=16384: 8 MiB; a 70B-class MLP, 8192 -> 28672 and 28672 -> 8192: 7 MiB): the call is
     re-planned onto the prefill kernel with the largest K split whose partials fit the array
